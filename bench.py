@@ -1,0 +1,274 @@
+"""Benchmark of the MI355X attention hot path (one JSON line on stdout).
+
+Headline workload: one Llama-3-8B-shaped bf16 decode step per
+layer — batch 64, contexts U[512, 4096], 32 q / 8 kv heads, head_dim 128, block 16, shuffled
+block tables — made of the fused RoPE + cache write of the 64 new tokens followed by paged
+attention v1.  ``value`` is the step's algorithmic HBM bytes / step time (inputs resident in
+HBM).  ``roofline`` is for the dominant call, paged attention v1 (partition + merge
+kernels), timed with HIP events on the stream it is launched on.  Side figures: config 3
+(v2 split-K, 8 x 32k) and config 4 (packed causal prefill, bf16 MFMA roofline).
+
+``cpu_baseline`` times the restated reference CPU path (gather -> q.K^T*scale -> softmax -> .V,
+oracle/oracle.c) on host cores over a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "paged decode achieved HBM GB/s (% of peak) + prefill MFMA util, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2516.6
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-side", action="store_true", help="skip the config 3 / config 4 side figures")
+    return ap.parse_args()
+
+
+def bf16_normal(shape, gen, device):
+    import torch
+
+    return torch.randn(shape, generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+
+
+def time_events(fn, steps: int, warmup: int):
+    """Average ms per call of fn() over `steps` calls, bracketed by HIP events on the
+    current stream (the stream every launch goes to)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / steps
+
+
+def decode_setup(w, device, gen):
+    import torch
+
+    from railgun_amd.ops import PagedAttentionKernels, PagedAttentionOp, rope_cos_sin_table
+
+    kernels = PagedAttentionKernels(0)
+    shape = (w.num_blocks, w.num_kv_heads, w.block_size, w.head_dim)
+    st = dict(
+        kernels=kernels,
+        op=PagedAttentionOp(w.scale, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size, kernels),
+        kc=bf16_normal(shape, gen, device), vc=bf16_normal(shape, gen, device),
+        q=bf16_normal((w.batch, w.num_heads, w.head_dim), gen, device),
+        k=bf16_normal((w.batch, w.num_kv_heads, w.head_dim), gen, device),
+        v=bf16_normal((w.batch, w.num_kv_heads, w.head_dim), gen, device),
+        bt=torch.from_numpy(w.block_table).to(device), ctx=torch.from_numpy(w.context_lens).to(device),
+        pos=torch.from_numpy(w.positions).to(device), slots=torch.from_numpy(w.slot_mapping).to(device),
+    )
+    st["out"] = torch.empty_like(st["q"])
+    if w.rope_theta:
+        st["cos_sin"] = rope_cos_sin_table(int(w.context_lens.max()), w.head_dim, w.rope_theta, device)
+    nbytes = kernels.v1_workspace_bytes(w.batch, w.num_heads, w.head_dim, w.block_size, w.max_blocks)
+    st["ws"] = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+    return st
+
+
+def v1_call(w, st):
+    st["kernels"].launch_v1(st["q"], st["kc"], st["vc"], st["bt"], st["ctx"], st["out"], w.scale, w.num_heads,
+                            w.num_kv_heads, w.head_dim, w.block_size, w.max_blocks, w.batch, workspace=st["ws"])
+
+
+def rope_cache_call(w, st):
+    st["op"].rope_reshape_and_cache(st["q"], st["k"], st["v"], st["kc"], st["vc"], st["cos_sin"], st["pos"],
+                                    st["slots"])
+
+
+def cpu_baseline(w, seconds_target: float = 10.0) -> dict:
+    """The restated reference CPU path on a bounded sample of config 2 (first n sequences)."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    import dataclasses
+
+    from railgun_amd import workloads as wl
+
+    cores = min(os.cpu_count() or 1, 16)
+    rng = np.random.default_rng(7)
+    n = 8
+    sub_ctx = w.context_lens[:n]
+    need = int(((sub_ctx.astype(np.int64) + w.block_size - 1) // w.block_size).sum())
+    bt = wl.assign_blocks(sub_ctx, w.block_size, need, w.max_blocks, rng)
+    shape = (need, w.num_kv_heads, w.block_size, w.head_dim)
+    kc = orc.bf16_round(rng.standard_normal(size=shape, dtype=np.float32))
+    vc = orc.bf16_round(rng.standard_normal(size=shape, dtype=np.float32))
+    q = orc.bf16_round(rng.standard_normal(size=(n, w.num_heads, w.head_dim), dtype=np.float32))
+    sub = dataclasses.replace(w, num_blocks=need, context_lens=sub_ctx, block_table=bt)
+    t0 = time.perf_counter()
+    orc.cpu_attention_gathered(q, kc, vc, bt, sub_ctx, w.scale, "bf16", nthreads=cores)
+    one = time.perf_counter() - t0
+    reps = max(1, min(20, int(seconds_target / max(one, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        orc.cpu_attention_gathered(q, kc, vc, bt, sub_ctx, w.scale, "bf16", nthreads=cores)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    return {"value": round(sub.decode_bytes() / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"first {n} of the 64 config-2 sequences ({int(sub_ctx.sum())} context tokens, 32/8 heads, "
+                      f"D 128, bf16 upcast to fp32), median of {reps} runs after a warm-up, "
+                      f"{sub.decode_bytes() / 1e6:.1f} MB algorithmic bytes per run"}
+
+
+def side_v2(device, gen, steps: int) -> dict:
+    import torch
+
+    from railgun_amd import workloads as wl
+
+    w = wl.config3()
+    st = decode_setup(w, device, gen)
+    P = w.partition_size
+    np_ = math.ceil(int(w.context_lens.max()) / P)
+    ws = torch.empty(st["kernels"].v2_workspace_bytes(w.batch, w.num_heads, np_, w.head_dim), dtype=torch.uint8,
+                     device=device)
+
+    def call():
+        st["kernels"].launch_v2(st["q"], st["kc"], st["vc"], st["bt"], st["ctx"], st["out"], w.scale, w.num_heads,
+                                w.num_kv_heads, w.head_dim, w.block_size, w.max_blocks, w.batch,
+                                int(w.context_lens.max()), P, ws)
+
+    ms = time_events(call, steps, 3)
+    gbs = w.decode_bytes() / (ms * 1e-3) / 1e9
+    del st, ws
+    torch.cuda.empty_cache()
+    return {"workload": w.name, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": w.decode_bytes()}
+
+
+def side_prefill(device, gen, steps: int) -> dict:
+    import torch
+
+    from railgun_amd import workloads as wl
+    from railgun_amd.ops import PagedAttentionKernels, PagedAttentionOp, rope_cos_sin_table
+
+    w = wl.config4()
+    kernels = PagedAttentionKernels(0)
+    op = PagedAttentionOp(w.scale, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size, kernels)
+    T = w.num_tokens
+    shape = (w.num_blocks, w.num_kv_heads, w.block_size, w.head_dim)
+    kc, vc = bf16_normal(shape, gen, device), bf16_normal(shape, gen, device)
+    q = bf16_normal((T, w.num_heads, w.head_dim), gen, device)
+    k = bf16_normal((T, w.num_kv_heads, w.head_dim), gen, device)
+    v = bf16_normal((T, w.num_kv_heads, w.head_dim), gen, device)
+    cs = rope_cos_sin_table(int(w.context_lens.max()), w.head_dim, w.rope_theta, device)
+    i32 = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    pos, slots, bt, ctx, cu = (i32(a) for a in (w.positions, w.slot_mapping, w.block_table, w.context_lens,
+                                                w.cu_seqlens))
+    op.rope_reshape_and_cache(q, k, v, kc, vc, cs, pos, slots)
+    out = torch.empty_like(q)
+    maxq = int(w.seq_lens.max())
+
+    def call():
+        kernels.launch_prefill_packed(q, kc, vc, bt, ctx, cu, out, w.scale, w.num_heads, w.num_kv_heads,
+                                      w.head_dim, w.block_size, w.max_blocks, w.num_seqs, T, maxq)
+
+    ms = time_events(call, steps, 2)
+    tflops = w.causal_flops() / (ms * 1e-3) / 1e12
+    return {"workload": w.name, "tokens": T, "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 2),
+            "frac_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops": w.causal_flops()}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(the decode path shards by sequence or kv-head with no exchange, see DESIGN.md)"}))
+        return 2
+    import torch
+
+    from railgun_amd import workloads as wl
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(1002)
+    w = wl.config2()
+    log(f"[bench] config2: B={w.batch} tokens={int(w.context_lens.sum())} pool={w.num_blocks} blocks")
+    st = decode_setup(w, device, gen)
+
+    def step():
+        rope_cache_call(w, st)
+        v1_call(w, st)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # Timed region: K whole steps; the v1 call of each step is bracketed by its own events.
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t_start.record()
+    for i in range(args.steps):
+        rope_cache_call(w, st)
+        ev[i][0].record()
+        v1_call(w, st)
+        ev[i][1].record()
+    t_end.record()
+    torch.cuda.synchronize()
+    ms_step = t_start.elapsed_time(t_end) / args.steps
+    ms_v1 = sum(a.elapsed_time(b) for a, b in ev) / args.steps
+    step_bytes = w.decode_bytes() + w.rope_cache_bytes()
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    achieved = w.decode_bytes() / (ms_v1 * 1e-3) / 1e9
+    log(f"[bench] step {ms_step * 1e3:.1f} us, v1 {ms_v1 * 1e3:.1f} us, {achieved:.0f} GB/s")
+    del st
+    torch.cuda.empty_cache()
+
+    result = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) q/k/v and pool, shuffled tables)",
+        "config": {"workload": w.name, "batch": w.batch, "context": "U[512,4096]", "context_tokens":
+                   int(w.context_lens.sum()), "heads": f"{w.num_heads}/{w.num_kv_heads}", "head_dim": w.head_dim,
+                   "block_size": w.block_size, "pool_blocks": w.num_blocks,
+                   "step": "fused RoPE(theta 5e5)+reshape_and_cache, then paged_attention_v1"},
+        "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": "paged_attention_v1 (decode partition + merge)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": w.decode_bytes(), "us_per_launch": round(ms_v1 * 1e3, 2)},
+    }
+    if not args.no_side:
+        log("[bench] config3 v2 ...")
+        result["v2_long_context"] = side_v2(device, gen, max(3, args.steps // 5))
+        log("[bench] config4 prefill ...")
+        result["prefill"] = side_prefill(device, gen, 3)
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

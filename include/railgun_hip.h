@@ -1,0 +1,255 @@
+/*
+ * railgun_hip.h — C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Every entry point is `extern "C"`, takes raw device pointers and plain
+ * integers, launches asynchronously on the HIP stream it is given (NULL =
+ * the null stream) and never allocates device memory.  This is the surface a
+ * Rust FFI crate binds in place of Railgun's `PagedAttentionKernels`
+ * (crates/vllm-cuda/src/kernels/mod.rs:23-509); the comment above each entry
+ * names the launcher it replaces.
+ *
+ * Conventions shared by all entries
+ *  - Return value: RG_OK (0) or one of the RG_ERR_* codes below.  On error
+ *    rg_last_error() returns a thread-local, human-readable message.  Argument
+ *    checks mirror the reference's CoreError::NotSupported / CoreError::Tensor
+ *    (crates/vllm-cuda/src/kernels/mod.rs:42-54,477-482).
+ *  - dtype: RG_DTYPE_F32 / RG_DTYPE_BF16 / RG_DTYPE_F16, the element type of
+ *    q/k/v/output and of the KV cache.  Arithmetic is fp32 throughout.
+ *  - KV cache layout per block: [num_kv_heads, block_size, head_dim]
+ *    (crates/vllm-cuda/src/kernels/paged_attention.cu:9-10).  kv_block_stride
+ *    is the distance in ELEMENTS between consecutive blocks; pass 0 for the
+ *    dense layout (num_kv_heads*block_size*head_dim).  Railgun's fused pool
+ *    [num_blocks, 2, num_kv_heads, block_size, head_dim]
+ *    (crates/vllm-paged-attention/src/block.rs:70) is addressed with
+ *    k_cache = base, v_cache = base + num_kv_heads*block_size*head_dim and
+ *    kv_block_stride = 2*num_kv_heads*block_size*head_dim.
+ *  - block_table is row-major int32 [batch, max_blocks_per_seq]; context_lens
+ *    is int32 [batch]; slot_mapping is int32 [num_tokens] with
+ *    slot = block_id*block_size + position%block_size, negative = skip
+ *    (crates/vllm-scheduler/src/scheduler.rs:230-235,258-263).
+ *  - Grouped-query attention: q-head h reads kv-head h / (num_heads/num_kv_heads)
+ *    (crates/vllm-cuda/src/kernels/paged_attention.cu:40).
+ *  - rotation_metadata arguments exist for signature compatibility with the
+ *    IsoQuant launchers.  Railgun's rotation is the identity
+ *    (crates/vllm-cuda/src/kernels/isoquant_utils.cuh:54-58), so the attention
+ *    entries ignore it (it may be NULL).
+ */
+#ifndef RAILGUN_HIP_H
+#define RAILGUN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RG_ABI_VERSION 1
+
+/* Status codes. */
+#define RG_OK 0
+#define RG_ERR_INVALID_ARGUMENT 1 /* null pointer, negative size, bad GQA ratio  */
+#define RG_ERR_NOT_SUPPORTED 2    /* head_dim / dtype / block_size out of range  */
+#define RG_ERR_HIP 3              /* HIP runtime or launch failure               */
+#define RG_ERR_WORKSPACE 4        /* workspace missing or smaller than required  */
+
+/* Element types. */
+#define RG_DTYPE_F32 0
+#define RG_DTYPE_BF16 1
+#define RG_DTYPE_F16 2
+
+/* Largest head_dim the paged-attention entries accept
+ * (MAX_HEAD_DIM_PAGED_ATTENTION, crates/vllm-cuda/src/kernels/mod.rs:20). */
+#define RG_MAX_HEAD_DIM 256
+
+/* Thread-local message describing the last failing call on this thread. */
+const char* rg_last_error(void);
+
+/* RG_ABI_VERSION of the loaded library. */
+int rg_abi_version(void);
+
+/* Checks that `device_ordinal` is a gfx950 device and that every kernel's code
+ * object is loadable there.  Replaces PagedAttentionKernels::new
+ * (crates/vllm-cuda/src/kernels/mod.rs:57-190), which loads the PTX modules;
+ * here the code objects are linked into the library, so nothing is cached
+ * and the call is optional. */
+int rg_init(int device_ordinal);
+
+/* ---------------------------------------------------------------- RoPE ---- */
+
+/* In-place rotate-half RoPE on x [num_tokens, num_heads, head_dim]:
+ *   x[i]      = x[i]*c - x[i+D/2]*s
+ *   x[i+D/2]  = x[i+D/2]*c + x[i]*s,   c = cos_sin[pos*D + i], s = cos_sin[pos*D + D/2 + i]
+ * with pos = positions[token].  cos_sin is fp32 [max_position, head_dim].
+ * Replaces launch_rope (crates/vllm-cuda/src/kernels/mod.rs:196-225) /
+ * rotary_embedding_kernel (crates/vllm-cuda/src/kernels/rope.cu:11-42). */
+int rg_rope(void* x, const float* cos_sin, const int32_t* positions,
+            int32_t num_heads, int32_t head_dim, int32_t num_tokens,
+            int32_t dtype, void* stream);
+
+/* Host helper (no GPU): fills `table` (host memory, fp32 [max_position, head_dim])
+ * with the HF Llama convention inv_freq_i = theta^(-2i/D), angle = pos*inv_freq_i,
+ * cos in columns [0, D/2), sin in columns [D/2, D).  Computed in double and
+ * rounded once to fp32.  The reference never builds this table
+ * (crates/vllm-cuda/src/kernels/paged_attn_op.rs:236-268 takes it as input). */
+int rg_rope_cos_sin_table(float* table, int32_t max_position, int32_t head_dim,
+                          double theta);
+
+/* ------------------------------------------------------ KV-cache writes ---- */
+
+/* Scatters k, v [num_tokens, num_kv_heads, head_dim] into the paged caches:
+ * slot = slot_mapping[t]; skipped when slot < 0; block = slot / block_size,
+ * offset = slot % block_size.  A bit-exact copy.
+ * Replaces launch_reshape_and_cache (crates/vllm-cuda/src/kernels/mod.rs:227-262)
+ * / reshape_and_cache (crates/vllm-cuda/src/kernels/paged_attention.cu:111-138). */
+int rg_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_cache,
+                         const int32_t* slot_mapping, int32_t num_kv_heads,
+                         int32_t head_dim, int32_t block_size, int32_t num_tokens,
+                         int32_t dtype, int64_t kv_block_stride, void* stream);
+
+/* As rg_reshape_and_cache, and additionally, for every token written at
+ * offset 0 of its block, stores the identity rotation (0,0,0,1, 0,0,0,1) into
+ * rotation_metadata fp32 [num_blocks, num_kv_heads, head_dim/4, 8].  The
+ * K/V data are copied unchanged (the rotation is the identity).
+ * Replaces launch_reshape_and_cache_isoquant
+ * (crates/vllm-cuda/src/kernels/mod.rs:264-303) /
+ * reshape_and_cache_isoquant (crates/vllm-cuda/src/kernels/paged_attention.cu:140-185). */
+int rg_reshape_and_cache_isoquant(const void* k, const void* v, void* k_cache,
+                                  void* v_cache, const int32_t* slot_mapping,
+                                  float* rotation_metadata, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t block_size,
+                                  int32_t num_tokens, int32_t dtype,
+                                  int64_t kv_block_stride, void* stream);
+
+/* One pass over the new tokens: RoPE on q [num_tokens, num_heads, head_dim]
+ * in place, RoPE on k [num_tokens, num_kv_heads, head_dim] (k itself is left
+ * unchanged; the rotated rows go to the cache) and the scatter of rotated k
+ * and of v into the paged caches by slot_mapping, with the same arithmetic
+ * as rg_rope followed by rg_reshape_and_cache.  New entry (the reference's
+ * RoPE has no caller, crates/vllm-cuda/src/kernels/paged_attn_op.rs:236-268). */
+int rg_rope_reshape_and_cache(void* q, const void* k, const void* v,
+                              void* k_cache, void* v_cache, const float* cos_sin,
+                              const int32_t* positions, const int32_t* slot_mapping,
+                              int32_t num_heads, int32_t num_kv_heads,
+                              int32_t head_dim, int32_t block_size,
+                              int32_t num_tokens, int32_t dtype,
+                              int64_t kv_block_stride, void* stream);
+
+/* ------------------------------------------------------- decode, v1 -------- */
+
+/* Bytes of workspace rg_paged_attention_v1 / _v1_plus use for the given shape
+ * (0 is a valid answer: then no workspace is needed). */
+size_t rg_paged_attention_v1_workspace_bytes(int32_t batch_size, int32_t num_heads,
+                                             int32_t head_dim, int32_t block_size,
+                                             int32_t max_blocks_per_seq);
+
+/* Decode attention, one query token per sequence:
+ *   out[s,h,:] = sum_t softmax_t(scale * q[s,h,:].K_t) V_t  over t < context_lens[s]
+ * q/out [batch, num_heads, head_dim].  context_lens[s] == 0 gives zeros.
+ * With workspace == NULL the whole context of a sequence is processed by one
+ * workgroup per kv-head; with a workspace of rg_paged_attention_v1_workspace_bytes
+ * the context is split into partitions that run in parallel and are merged
+ * (faster for ragged batches).  Both give the same result within fp32 rounding.
+ * Replaces launch_v1 (crates/vllm-cuda/src/kernels/mod.rs:305-348). */
+int rg_paged_attention_v1(const void* query, const void* key_cache,
+                          const void* value_cache, const int32_t* block_table,
+                          const int32_t* context_lens, void* output, float scale,
+                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                          int32_t block_size, int32_t max_blocks_per_seq,
+                          int32_t batch_size, int32_t dtype, int64_t kv_block_stride,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Same computation as rg_paged_attention_v1, with the rotation_metadata
+ * argument of launch_v1_plus (crates/vllm-cuda/src/kernels/mod.rs:350-399),
+ * which is ignored (identity rotation). */
+int rg_paged_attention_v1_plus(const void* query, const void* key_cache,
+                               const void* value_cache, const int32_t* block_table,
+                               const int32_t* context_lens, void* output,
+                               const float* rotation_metadata, float scale,
+                               int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_dim, int32_t block_size,
+                               int32_t max_blocks_per_seq, int32_t batch_size,
+                               int32_t dtype, int64_t kv_block_stride,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------- decode, v2 split-K ------ */
+
+/* Bytes of the three fp32 scratch arrays of v2 (tmp_out, exp_sums, max_logits)
+ * for a [batch, num_heads, num_partitions, head_dim] problem, laid out
+ * back-to-back in that order, each 256-byte aligned. */
+size_t rg_v2_workspace_bytes(int32_t batch_size, int32_t num_heads,
+                             int32_t num_partitions, int32_t head_dim);
+
+/* Partition p of sequence s covers tokens [p*P, min((p+1)*P, ctx)).  Writes
+ *   tmp_out[s,h,p,:]   = sum_t exp(x_t - m_p) V_t      (fp32, unnormalised)
+ *   exp_sums[s,h,p]    = sum_t exp(x_t - m_p)
+ *   max_logits[s,h,p]  = m_p = max_t x_t,   x_t = scale * q.K_t
+ * Partitions with p*P >= ctx are left untouched.  P = partition_size must be a
+ * positive multiple of block_size (the reference fixes P = 256,
+ * crates/vllm-cuda/src/kernels/paged_attention_utils.cuh:10).
+ * Replaces launch_v2_partition (crates/vllm-cuda/src/kernels/mod.rs:401-456). */
+int rg_paged_attention_v2_partition(const void* query, const void* key_cache,
+                                    const void* value_cache,
+                                    const int32_t* block_table,
+                                    const int32_t* context_lens, float* tmp_out,
+                                    float* exp_sums, float* max_logits,
+                                    const float* rotation_metadata, float scale,
+                                    int32_t num_heads, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t block_size,
+                                    int32_t max_blocks_per_seq,
+                                    int32_t num_partitions, int32_t batch_size,
+                                    int32_t partition_size, int32_t dtype,
+                                    int64_t kv_block_stride, void* stream);
+
+/* Merges the ceil(ctx/P) partitions of each (s,h):
+ *   M = max_p m_p, r_p = exp(m_p - M), out = sum_p r_p tmp_out_p / sum_p r_p l_p
+ * ctx == 0 writes zeros.  No cap on the number of partitions (the reference
+ * caps at 512, crates/vllm-cuda/src/kernels/paged_attention_v2_reduce.cu:48).
+ * Replaces launch_v2_reduce (crates/vllm-cuda/src/kernels/mod.rs:458-508). */
+int rg_paged_attention_v2_reduce(void* output, const float* exp_sums,
+                                 const float* max_logits, const float* tmp_out,
+                                 const int32_t* context_lens,
+                                 const float* rotation_metadata, int32_t num_heads,
+                                 int32_t head_dim, int32_t num_partitions,
+                                 int32_t batch_size, int32_t partition_size,
+                                 int32_t dtype, void* stream);
+
+/* v2_partition followed by v2_reduce, with the scratch carved out of
+ * `workspace` (rg_v2_workspace_bytes).  num_partitions = ceil(max_context_len/P).
+ * The host side of PagedAttentionOp::execute's v2 branch
+ * (crates/vllm-cuda/src/kernels/paged_attn_op.rs:108-158). */
+int rg_paged_attention_v2(const void* query, const void* key_cache,
+                          const void* value_cache, const int32_t* block_table,
+                          const int32_t* context_lens, void* output, float scale,
+                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                          int32_t block_size, int32_t max_blocks_per_seq,
+                          int32_t batch_size, int32_t max_context_len,
+                          int32_t partition_size, int32_t dtype,
+                          int64_t kv_block_stride, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------ packed prefill ---- */
+
+/* Causal attention for a packed stream of new tokens (continuous batching).
+ * Sequence s owns query rows [cu_seqlens[s], cu_seqlens[s+1]) of
+ * query/output [num_tokens, num_heads, head_dim]; its context (prior cache +
+ * these rows) has length context_lens[s] and must already be in the paged
+ * cache (written by rg_reshape_and_cache / rg_rope_reshape_and_cache).
+ * Row j of sequence s sits at position context_lens[s] - L_s + j and attends
+ * to cache positions 0..that position inclusive, read through block_table.
+ * The reference has no such kernel (it routes prefill through the decode op,
+ * crates/vllm-models/src/llama/attention.rs:128-132). */
+int rg_prefill_packed(const void* query, const void* key_cache,
+                      const void* value_cache, const int32_t* block_table,
+                      const int32_t* context_lens, const int32_t* cu_seqlens,
+                      void* output, float scale, int32_t num_heads,
+                      int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                      int32_t max_blocks_per_seq, int32_t num_seqs,
+                      int32_t num_tokens, int32_t max_query_len, int32_t dtype,
+                      int64_t kv_block_stride, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* RAILGUN_HIP_H */

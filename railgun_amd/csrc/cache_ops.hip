@@ -1,0 +1,366 @@
+// KV-cache scatter (reshape_and_cache), identity-IsoQuant metadata, RoPE and the
+// fused RoPE + scatter pass over the new tokens.
+//
+// All four are HBM-bound byte movers: one workgroup per new token, 16-byte
+// vector loads/stores along the contiguous head_dim rows wherever the row
+// length and the pointers allow it, and no LDS.
+#include "rg_common.hpp"
+
+namespace rg {
+namespace {
+
+constexpr int kCacheThreads = 256;
+
+struct CacheGeom {
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t block_size;
+  int64_t kv_block_stride;  // elements
+};
+
+// Element offset of (block, kv-head, in-block offset) row in a paged cache
+// (crates/vllm-cuda/src/kernels/paged_attention.cu:130-134, with an explicit
+// block stride).
+__device__ __forceinline__ int64_t cache_row(const CacheGeom& g, int64_t blk, int h, int off) {
+  return blk * g.kv_block_stride + ((int64_t)h * g.block_size + off) * g.head_dim;
+}
+
+// One token per workgroup; copies its num_kv_heads rows of k and v with
+// 16-byte (uint4) moves.  Requires head_dim*elem_bytes % 16 == 0 and 16-byte
+// aligned bases / block stride (checked on the host).
+__global__ __launch_bounds__(kCacheThreads) void scatter_kv_vec16(
+    const uint4* __restrict__ k, const uint4* __restrict__ v, uint4* __restrict__ k_cache,
+    uint4* __restrict__ v_cache, const int32_t* __restrict__ slot_mapping, CacheGeom g,
+    int row_vecs, int64_t stride_vecs, float* __restrict__ rotation_metadata) {
+  const int t = blockIdx.x;
+  const int32_t slot = slot_mapping[t];
+  if (slot < 0) return;  // padding token (paged_attention.cu:127-128)
+  const int64_t blk = slot / g.block_size;
+  const int off = slot % g.block_size;
+  const int per_tensor = g.num_kv_heads * row_vecs;
+  const int64_t src_base = (int64_t)t * per_tensor;
+  for (int i = threadIdx.x; i < 2 * per_tensor; i += kCacheThreads) {
+    const bool is_v = i >= per_tensor;
+    const int j = is_v ? i - per_tensor : i;
+    const int h = j / row_vecs;
+    const int c = j - h * row_vecs;
+    const int64_t dst = blk * stride_vecs + ((int64_t)h * g.block_size + off) * row_vecs + c;
+    if (is_v) {
+      v_cache[dst] = v[src_base + j];
+    } else {
+      k_cache[dst] = k[src_base + j];
+    }
+  }
+  if (rotation_metadata != nullptr && off == 0) {
+    // Identity (qL, qR) = ((0,0,0,1), (0,0,0,1)) for every 4-d group
+    // (paged_attention.cu:168-173 with isoquant_utils.cuh:54-58).
+    const int groups = g.num_kv_heads * (g.head_dim / 4);
+    float4* meta = reinterpret_cast<float4*>(rotation_metadata) + blk * groups * 2;
+    for (int i = threadIdx.x; i < groups * 2; i += kCacheThreads) {
+      meta[i] = make_float4(0.f, 0.f, 0.f, 1.f);
+    }
+  }
+}
+
+// Element-wise fallback for rows that are not 16-byte multiples or unaligned
+// pointers.  S is the storage type (float or uint16_t).
+template <typename S>
+__global__ __launch_bounds__(kCacheThreads) void scatter_kv_elem(
+    const S* __restrict__ k, const S* __restrict__ v, S* __restrict__ k_cache,
+    S* __restrict__ v_cache, const int32_t* __restrict__ slot_mapping, CacheGeom g,
+    float* __restrict__ rotation_metadata) {
+  const int t = blockIdx.x;
+  const int32_t slot = slot_mapping[t];
+  if (slot < 0) return;
+  const int64_t blk = slot / g.block_size;
+  const int off = slot % g.block_size;
+  const int per_tensor = g.num_kv_heads * g.head_dim;
+  const int64_t src_base = (int64_t)t * per_tensor;
+  for (int i = threadIdx.x; i < 2 * per_tensor; i += kCacheThreads) {
+    const bool is_v = i >= per_tensor;
+    const int j = is_v ? i - per_tensor : i;
+    const int h = j / g.head_dim;
+    const int d = j - h * g.head_dim;
+    const int64_t dst = cache_row(g, blk, h, off) + d;
+    if (is_v) {
+      v_cache[dst] = v[src_base + j];
+    } else {
+      k_cache[dst] = k[src_base + j];
+    }
+  }
+  if (rotation_metadata != nullptr && off == 0) {
+    const int groups = g.num_kv_heads * (g.head_dim / 4);
+    float* meta = rotation_metadata + blk * groups * 8;
+    for (int i = threadIdx.x; i < groups * 8; i += kCacheThreads) {
+      meta[i] = ((i & 3) == 3) ? 1.f : 0.f;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ RoPE ----
+
+// Rotate-half on one pair with the rounding of the reference expression
+// (rope.cu:34-41) made explicit: each product and the difference/sum are
+// rounded separately (no fused multiply-add), so results are reproducible.
+__device__ __forceinline__ void rotate_pair(float lo, float hi, float c, float s, float& out_lo,
+                                            float& out_hi) {
+#pragma clang fp contract(off)
+  const float a = lo * c;
+  const float b = hi * s;
+  const float e = hi * c;
+  const float f = lo * s;
+  out_lo = a - b;
+  out_hi = e + f;
+}
+
+// Applies RoPE to `nheads` rows of `x` (row stride head_dim) for one token and
+// writes them to dst rows (dst may alias x).  Each thread handles VP
+// consecutive pairs.  dst_row(h) returns the element offset of row h.
+template <typename T, int VP, typename DstRow>
+__device__ __forceinline__ void rope_rows(const typename elem<T>::storage* __restrict__ x,
+                                          typename elem<T>::storage* dst, DstRow dst_row,
+                                          const float* __restrict__ cs, int nheads,
+                                          int head_dim) {
+  using E = elem<T>;
+  const int half = head_dim / 2;
+  const int groups_per_row = half / VP;
+  const int total = nheads * groups_per_row;
+  for (int i = threadIdx.x; i < total; i += kCacheThreads) {
+    const int h = i / groups_per_row;
+    const int c0 = (i - h * groups_per_row) * VP;
+    const typename E::storage* src = x + (int64_t)h * head_dim;
+    float lo[VP], hi[VP];
+#pragma unroll
+    for (int u = 0; u < VP; ++u) {
+      lo[u] = E::to_f32(src[c0 + u]);
+      hi[u] = E::to_f32(src[half + c0 + u]);
+    }
+    const int64_t d0 = dst_row(h);
+#pragma unroll
+    for (int u = 0; u < VP; ++u) {
+      float ol, oh;
+      rotate_pair(lo[u], hi[u], cs[c0 + u], cs[half + c0 + u], ol, oh);
+      dst[d0 + c0 + u] = E::from_f32(ol);
+      dst[d0 + half + c0 + u] = E::from_f32(oh);
+    }
+  }
+}
+
+// In-place RoPE; one workgroup per token (rope.cu:11-42 semantics).
+template <typename T, int VP>
+__global__ __launch_bounds__(kCacheThreads) void rope_inplace_kernel(
+    typename elem<T>::storage* __restrict__ x, const float* __restrict__ cos_sin,
+    const int32_t* __restrict__ positions, int num_heads, int head_dim) {
+  const int t = blockIdx.x;
+  const int64_t pos = positions[t];
+  auto* row = x + (int64_t)t * num_heads * head_dim;
+  rope_rows<T, VP>(row, row, [=](int h) { return (int64_t)h * head_dim; },
+                   cos_sin + pos * head_dim, num_heads, head_dim);
+}
+
+// Fused pass over one new token: rotate q in place, rotate k into the cache,
+// copy v into the cache.
+template <typename T, int VP>
+__global__ __launch_bounds__(kCacheThreads) void rope_cache_kernel(
+    typename elem<T>::storage* __restrict__ q, const typename elem<T>::storage* __restrict__ k,
+    const typename elem<T>::storage* __restrict__ v, typename elem<T>::storage* __restrict__ k_cache,
+    typename elem<T>::storage* __restrict__ v_cache, const float* __restrict__ cos_sin,
+    const int32_t* __restrict__ positions, const int32_t* __restrict__ slot_mapping,
+    int num_heads, CacheGeom g) {
+  using S = typename elem<T>::storage;
+  const int t = blockIdx.x;
+  const int D = g.head_dim;
+  const int64_t pos = positions[t];
+  const float* cs = cos_sin + pos * D;
+  S* qrow = q + (int64_t)t * num_heads * D;
+  rope_rows<T, VP>(qrow, qrow, [=](int h) { return (int64_t)h * D; }, cs, num_heads, D);
+
+  const int32_t slot = slot_mapping[t];
+  if (slot < 0) return;
+  const int64_t blk = slot / g.block_size;
+  const int off = slot % g.block_size;
+  const S* krow = k + (int64_t)t * g.num_kv_heads * D;
+  rope_rows<T, VP>(krow, k_cache, [=](int h) { return cache_row(g, blk, h, off); }, cs,
+                   g.num_kv_heads, D);
+  const S* vrow = v + (int64_t)t * g.num_kv_heads * D;
+  for (int i = threadIdx.x; i < g.num_kv_heads * D; i += kCacheThreads) {
+    const int h = i / D;
+    const int d = i - h * D;
+    v_cache[cache_row(g, blk, h, off) + d] = vrow[i];
+  }
+}
+
+// ------------------------------------------------------------ host side ----
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_cache_args(const char* op, const void* k, const void* v, const void* kc,
+                     const void* vc, const int32_t* slots, int32_t hkv, int32_t d, int32_t bs,
+                     int32_t n, int32_t dtype, int64_t stride) {
+  if (dtype_bytes(dtype) == 0) return fail(RG_ERR_NOT_SUPPORTED, "%s: unknown dtype %d", op, dtype);
+  if (n < 0 || hkv <= 0 || d <= 0 || bs <= 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT,
+                "%s: need num_tokens >= 0 and positive num_kv_heads/head_dim/block_size "
+                "(got %d, %d, %d, %d)", op, n, hkv, d, bs);
+  }
+  if (stride != 0 && stride < (int64_t)hkv * bs * d) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: kv_block_stride %lld smaller than a block (%lld)",
+                op, (long long)stride, (long long)hkv * bs * d);
+  }
+  if (n > 0 && (!k || !v || !kc || !vc || !slots)) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
+  }
+  return RG_OK;
+}
+
+int launch_scatter(const char* op, const void* k, const void* v, void* k_cache, void* v_cache,
+                   const int32_t* slot_mapping, float* meta, int32_t hkv, int32_t d, int32_t bs,
+                   int32_t n, int32_t dtype, int64_t stride, void* stream) {
+  int st = check_cache_args(op, k, v, k_cache, v_cache, slot_mapping, hkv, d, bs, n, dtype, stride);
+  if (st != RG_OK) return st;
+  if (meta != nullptr && d % 4 != 0) {
+    return fail(RG_ERR_NOT_SUPPORTED, "%s: head_dim must be a multiple of 4, got %d", op, d);
+  }
+  if (n == 0) return ok();
+  const int64_t stride_el = stride ? stride : (int64_t)hkv * bs * d;
+  CacheGeom g{hkv, d, bs, stride_el};
+  const int eb = dtype_bytes(dtype);
+  const int64_t row_bytes = (int64_t)d * eb;
+  hipStream_t s = as_stream(stream);
+  if (row_bytes % 16 == 0 && (stride_el * eb) % 16 == 0 && aligned16(k) && aligned16(v) &&
+      aligned16(k_cache) && aligned16(v_cache)) {
+    const int row_vecs = (int)(row_bytes / 16);
+    hipLaunchKernelGGL(scatter_kv_vec16, dim3(n), dim3(kCacheThreads), 0, s,
+                       static_cast<const uint4*>(k), static_cast<const uint4*>(v),
+                       static_cast<uint4*>(k_cache), static_cast<uint4*>(v_cache), slot_mapping,
+                       g, row_vecs, stride_el * eb / 16, meta);
+  } else if (eb == 4) {
+    hipLaunchKernelGGL(scatter_kv_elem<float>, dim3(n), dim3(kCacheThreads), 0, s,
+                       static_cast<const float*>(k), static_cast<const float*>(v),
+                       static_cast<float*>(k_cache), static_cast<float*>(v_cache), slot_mapping,
+                       g, meta);
+  } else {
+    hipLaunchKernelGGL(scatter_kv_elem<uint16_t>, dim3(n), dim3(kCacheThreads), 0, s,
+                       static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                       static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
+                       slot_mapping, g, meta);
+  }
+  return check_launch(op);
+}
+
+template <typename T>
+int launch_rope_inplace(void* x, const float* cs, const int32_t* pos, int h, int d, int n,
+                        hipStream_t s) {
+  using S = typename elem<T>::storage;
+  if ((d / 2) % 4 == 0) {
+    hipLaunchKernelGGL((rope_inplace_kernel<T, 4>), dim3(n), dim3(kCacheThreads), 0, s,
+                       static_cast<S*>(x), cs, pos, h, d);
+  } else {
+    hipLaunchKernelGGL((rope_inplace_kernel<T, 1>), dim3(n), dim3(kCacheThreads), 0, s,
+                       static_cast<S*>(x), cs, pos, h, d);
+  }
+  return check_launch("rope");
+}
+
+template <typename T>
+int launch_rope_cache(void* q, const void* k, const void* v, void* kc, void* vc, const float* cs,
+                      const int32_t* pos, const int32_t* slots, int h, CacheGeom g, int n,
+                      hipStream_t s) {
+  using S = typename elem<T>::storage;
+  if ((g.head_dim / 2) % 4 == 0) {
+    hipLaunchKernelGGL((rope_cache_kernel<T, 4>), dim3(n), dim3(kCacheThreads), 0, s,
+                       static_cast<S*>(q), static_cast<const S*>(k), static_cast<const S*>(v),
+                       static_cast<S*>(kc), static_cast<S*>(vc), cs, pos, slots, h, g);
+  } else {
+    hipLaunchKernelGGL((rope_cache_kernel<T, 1>), dim3(n), dim3(kCacheThreads), 0, s,
+                       static_cast<S*>(q), static_cast<const S*>(k), static_cast<const S*>(v),
+                       static_cast<S*>(kc), static_cast<S*>(vc), cs, pos, slots, h, g);
+  }
+  return check_launch("rope_reshape_and_cache");
+}
+
+}  // namespace
+
+int probe_cache_kernels() {
+  hipFuncAttributes a;
+  if (hipFuncGetAttributes(&a, reinterpret_cast<const void*>(scatter_kv_vec16)) != hipSuccess ||
+      hipFuncGetAttributes(&a, reinterpret_cast<const void*>(rope_cache_kernel<bf16_t, 4>)) !=
+          hipSuccess) {
+    return fail(RG_ERR_HIP, "failed to load the KV-cache kernels: %s",
+                hipGetErrorString(hipGetLastError()));
+  }
+  return RG_OK;
+}
+
+}  // namespace rg
+
+using namespace rg;
+
+extern "C" int rg_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_cache,
+                                    const int32_t* slot_mapping, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t block_size, int32_t num_tokens,
+                                    int32_t dtype, int64_t kv_block_stride, void* stream) {
+  return launch_scatter("reshape_and_cache", k, v, k_cache, v_cache, slot_mapping, nullptr,
+                        num_kv_heads, head_dim, block_size, num_tokens, dtype, kv_block_stride,
+                        stream);
+}
+
+extern "C" int rg_reshape_and_cache_isoquant(const void* k, const void* v, void* k_cache,
+                                             void* v_cache, const int32_t* slot_mapping,
+                                             float* rotation_metadata, int32_t num_kv_heads,
+                                             int32_t head_dim, int32_t block_size,
+                                             int32_t num_tokens, int32_t dtype,
+                                             int64_t kv_block_stride, void* stream) {
+  if (rotation_metadata == nullptr && num_tokens > 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "reshape_and_cache_isoquant: null rotation_metadata");
+  }
+  return launch_scatter("reshape_and_cache_isoquant", k, v, k_cache, v_cache, slot_mapping,
+                        rotation_metadata, num_kv_heads, head_dim, block_size, num_tokens, dtype,
+                        kv_block_stride, stream);
+}
+
+extern "C" int rg_rope(void* x, const float* cos_sin, const int32_t* positions, int32_t num_heads,
+                       int32_t head_dim, int32_t num_tokens, int32_t dtype, void* stream) {
+  if (dtype_bytes(dtype) == 0) return fail(RG_ERR_NOT_SUPPORTED, "rope: unknown dtype %d", dtype);
+  if (num_tokens < 0 || num_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT,
+                "rope: need num_tokens >= 0, num_heads > 0 and an even head_dim > 0 "
+                "(got %d, %d, %d)", num_tokens, num_heads, head_dim);
+  }
+  if (num_tokens == 0) return ok();
+  if (!x || !cos_sin || !positions) return fail(RG_ERR_INVALID_ARGUMENT, "rope: null pointer");
+  hipStream_t s = as_stream(stream);
+  return dispatch_dtype(dtype, [&](auto tag) {
+    return launch_rope_inplace<decltype(tag)>(x, cos_sin, positions, num_heads, head_dim,
+                                              num_tokens, s);
+  });
+}
+
+extern "C" int rg_rope_reshape_and_cache(void* q, const void* k, const void* v, void* k_cache,
+                                         void* v_cache, const float* cos_sin,
+                                         const int32_t* positions, const int32_t* slot_mapping,
+                                         int32_t num_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t block_size,
+                                         int32_t num_tokens, int32_t dtype,
+                                         int64_t kv_block_stride, void* stream) {
+  const char* op = "rope_reshape_and_cache";
+  int st = check_cache_args(op, k, v, k_cache, v_cache, slot_mapping, num_kv_heads, head_dim,
+                            block_size, num_tokens, dtype, kv_block_stride);
+  if (st != RG_OK) return st;
+  if (num_heads <= 0 || head_dim % 2 != 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: need num_heads > 0 and an even head_dim", op);
+  }
+  if (num_heads % num_kv_heads != 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: num_heads %d not a multiple of num_kv_heads %d", op,
+                num_heads, num_kv_heads);
+  }
+  if (num_tokens == 0) return ok();
+  if (!q || !cos_sin || !positions) return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer", op);
+  CacheGeom g{num_kv_heads, head_dim, block_size,
+              kv_block_stride ? kv_block_stride : (int64_t)num_kv_heads * block_size * head_dim};
+  hipStream_t s = as_stream(stream);
+  return dispatch_dtype(dtype, [&](auto tag) {
+    return launch_rope_cache<decltype(tag)>(q, k, v, k_cache, v_cache, cos_sin, positions,
+                                            slot_mapping, num_heads, g, num_tokens, s);
+  });
+}

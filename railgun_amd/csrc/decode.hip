@@ -1,0 +1,852 @@
+// Paged decode attention (one query token per sequence) for gfx950.
+//
+// Two partition kernels share one contract.  A workgroup handles one
+// (partition p, kv-head, sequence) work item; partition p covers context
+// tokens [p*P, min((p+1)*P, ctx)).  Depending on `mode` it writes
+//   MODE_FINAL  : the normalised output (the grid has one partition per sequence)
+//   MODE_PARTIAL: the unnormalised partial  tmp_out / exp_sums / max_logits
+//                 (crates/vllm-cuda/src/kernels/paged_attention_v2_partition.cu:95-106)
+//   MODE_AUTO   : MODE_FINAL for sequences that fit one partition, MODE_PARTIAL
+//                 otherwise; the merge kernel then skips the single-partition ones.
+//
+// * decode_mfma_kernel (bf16/f16, head_dim 64/128, block_size 16): the GQA
+//   group's query heads are replicated into the 16 rows of a
+//   v_mfma_f32_16x16x32 A operand, each 16-token K block is the B operand, so
+//   one K/V block is read from HBM once per kv-head for all of its q-heads.
+//   Scores go through an exp2 online softmax whose max is shared by the whole
+//   wave (DPP row reductions), P.V runs on the VALU in fp32 with 16-byte V
+//   loads, and four waves split the partition's blocks and merge through LDS.
+// * decode_generic_kernel: any dtype (fp32 included), head_dim % 4 == 0 up to
+//   256, any block size and GQA ratio; one wave per (partition, q-head, seq),
+//   each lane owning 4 dims.  Used where the MFMA kernel does not apply.
+//
+// decode_merge_kernel combines the partials of one (seq, q-head):
+//   M = max_p m_p, out = sum_p e^(m_p-M) tmp_p / sum_p e^(m_p-M) l_p
+// (crates/vllm-cuda/src/kernels/paged_attention_v2_reduce.cu:50-95).
+#include <math.h>
+
+#include <algorithm>
+
+#include "rg_common.hpp"
+
+namespace rg {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+enum DecodeMode : int32_t { MODE_FINAL = 0, MODE_PARTIAL = 1, MODE_AUTO = 2 };
+
+struct DecodeArgs {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  const int32_t* block_table;
+  const int32_t* context_lens;
+  void* out;
+  float* tmp_out;
+  float* exp_sums;
+  float* max_logits;
+  float scale_log2;  // scale * log2(e)
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t block_size;
+  int32_t max_blocks;
+  int32_t num_partitions;  // stride of the partial arrays
+  int32_t partition_size;  // tokens per partition
+  int64_t kv_stride;       // elements between blocks
+  int32_t mode;
+};
+
+__device__ __forceinline__ int num_parts_for(int ctx, int P) { return (ctx + P - 1) / P; }
+
+// ------------------------------------------------------------- generic ------
+
+template <typename T>
+__global__ __launch_bounds__(64) void decode_generic_kernel(DecodeArgs a) {
+  using E = elem<T>;
+  using S = typename E::storage;
+  const int p = blockIdx.x;
+  const int h = blockIdx.y;
+  const int s = blockIdx.z;
+  const int lane = threadIdx.x;
+  // Contexts longer than the block table row are clamped to it, negative ones to 0.
+  const int ctx = max(0, min(a.context_lens[s], a.max_blocks * a.block_size));
+  const int P = a.partition_size;
+  const int np_s = min(num_parts_for(ctx, P), a.num_partitions);
+  const int D = a.head_dim;
+  const bool final_out = a.mode == MODE_FINAL || (a.mode == MODE_AUTO && np_s <= 1);
+
+  if (p >= np_s) {
+    // Empty context: the single-pass kernels leave zeros
+    // (paged_attention_v1_plus.cu:38 on a zero-filled output).
+    if (ctx == 0 && p == 0 && final_out) {
+      S* o = static_cast<S*>(a.out) + ((int64_t)s * a.num_heads + h) * D;
+      for (int d = lane; d < D; d += 64) E::store(o, d, 0.f);
+    }
+    return;
+  }
+  const int kvh = h / (a.num_heads / a.num_kv_heads);
+  const int d0 = lane * 4;
+  const bool act = d0 < D;
+  const S* qp = static_cast<const S*>(a.q) + ((int64_t)s * a.num_heads + h) * D;
+  float qv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (act) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) qv[u] = E::load(qp, d0 + u);
+  }
+  const S* kc = static_cast<const S*>(a.k_cache);
+  const S* vc = static_cast<const S*>(a.v_cache);
+  const int32_t* bt = a.block_table + (int64_t)s * a.max_blocks;
+
+  float m = -INFINITY, l = 0.f;
+  float o[4] = {0.f, 0.f, 0.f, 0.f};
+  const int t1 = min(ctx, (p + 1) * P);
+  for (int t = p * P; t < t1; ++t) {
+    const int64_t blk = bt[t / a.block_size];
+    const int off = t % a.block_size;
+    const int64_t row = blk * a.kv_stride + ((int64_t)kvh * a.block_size + off) * D;
+    float kv[4] = {0.f, 0.f, 0.f, 0.f}, vv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (act) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        kv[u] = E::load(kc, row + d0 + u);
+        vv[u] = E::load(vc, row + d0 + u);
+      }
+    }
+    float dot = qv[0] * kv[0] + qv[1] * kv[1] + qv[2] * kv[2] + qv[3] * kv[3];
+    dot = wave_sum(dot);
+    const float x = dot * a.scale_log2;
+    const float m_new = fmaxf(m, x);
+    const float alpha = exp2f(m - m_new);
+    const float pe = exp2f(x - m_new);
+    l = l * alpha + pe;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) o[u] = o[u] * alpha + pe * vv[u];
+    m = m_new;
+  }
+
+  if (final_out) {
+    const float inv = l != 0.f ? 1.f / l : 1.f;
+    S* op = static_cast<S*>(a.out) + ((int64_t)s * a.num_heads + h) * D;
+    if (act) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) E::store(op, d0 + u, o[u] * inv);
+    }
+  } else {
+    const int64_t sh = ((int64_t)s * a.num_heads + h) * a.num_partitions + p;
+    if (act) {
+      float4* tp = reinterpret_cast<float4*>(a.tmp_out + sh * D + d0);
+      *tp = make_float4(o[0], o[1], o[2], o[3]);
+    }
+    if (lane == 0) {
+      a.exp_sums[sh] = l;
+      a.max_logits[sh] = m * kLn2;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- MFMA ------
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T> struct mfma16;
+template <> struct mfma16<bf16_t> {
+  __device__ static __forceinline__ f32x4_t run(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ void unpack8(uint4 u, float* f) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
+template <> struct mfma16<f16_t> {
+  __device__ static __forceinline__ f32x4_t run(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ void unpack8(uint4 u, float* f) {
+    const f16x8_t h = __builtin_bit_cast(f16x8_t, u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)h[i];
+  }
+};
+
+// DPP helpers: `ctrl` is a DPP control word (quad_perm / row_ror).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Max / sum over the 16 lanes of a row, result in every lane of the row.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp<0x128>(v));  // row_ror:8
+  return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x124>(v);
+  v += dpp<0x128>(v);
+  return v;
+}
+
+// Orders LDS writes of one lane before LDS reads of another lane of the same
+// wave (and keeps the compiler from moving accesses across).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+constexpr int kBS = 16;       // tokens per KV block on the MFMA path
+constexpr int kWaves = 4;     // waves per workgroup
+constexpr int kThreads = kWaves * 64;
+
+// D: head_dim (64 or 128); G: q-heads per kv-head (1, 2, 4, 8 or 16).
+template <typename T, int D, int G>
+__global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
+  using MF = mfma16<T>;
+  using S = uint16_t;
+  constexpr int NK = D / 32;           // MFMAs (and 16-byte K loads) per block
+  constexpr int ROWV = D / 8;          // 16-byte vectors per token row
+  constexpr int TPI = 64 / ROWV;       // tokens covered by one V load instruction
+  constexpr int NV = kBS / TPI;        // V loads per block
+  constexpr int GP = G < 4 ? 4 : G;    // padded heads per LDS row
+  constexpr int HG = (G + 3) / 4;      // rows of the MFMA output that hold distinct heads
+
+  __shared__ float p_lds[kWaves][2][kBS * GP];
+  __shared__ float alpha_lds[kWaves][2][GP];
+  __shared__ float acc_lds[kWaves][G * D];
+  __shared__ float ml_lds[kWaves][2][GP];
+
+  const int p = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int s = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  const int ctx = max(0, min(a.context_lens[s], a.max_blocks * kBS));
+  const int P = a.partition_size;
+  const int np_s = min(num_parts_for(ctx, P), a.num_partitions);
+  const bool final_out = a.mode == MODE_FINAL || (a.mode == MODE_AUTO && np_s <= 1);
+  const int H = a.num_heads;
+
+  if (p >= np_s) {
+    if (ctx == 0 && p == 0 && final_out) {
+      S* o = static_cast<S*>(a.out) + ((int64_t)s * H + (int64_t)kvh * G) * D;
+      for (int i = tid; i < G * D; i += kThreads) o[i] = 0;
+    }
+    return;
+  }
+
+  // Blocks of this partition; wave w takes blocks b0+w, b0+w+4, ...
+  const int nblk_ctx = (ctx + kBS - 1) / kBS;
+  const int b0 = p * (P / kBS);
+  const int b1 = min(nblk_ctx, b0 + P / kBS);
+  const int nb = b0 + w < b1 ? (b1 - (b0 + w) + kWaves - 1) / kWaves : 0;
+
+  // QK role: column (token in block) and k-segment of this lane.
+  const int col = lane & 15;
+  const int seg = lane >> 4;
+  // PV role: token row within a V load and the 8-element slice of head_dim.
+  const int vrow = lane / ROWV;
+  const int vd0 = (lane % ROWV) * 8;
+
+  // A operand: q rows replicated so that MFMA row m holds head (m % G).
+  const S* qbase = static_cast<const S*>(a.q) + ((int64_t)s * H + (int64_t)kvh * G) * D;
+  uint4 qa[NK];
+  {
+    const uint4* qrow = reinterpret_cast<const uint4*>(qbase + (int64_t)(col % G) * D + seg * (D / 4));
+#pragma unroll
+    for (int i = 0; i < NK; ++i) qa[i] = qrow[i];
+  }
+
+  const S* kc = static_cast<const S*>(a.k_cache);
+  const S* vc = static_cast<const S*>(a.v_cache);
+  const int32_t* bt = a.block_table + (int64_t)s * a.max_blocks;
+  const int64_t head_off = (int64_t)kvh * kBS * D;
+
+  float m_run[4], l_run[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m_run[r] = -INFINITY;
+    l_run[r] = 0.f;
+  }
+  float acc[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+
+  uint4 kr[NK], vr[NV];
+  auto load_block = [&](int bidx, uint4* kk, uint4* vv) {
+    const int64_t blk = bt[bidx];
+    const S* kb = kc + blk * a.kv_stride + head_off;
+    const S* vb = vc + blk * a.kv_stride + head_off;
+    const uint4* kp = reinterpret_cast<const uint4*>(kb + col * D + seg * (D / 4));
+#pragma unroll
+    for (int i = 0; i < NK; ++i) kk[i] = kp[i];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      vv[i] = *reinterpret_cast<const uint4*>(vb + (i * TPI + vrow) * D + vd0);
+    }
+  };
+
+  if (nb > 0) load_block(b0 + w, kr, vr);
+  for (int j = 0; j < nb; ++j) {
+    const int bidx = b0 + w + j * kWaves;
+    uint4 kn[NK], vn[NV];
+    const bool more = j + 1 < nb;
+    if (more) load_block(bidx + kWaves, kn, vn);
+    const int slot = j & 1;
+
+    // S = Q K^T for the 16 tokens of the block: lane holds rows 4*seg+r, column col.
+    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NK; ++i) c = MF::run(qa[i], kr[i], c);
+
+    const int tok0 = bidx * kBS;
+    const bool tail = tok0 + kBS > ctx;
+    const bool valid = tok0 + col < ctx;
+    float pr[4], al[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x = valid ? c[r] * a.scale_log2 : -INFINITY;
+      const float bm = row16_max(x);
+      const float m_new = fmaxf(m_run[r], bm);
+      al[r] = exp2f(m_run[r] - m_new);
+      pr[r] = exp2f(x - m_new);
+      l_run[r] = l_run[r] * al[r] + pr[r];
+      m_run[r] = m_new;
+    }
+    if (seg < HG) {
+      *reinterpret_cast<float4*>(&p_lds[w][slot][col * GP + 4 * seg]) =
+          make_float4(pr[0], pr[1], pr[2], pr[3]);
+      if (col == 0) {
+        *reinterpret_cast<float4*>(&alpha_lds[w][slot][4 * seg]) =
+            make_float4(al[0], al[1], al[2], al[3]);
+      }
+    }
+    wave_lds_sync();
+
+    // O = alpha * O + P V on the VALU.
+    {
+      float alh[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) alh[h] = alpha_lds[w][slot][h];
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] *= alh[h];
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int t = i * TPI + vrow;
+      float vf[8];
+      MF::unpack8(vr[i], vf);
+      if (tail && tok0 + t >= ctx) {
+        // Rows past the context may hold any bit pattern; keep them out of 0*x.
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vf[e] = 0.f;
+      }
+      float ph[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) ph[h] = p_lds[w][slot][t * GP + h];
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] += ph[h] * vf[e];
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < NK; ++i) kr[i] = kn[i];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) vr[i] = vn[i];
+    }
+  }
+
+  // Reduce the TPI token rows of the PV layout (lanes with equal lane % ROWV).
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[h][e];
+#pragma unroll
+      for (int o = ROWV; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+      acc[h][e] = v;
+    }
+  if (vrow == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float4* dst = reinterpret_cast<float4*>(&acc_lds[w][h * D + vd0]);
+      dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+      dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+    }
+  }
+  // Softmax state per head: l summed over the 16 columns of a row.
+  float lsum[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) lsum[r] = row16_sum(l_run[r]);
+  if (seg < HG && col == 0) {
+    *reinterpret_cast<float4*>(&ml_lds[w][0][4 * seg]) =
+        make_float4(m_run[0], m_run[1], m_run[2], m_run[3]);
+    *reinterpret_cast<float4*>(&ml_lds[w][1][4 * seg]) =
+        make_float4(lsum[0], lsum[1], lsum[2], lsum[3]);
+  }
+  __syncthreads();
+
+  // Merge the four waves and write out two consecutive dims per thread.
+  for (int idx = tid; idx < G * D / 2; idx += kThreads) {
+    const int h = idx / (D / 2);
+    const int d = (idx % (D / 2)) * 2;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, ml_lds[ww][0][h]);
+    float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float mw = ml_lds[ww][0][h];
+      const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
+      L += f * ml_lds[ww][1][h];
+      o0 += f * acc_lds[ww][h * D + d];
+      o1 += f * acc_lds[ww][h * D + d + 1];
+    }
+    const int hq = kvh * G + h;
+    if (final_out) {
+      const float inv = L != 0.f ? 1.f / L : 1.f;
+      S* op = static_cast<S*>(a.out) + ((int64_t)s * H + hq) * D + d;
+      const uint32_t packed = (uint32_t)elem<T>::from_f32(o0 * inv) |
+                              ((uint32_t)elem<T>::from_f32(o1 * inv) << 16);
+      *reinterpret_cast<uint32_t*>(op) = packed;
+    } else {
+      const int64_t sh = ((int64_t)s * H + hq) * a.num_partitions + p;
+      *reinterpret_cast<float2*>(a.tmp_out + sh * D + d) = make_float2(o0, o1);
+      if (d == 0) {
+        a.exp_sums[sh] = L;
+        a.max_logits[sh] = M * kLn2;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- merge -----
+
+struct MergeArgs {
+  void* out;
+  const float* exp_sums;
+  const float* max_logits;
+  const float* tmp_out;
+  const int32_t* context_lens;
+  int32_t num_heads;
+  int32_t head_dim;
+  int32_t num_partitions;
+  int32_t partition_size;
+  int32_t skip_single;  // 1: sequences with one partition were written by the partition kernel
+};
+
+template <typename T>
+__global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
+  using E = elem<T>;
+  using S = typename E::storage;
+  const int h = blockIdx.x;
+  const int s = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int D = a.head_dim;
+  const int ctx = max(0, a.context_lens[s]);
+  const int np_s = min(num_parts_for(ctx, a.partition_size), a.num_partitions);
+  if (a.skip_single && np_s <= 1) return;
+  S* op = static_cast<S*>(a.out) + ((int64_t)s * a.num_heads + h) * D;
+  if (np_s == 0) {
+    for (int d = lane; d < D; d += 64) E::store(op, d, 0.f);
+    return;
+  }
+  const int64_t sh = ((int64_t)s * a.num_heads + h) * a.num_partitions;
+  const float* ml = a.max_logits + sh;
+  const float* es = a.exp_sums + sh;
+  float M = -INFINITY;
+  for (int q = lane; q < np_s; q += 64) M = fmaxf(M, ml[q]);
+  M = wave_max(M);
+  float L = 0.f;
+  for (int q = lane; q < np_s; q += 64) L += expf(ml[q] - M) * es[q];
+  L = wave_sum(L);
+  const float inv = L != 0.f ? 1.f / L : 1.f;
+  const float* tp = a.tmp_out + sh * D;
+  for (int d0 = lane * 4; d0 < D; d0 += 256) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int q = 0; q < np_s; ++q) {
+      const float r = expf(ml[q] - M);
+      const float4 v = *reinterpret_cast<const float4*>(tp + (int64_t)q * D + d0);
+      acc.x += r * v.x;
+      acc.y += r * v.y;
+      acc.z += r * v.z;
+      acc.w += r * v.w;
+    }
+    E::store(op, d0 + 0, acc.x * inv);
+    E::store(op, d0 + 1, acc.y * inv);
+    E::store(op, d0 + 2, acc.z * inv);
+    E::store(op, d0 + 3, acc.w * inv);
+  }
+}
+
+// ------------------------------------------------------------ host side -----
+
+// Tokens per partition the v1 entries use when given a workspace.
+constexpr int kV1PartitionTokens = 256;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct Shape {
+  int32_t H, Hkv, D, bs, MB, B;
+};
+
+int check_decode_shape(const char* op, const Shape& sh, int32_t dtype, int64_t kv_stride) {
+  if (dtype_bytes(dtype) == 0) return fail(RG_ERR_NOT_SUPPORTED, "%s: unknown dtype %d", op, dtype);
+  if (sh.D % 4 != 0 || sh.D > RG_MAX_HEAD_DIM || sh.D <= 0) {
+    return fail(RG_ERR_NOT_SUPPORTED,
+                "not supported: PagedAttention - head_dim must be a multiple of 4 and <= %d, "
+                "but got %d", RG_MAX_HEAD_DIM, sh.D);
+  }
+  if (sh.B < 0 || sh.H <= 0 || sh.Hkv <= 0 || sh.bs <= 0 || sh.MB < 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT,
+                "%s: need batch >= 0, max_blocks_per_seq >= 0 and positive heads/block_size", op);
+  }
+  if (sh.H % sh.Hkv != 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: num_heads %d is not a multiple of num_kv_heads %d",
+                op, sh.H, sh.Hkv);
+  }
+  if (kv_stride != 0 && kv_stride < (int64_t)sh.Hkv * sh.bs * sh.D) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: kv_block_stride %lld smaller than a block", op,
+                (long long)kv_stride);
+  }
+  return RG_OK;
+}
+
+template <typename T, int D, int G>
+void launch_mfma(const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((decode_mfma_kernel<T, D, G>), grid, dim3(kThreads), 0, s, a);
+}
+
+template <typename T, int D>
+bool launch_mfma_g(const DecodeArgs& a, int G, dim3 grid, hipStream_t s) {
+  switch (G) {
+    case 1: launch_mfma<T, D, 1>(a, grid, s); return true;
+    case 2: launch_mfma<T, D, 2>(a, grid, s); return true;
+    case 4: launch_mfma<T, D, 4>(a, grid, s); return true;
+    case 8: launch_mfma<T, D, 8>(a, grid, s); return true;
+    case 16: launch_mfma<T, D, 16>(a, grid, s); return true;
+    default: return false;
+  }
+}
+
+bool mfma_applies(const DecodeArgs& a, int32_t dtype) {
+  const int G = a.num_heads / a.num_kv_heads;
+  const int eb = dtype_bytes(dtype);
+  return (dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && a.block_size == kBS &&
+         (a.head_dim == 64 || a.head_dim == 128) &&
+         (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && a.partition_size % kBS == 0 &&
+         aligned16(a.q) && aligned16(a.k_cache) && aligned16(a.v_cache) &&
+         (a.kv_stride * eb) % 16 == 0 &&
+         (a.out == nullptr || (reinterpret_cast<uintptr_t>(a.out) & 3u) == 0);
+}
+
+// Launches the partition kernel over grid (grid_parts, heads, batch).
+int run_partition(const char* op, const DecodeArgs& a, int32_t dtype, int32_t batch,
+                  int32_t grid_parts, hipStream_t s) {
+  if (batch == 0 || grid_parts == 0) return ok();
+  if (mfma_applies(a, dtype)) {
+    const int G = a.num_heads / a.num_kv_heads;
+    const dim3 grid(grid_parts, a.num_kv_heads, batch);
+    if (dtype == RG_DTYPE_BF16) {
+      if (a.head_dim == 128) launch_mfma_g<bf16_t, 128>(a, G, grid, s);
+      else launch_mfma_g<bf16_t, 64>(a, G, grid, s);
+    } else {
+      if (a.head_dim == 128) launch_mfma_g<f16_t, 128>(a, G, grid, s);
+      else launch_mfma_g<f16_t, 64>(a, G, grid, s);
+    }
+    return check_launch(op);
+  }
+  const dim3 grid(grid_parts, a.num_heads, batch);
+  return dispatch_dtype(dtype, [&](auto tag) {
+    hipLaunchKernelGGL(decode_generic_kernel<decltype(tag)>, grid, dim3(64), 0, s, a);
+    return check_launch(op);
+  });
+}
+
+int run_merge(const char* op, const MergeArgs& m, int32_t dtype, int32_t batch, hipStream_t s) {
+  if (batch == 0) return ok();
+  const dim3 grid(m.num_heads, batch);
+  return dispatch_dtype(dtype, [&](auto tag) {
+    hipLaunchKernelGGL(decode_merge_kernel<decltype(tag)>, grid, dim3(64), 0, s, m);
+    return check_launch(op);
+  });
+}
+
+DecodeArgs make_args(const void* q, const void* kc, const void* vc, const int32_t* bt,
+                     const int32_t* cl, void* out, float scale, const Shape& sh,
+                     int64_t kv_stride, int32_t P, int32_t NP, int32_t mode) {
+  DecodeArgs a;
+  a.q = q;
+  a.k_cache = kc;
+  a.v_cache = vc;
+  a.block_table = bt;
+  a.context_lens = cl;
+  a.out = out;
+  a.tmp_out = nullptr;
+  a.exp_sums = nullptr;
+  a.max_logits = nullptr;
+  a.scale_log2 = scale * kLog2e;
+  a.num_heads = sh.H;
+  a.num_kv_heads = sh.Hkv;
+  a.head_dim = sh.D;
+  a.block_size = sh.bs;
+  a.max_blocks = sh.MB;
+  a.num_partitions = NP;
+  a.partition_size = P;
+  a.kv_stride = kv_stride ? kv_stride : (int64_t)sh.Hkv * sh.bs * sh.D;
+  a.mode = mode;
+  return a;
+}
+
+struct V2Scratch {
+  float* tmp_out;
+  float* exp_sums;
+  float* max_logits;
+};
+
+size_t v2_bytes(int64_t B, int64_t H, int64_t NP, int64_t D, V2Scratch* carve, void* base) {
+  const size_t n_stat = (size_t)(B * H * NP);
+  const size_t tmp = align_up(n_stat * (size_t)D * 4, 256);
+  const size_t stat = align_up(n_stat * 4, 256);
+  if (carve) {
+    char* p = static_cast<char*>(base);
+    carve->tmp_out = reinterpret_cast<float*>(p);
+    carve->exp_sums = reinterpret_cast<float*>(p + tmp);
+    carve->max_logits = reinterpret_cast<float*>(p + tmp + stat);
+  }
+  return tmp + 2 * stat;
+}
+
+int32_t v1_num_partitions(const Shape& sh) {
+  const int64_t max_ctx = (int64_t)sh.MB * sh.bs;
+  return (int32_t)ceil_div(max_ctx, kV1PartitionTokens);
+}
+
+// Body shared by the v1 and v1_plus entries.
+int paged_v1(const char* op, const void* q, const void* kc, const void* vc, const int32_t* bt,
+             const int32_t* cl, void* out, float scale, const Shape& sh, int32_t dtype,
+             int64_t kv_stride, void* ws, size_t ws_bytes, void* stream) {
+  int st = check_decode_shape(op, sh, dtype, kv_stride);
+  if (st != RG_OK) return st;
+  if (sh.B == 0) return ok();
+  if (!q || !kc || !vc || !bt || !cl || !out) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
+  }
+  hipStream_t s = as_stream(stream);
+  const int32_t np = v1_num_partitions(sh);
+  if (ws != nullptr && np > 1) {
+    V2Scratch sc;
+    const size_t need = v2_bytes(sh.B, sh.H, np, sh.D, &sc, ws);
+    if (ws_bytes < need) {
+      return fail(RG_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu required", op, ws_bytes, need);
+    }
+    DecodeArgs a = make_args(q, kc, vc, bt, cl, out, scale, sh, kv_stride, kV1PartitionTokens, np,
+                             MODE_AUTO);
+    a.tmp_out = sc.tmp_out;
+    a.exp_sums = sc.exp_sums;
+    a.max_logits = sc.max_logits;
+    st = run_partition(op, a, dtype, sh.B, np, s);
+    if (st != RG_OK) return st;
+    MergeArgs m{out, sc.exp_sums, sc.max_logits, sc.tmp_out, cl, sh.H, sh.D, np,
+                kV1PartitionTokens, 1};
+    return run_merge(op, m, dtype, sh.B, s);
+  }
+  // One partition spans the whole block table.
+  const int32_t P = (int32_t)std::max<int64_t>(16, ceil_div((int64_t)sh.MB * sh.bs, 16) * 16);
+  DecodeArgs a = make_args(q, kc, vc, bt, cl, out, scale, sh, kv_stride, P, 1, MODE_FINAL);
+  return run_partition(op, a, dtype, sh.B, 1, s);
+}
+
+}  // namespace
+
+int probe_decode_kernels() {
+  hipFuncAttributes at;
+  if (hipFuncGetAttributes(&at, reinterpret_cast<const void*>(decode_mfma_kernel<bf16_t, 128, 4>)) !=
+          hipSuccess ||
+      hipFuncGetAttributes(&at, reinterpret_cast<const void*>(decode_generic_kernel<f32_t>)) !=
+          hipSuccess) {
+    return fail(RG_ERR_HIP, "failed to load the decode kernels: %s",
+                hipGetErrorString(hipGetLastError()));
+  }
+  return RG_OK;
+}
+
+}  // namespace rg
+
+using namespace rg;
+
+extern "C" size_t rg_paged_attention_v1_workspace_bytes(int32_t batch_size, int32_t num_heads,
+                                                        int32_t head_dim, int32_t block_size,
+                                                        int32_t max_blocks_per_seq) {
+  if (batch_size <= 0 || num_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+      max_blocks_per_seq <= 0) {
+    return 0;
+  }
+  const Shape sh{num_heads, 1, head_dim, block_size, max_blocks_per_seq, batch_size};
+  const int32_t np = v1_num_partitions(sh);
+  if (np <= 1) return 0;
+  return v2_bytes(batch_size, num_heads, np, head_dim, nullptr, nullptr);
+}
+
+extern "C" int rg_paged_attention_v1(const void* query, const void* key_cache,
+                                     const void* value_cache, const int32_t* block_table,
+                                     const int32_t* context_lens, void* output, float scale,
+                                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t block_size, int32_t max_blocks_per_seq,
+                                     int32_t batch_size, int32_t dtype, int64_t kv_block_stride,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  const Shape sh{num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, batch_size};
+  return paged_v1("paged_attention_v1", query, key_cache, value_cache, block_table, context_lens,
+                  output, scale, sh, dtype, kv_block_stride, workspace, workspace_bytes, stream);
+}
+
+extern "C" int rg_paged_attention_v1_plus(const void* query, const void* key_cache,
+                                          const void* value_cache, const int32_t* block_table,
+                                          const int32_t* context_lens, void* output,
+                                          const float* rotation_metadata, float scale,
+                                          int32_t num_heads, int32_t num_kv_heads,
+                                          int32_t head_dim, int32_t block_size,
+                                          int32_t max_blocks_per_seq, int32_t batch_size,
+                                          int32_t dtype, int64_t kv_block_stride, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  (void)rotation_metadata;  // identity rotation
+  const Shape sh{num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, batch_size};
+  return paged_v1("paged_attention_v1_plus", query, key_cache, value_cache, block_table,
+                  context_lens, output, scale, sh, dtype, kv_block_stride, workspace,
+                  workspace_bytes, stream);
+}
+
+extern "C" size_t rg_v2_workspace_bytes(int32_t batch_size, int32_t num_heads,
+                                        int32_t num_partitions, int32_t head_dim) {
+  if (batch_size <= 0 || num_heads <= 0 || num_partitions <= 0 || head_dim <= 0) return 0;
+  return v2_bytes(batch_size, num_heads, num_partitions, head_dim, nullptr, nullptr);
+}
+
+extern "C" int rg_paged_attention_v2_partition(
+    const void* query, const void* key_cache, const void* value_cache, const int32_t* block_table,
+    const int32_t* context_lens, float* tmp_out, float* exp_sums, float* max_logits,
+    const float* rotation_metadata, float scale, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq, int32_t num_partitions,
+    int32_t batch_size, int32_t partition_size, int32_t dtype, int64_t kv_block_stride,
+    void* stream) {
+  (void)rotation_metadata;
+  const char* op = "paged_attention_v2_partition";
+  const Shape sh{num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, batch_size};
+  int st = check_decode_shape(op, sh, dtype, kv_block_stride);
+  if (st != RG_OK) return st;
+  if (partition_size <= 0 || partition_size % block_size != 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT,
+                "%s: partition_size %d must be a positive multiple of block_size %d", op,
+                partition_size, block_size);
+  }
+  if (num_partitions < 0) return fail(RG_ERR_INVALID_ARGUMENT, "%s: num_partitions < 0", op);
+  if (batch_size == 0 || num_partitions == 0) return ok();
+  if (!query || !key_cache || !value_cache || !block_table || !context_lens || !tmp_out ||
+      !exp_sums || !max_logits) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
+  }
+  DecodeArgs a = make_args(query, key_cache, value_cache, block_table, context_lens, nullptr,
+                           scale, sh, kv_block_stride, partition_size, num_partitions,
+                           MODE_PARTIAL);
+  a.tmp_out = tmp_out;
+  a.exp_sums = exp_sums;
+  a.max_logits = max_logits;
+  return run_partition(op, a, dtype, batch_size, num_partitions, as_stream(stream));
+}
+
+extern "C" int rg_paged_attention_v2_reduce(void* output, const float* exp_sums,
+                                            const float* max_logits, const float* tmp_out,
+                                            const int32_t* context_lens,
+                                            const float* rotation_metadata, int32_t num_heads,
+                                            int32_t head_dim, int32_t num_partitions,
+                                            int32_t batch_size, int32_t partition_size,
+                                            int32_t dtype, void* stream) {
+  (void)rotation_metadata;
+  const char* op = "paged_attention_v2_reduce";
+  if (dtype_bytes(dtype) == 0) return fail(RG_ERR_NOT_SUPPORTED, "%s: unknown dtype %d", op, dtype);
+  if (head_dim > 1024) {
+    // MAX_HEAD_DIM_V2_REDUCE (crates/vllm-cuda/src/kernels/mod.rs:477-482)
+    return fail(RG_ERR_INVALID_ARGUMENT,
+                "head_dim %d exceeds maximum block size 1024 for reduction kernel", head_dim);
+  }
+  if (head_dim <= 0 || head_dim % 4 != 0) {
+    return fail(RG_ERR_NOT_SUPPORTED, "%s: head_dim must be a positive multiple of 4, got %d", op,
+                head_dim);
+  }
+  if (num_heads <= 0 || batch_size < 0 || num_partitions < 0 || partition_size <= 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT,
+                "%s: need num_heads > 0, batch >= 0, num_partitions >= 0, partition_size > 0",
+                op);
+  }
+  if (batch_size == 0) return ok();
+  if (!output || !context_lens || (num_partitions > 0 && (!exp_sums || !max_logits || !tmp_out))) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
+  }
+  MergeArgs m{output, exp_sums, max_logits, tmp_out, context_lens, num_heads, head_dim,
+              num_partitions, partition_size, 0};
+  return run_merge(op, m, dtype, batch_size, as_stream(stream));
+}
+
+extern "C" int rg_paged_attention_v2(const void* query, const void* key_cache,
+                                     const void* value_cache, const int32_t* block_table,
+                                     const int32_t* context_lens, void* output, float scale,
+                                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t block_size, int32_t max_blocks_per_seq,
+                                     int32_t batch_size, int32_t max_context_len,
+                                     int32_t partition_size, int32_t dtype,
+                                     int64_t kv_block_stride, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  const char* op = "paged_attention_v2";
+  const Shape sh{num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, batch_size};
+  int st = check_decode_shape(op, sh, dtype, kv_block_stride);
+  if (st != RG_OK) return st;
+  if (partition_size <= 0 || partition_size % block_size != 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT,
+                "%s: partition_size %d must be a positive multiple of block_size %d", op,
+                partition_size, block_size);
+  }
+  if (max_context_len < 0) return fail(RG_ERR_INVALID_ARGUMENT, "%s: max_context_len < 0", op);
+  if (batch_size == 0) return ok();
+  if (!query || !key_cache || !value_cache || !block_table || !context_lens || !output) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
+  }
+  const int32_t np = (int32_t)std::max<int64_t>(1, ceil_div(max_context_len, partition_size));
+  V2Scratch sc;
+  const size_t need = v2_bytes(batch_size, num_heads, np, head_dim, &sc, workspace);
+  if (workspace == nullptr || workspace_bytes < need) {
+    return fail(RG_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu required", op,
+                workspace ? workspace_bytes : (size_t)0, need);
+  }
+  hipStream_t s = as_stream(stream);
+  DecodeArgs a = make_args(query, key_cache, value_cache, block_table, context_lens, output, scale,
+                           sh, kv_block_stride, partition_size, np, MODE_AUTO);
+  a.tmp_out = sc.tmp_out;
+  a.exp_sums = sc.exp_sums;
+  a.max_logits = sc.max_logits;
+  st = run_partition(op, a, dtype, batch_size, np, s);
+  if (st != RG_OK) return st;
+  MergeArgs m{output, sc.exp_sums, sc.max_logits, sc.tmp_out, context_lens, num_heads, head_dim,
+              np, partition_size, 1};
+  return run_merge(op, m, dtype, batch_size, s);
+}

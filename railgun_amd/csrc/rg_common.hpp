@@ -1,0 +1,136 @@
+// Shared device/host helpers for the gfx950 kernels of the attention hot path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "railgun_hip.h"
+
+namespace rg {
+
+// ---------------------------------------------------------------- status ----
+
+// Records `msg` (printf-style) as this thread's last error and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Clears the thread's last error and returns RG_OK.
+int ok();
+
+// Converts a launch's hipError_t (hipGetLastError) into a status code.
+int check_launch(const char* what);
+
+// ------------------------------------------------------------ element types --
+
+// Storage types: fp32, bf16 and fp16 are all handled as their bit patterns.
+struct f32_t { using storage = float; };
+struct bf16_t { using storage = uint16_t; };
+struct f16_t { using storage = uint16_t; };
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t bits) {
+  _Float16 h = __builtin_bit_cast(_Float16, bits);
+  return (float)h;
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;  // v_cvt_f16_f32: round to nearest even
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+template <typename T> struct elem;
+template <> struct elem<f32_t> {
+  using storage = float;
+  static constexpr int bytes = 4;
+  __device__ static __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+  __device__ static __forceinline__ void store(float* p, int64_t i, float v) { p[i] = v; }
+  __device__ static __forceinline__ float to_f32(float v) { return v; }
+  __device__ static __forceinline__ float from_f32(float v) { return v; }
+};
+template <> struct elem<bf16_t> {
+  using storage = uint16_t;
+  static constexpr int bytes = 2;
+  __device__ static __forceinline__ float load(const uint16_t* p, int64_t i) {
+    return bf16_bits_to_f32(p[i]);
+  }
+  __device__ static __forceinline__ void store(uint16_t* p, int64_t i, float v) {
+    p[i] = f32_to_bf16_bits(v);
+  }
+  __device__ static __forceinline__ float to_f32(uint16_t v) { return bf16_bits_to_f32(v); }
+  __device__ static __forceinline__ uint16_t from_f32(float v) { return f32_to_bf16_bits(v); }
+};
+template <> struct elem<f16_t> {
+  using storage = uint16_t;
+  static constexpr int bytes = 2;
+  __device__ static __forceinline__ float load(const uint16_t* p, int64_t i) {
+    return f16_bits_to_f32(p[i]);
+  }
+  __device__ static __forceinline__ void store(uint16_t* p, int64_t i, float v) {
+    p[i] = f32_to_f16_bits(v);
+  }
+  __device__ static __forceinline__ float to_f32(uint16_t v) { return f16_bits_to_f32(v); }
+  __device__ static __forceinline__ uint16_t from_f32(float v) { return f32_to_f16_bits(v); }
+};
+
+inline int dtype_bytes(int32_t dtype) {
+  switch (dtype) {
+    case RG_DTYPE_F32: return 4;
+    case RG_DTYPE_BF16: return 2;
+    case RG_DTYPE_F16: return 2;
+    default: return 0;
+  }
+}
+
+inline const char* dtype_name(int32_t dtype) {
+  switch (dtype) {
+    case RG_DTYPE_F32: return "f32";
+    case RG_DTYPE_BF16: return "bf16";
+    case RG_DTYPE_F16: return "f16";
+    default: return "?";
+  }
+}
+
+// Calls f(tag) with tag = f32_t / bf16_t / f16_t for the runtime dtype.
+template <typename F>
+inline int dispatch_dtype(int32_t dtype, F&& f) {
+  switch (dtype) {
+    case RG_DTYPE_F32: return f(f32_t{});
+    case RG_DTYPE_BF16: return f(bf16_t{});
+    case RG_DTYPE_F16: return f(f16_t{});
+    default: return fail(RG_ERR_NOT_SUPPORTED, "unknown dtype code %d", (int)dtype);
+  }
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// ------------------------------------------------------- wave-level helpers --
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+}  // namespace rg

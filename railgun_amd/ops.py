@@ -1,0 +1,318 @@
+"""Host-side mirror of Railgun's kernel launchers and custom op over the C ABI.
+
+``PagedAttentionKernels`` mirrors ``crates/vllm-cuda/src/kernels/mod.rs:23-509`` (one
+``launch_*`` method per launcher, same argument order and meaning) and
+``PagedAttentionOp`` mirrors ``crates/vllm-cuda/src/kernels/paged_attn_op.rs:12-269``
+(``execute`` with the v1/v2 dispatch rule, ``reshape_and_cache``, ``apply_rope``).  Device
+buffers are torch tensors (PyTorch only supplies device memory and the current stream);
+every launch goes through ``librailgun_hip.so``.  Errors surface as
+:class:`railgun_amd.RailgunError` carrying the library's message, in the places the
+reference returns ``CoreError`` / ``candle_core::Error::Msg``.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import RailgunError, check, load_library
+
+_DTYPES = {torch.float32: _lib.RG_DTYPE_F32, torch.bfloat16: _lib.RG_DTYPE_BF16, torch.float16: _lib.RG_DTYPE_F16}
+
+# Dispatch threshold of PagedAttentionOp::execute (paged_attn_op.rs:89).
+V1_MAX_CONTEXT = 4096
+# Tokens per partition execute() uses for its v2 branch (the reference fixes 256,
+# paged_attention_utils.cuh:10; any multiple of block_size gives the same result).
+V2_PARTITION_SIZE = 512
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise RailgunError(_lib.RG_ERR_NOT_SUPPORTED, f"dtype {t.dtype} is not supported") from None
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_cuda(*tensors: Optional[torch.Tensor]) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "PagedAttentionOp requires GPU tensors")
+
+
+def _require_i32(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise RailgunError(
+                _lib.RG_ERR_INVALID_ARGUMENT,
+                f"index tensors must be contiguous int32 (block ids are read as i32), got {t.dtype}",
+            )
+
+
+def cache_geometry(k_cache: torch.Tensor, v_cache: torch.Tensor) -> tuple[int, int, int, int]:
+    """(num_kv_heads, block_size, head_dim, kv_block_stride) of a [NB, H_kv, bs, D] cache view.
+
+    Accepts Railgun's fused pool views ``storage[:, 0]`` / ``storage[:, 1]`` of a
+    ``[NB, 2, H_kv, bs, D]`` tensor (crates/vllm-paged-attention/src/block.rs:70,89-95): each
+    block's rows must be contiguous and both caches must share the block stride.
+    """
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT,
+                           f"caches must be [num_blocks, num_kv_heads, block_size, head_dim], got "
+                           f"{tuple(k_cache.shape)} and {tuple(v_cache.shape)}")
+    _, hkv, bs, d = k_cache.shape
+    for c in (k_cache, v_cache):
+        if c.stride(3) != 1 or c.stride(2) != d or c.stride(1) != bs * d:
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "cache blocks must be contiguous [H_kv, bs, D]")
+    if k_cache.stride(0) != v_cache.stride(0) or k_cache.dtype != v_cache.dtype:
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "k and v caches must share dtype and block stride")
+    return int(hkv), int(bs), int(d), int(k_cache.stride(0))
+
+
+def rope_cos_sin_table(max_position: int, head_dim: int, theta: float,
+                       device: Optional[torch.device] = None) -> torch.Tensor:
+    """fp32 [max_position, head_dim] table: cos in [:, :D/2], sin in [:, D/2:] (HF Llama)."""
+    lib = load_library()
+    table = np.empty((max_position, head_dim), dtype=np.float32)
+    check(lib.rg_rope_cos_sin_table(table.ctypes.data_as(_lib.f32p), max_position, head_dim, float(theta)))
+    t = torch.from_numpy(table)
+    return t.to(device) if device is not None else t
+
+
+class PagedAttentionKernels:
+    """Launchers of the attention hot path (crates/vllm-cuda/src/kernels/mod.rs:23-509).
+
+    Construction checks the device (``PagedAttentionKernels::new``, mod.rs:57-190).  Every
+    ``launch_*`` is asynchronous on the current torch stream of the tensors' device; none
+    allocates.  The KV block stride is taken from ``key_cache.stride(0)``.
+    """
+
+    def __init__(self, device: int | torch.device = 0):
+        self.lib = load_library()
+        ordinal = device.index if isinstance(device, torch.device) else int(device)
+        self.ordinal = 0 if ordinal is None else ordinal
+        check(self.lib.rg_init(self.ordinal))
+
+    # mod.rs:196-225
+    def launch_rope(self, x, cos_sin, positions, num_heads: int, head_dim: int, num_tokens: int) -> None:
+        _require_cuda(x, cos_sin, positions)
+        _require_i32(positions)
+        check(self.lib.rg_rope(x.data_ptr(), cos_sin.data_ptr(), positions.data_ptr(), num_heads, head_dim,
+                               num_tokens, dtype_code(x), _stream(x)))
+
+    # mod.rs:227-262
+    def launch_reshape_and_cache(self, k, v, k_cache, v_cache, slot_mapping, num_kv_heads: int,
+                                 head_dim: int, block_size: int, batch_size: int) -> None:
+        _require_cuda(k, v, k_cache, v_cache, slot_mapping)
+        _require_i32(slot_mapping)
+        check(self.lib.rg_reshape_and_cache(k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                            slot_mapping.data_ptr(), num_kv_heads, head_dim, block_size,
+                                            batch_size, dtype_code(k), k_cache.stride(0), _stream(k)))
+
+    # mod.rs:264-303
+    def launch_reshape_and_cache_isoquant(self, k, v, k_cache, v_cache, slot_mapping, rotation_metadata,
+                                          num_kv_heads: int, head_dim: int, block_size: int,
+                                          batch_size: int) -> None:
+        _require_cuda(k, v, k_cache, v_cache, slot_mapping, rotation_metadata)
+        _require_i32(slot_mapping)
+        check(self.lib.rg_reshape_and_cache_isoquant(
+            k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(),
+            rotation_metadata.data_ptr(), num_kv_heads, head_dim, block_size, batch_size, dtype_code(k),
+            k_cache.stride(0), _stream(k)))
+
+    def v1_workspace_bytes(self, batch_size: int, num_heads: int, head_dim: int, block_size: int,
+                           max_blocks_per_seq: int) -> int:
+        return int(self.lib.rg_paged_attention_v1_workspace_bytes(batch_size, num_heads, head_dim, block_size,
+                                                                  max_blocks_per_seq))
+
+    # mod.rs:305-348 (+ optional workspace: the split-K form of the same computation)
+    def launch_v1(self, query, key_cache, value_cache, block_table, context_lens, output, scale: float,
+                  num_heads: int, num_kv_heads: int, head_dim: int, block_size: int, max_blocks_per_seq: int,
+                  batch_size: int, workspace: Optional[torch.Tensor] = None) -> None:
+        _require_cuda(query, key_cache, value_cache, block_table, context_lens, output, workspace)
+        _require_i32(block_table, context_lens)
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        check(self.lib.rg_paged_attention_v1(
+            query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
+            context_lens.data_ptr(), output.data_ptr(), float(scale), num_heads, num_kv_heads, head_dim,
+            block_size, max_blocks_per_seq, batch_size, dtype_code(query), key_cache.stride(0),
+            _ptr(workspace), ws_bytes, _stream(query)))
+
+    # mod.rs:350-399
+    def launch_v1_plus(self, query, key_cache, value_cache, block_table, context_lens, output,
+                       rotation_metadata, scale: float, num_heads: int, num_kv_heads: int, head_dim: int,
+                       block_size: int, max_blocks_per_seq: int, batch_size: int,
+                       workspace: Optional[torch.Tensor] = None) -> None:
+        _require_cuda(query, key_cache, value_cache, block_table, context_lens, output, workspace)
+        _require_i32(block_table, context_lens)
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        check(self.lib.rg_paged_attention_v1_plus(
+            query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
+            context_lens.data_ptr(), output.data_ptr(), _ptr(rotation_metadata), float(scale), num_heads,
+            num_kv_heads, head_dim, block_size, max_blocks_per_seq, batch_size, dtype_code(query),
+            key_cache.stride(0), _ptr(workspace), ws_bytes, _stream(query)))
+
+    # mod.rs:401-456
+    def launch_v2_partition(self, query, key_cache, value_cache, block_table, context_lens, tmp_out, exp_sums,
+                            max_logits, rotation_metadata, scale: float, num_heads: int, num_kv_heads: int,
+                            head_dim: int, block_size: int, max_blocks_per_seq: int, num_partitions: int,
+                            batch_size: int, partition_size: int = 256) -> None:
+        _require_cuda(query, key_cache, value_cache, block_table, context_lens, tmp_out, exp_sums, max_logits)
+        _require_i32(block_table, context_lens)
+        check(self.lib.rg_paged_attention_v2_partition(
+            query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
+            context_lens.data_ptr(), tmp_out.data_ptr(), exp_sums.data_ptr(), max_logits.data_ptr(),
+            _ptr(rotation_metadata), float(scale), num_heads, num_kv_heads, head_dim, block_size,
+            max_blocks_per_seq, num_partitions, batch_size, partition_size, dtype_code(query),
+            key_cache.stride(0), _stream(query)))
+
+    # mod.rs:458-508
+    def launch_v2_reduce(self, output, exp_sums, max_logits, tmp_out, context_lens, rotation_metadata,
+                         num_heads: int, head_dim: int, num_partitions: int, batch_size: int,
+                         partition_size: int = 256) -> None:
+        _require_cuda(output, exp_sums, max_logits, tmp_out, context_lens)
+        _require_i32(context_lens)
+        check(self.lib.rg_paged_attention_v2_reduce(
+            output.data_ptr(), exp_sums.data_ptr(), max_logits.data_ptr(), tmp_out.data_ptr(),
+            context_lens.data_ptr(), _ptr(rotation_metadata), num_heads, head_dim, num_partitions, batch_size,
+            partition_size, dtype_code(output), _stream(output)))
+
+    def launch_v2(self, query, key_cache, value_cache, block_table, context_lens, output, scale: float,
+                  num_heads: int, num_kv_heads: int, head_dim: int, block_size: int, max_blocks_per_seq: int,
+                  batch_size: int, max_context_len: int, partition_size: int, workspace: torch.Tensor) -> None:
+        """v2 partition + reduce in one call, scratch carved from ``workspace``."""
+        _require_cuda(query, key_cache, value_cache, block_table, context_lens, output, workspace)
+        _require_i32(block_table, context_lens)
+        check(self.lib.rg_paged_attention_v2(
+            query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
+            context_lens.data_ptr(), output.data_ptr(), float(scale), num_heads, num_kv_heads, head_dim,
+            block_size, max_blocks_per_seq, batch_size, max_context_len, partition_size, dtype_code(query),
+            key_cache.stride(0), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+            _stream(query)))
+
+    def v2_workspace_bytes(self, batch_size: int, num_heads: int, num_partitions: int, head_dim: int) -> int:
+        return int(self.lib.rg_v2_workspace_bytes(batch_size, num_heads, num_partitions, head_dim))
+
+    # New entries (no reference launcher): fused RoPE + cache write, packed causal prefill.
+    def launch_rope_reshape_and_cache(self, q, k, v, k_cache, v_cache, cos_sin, positions, slot_mapping,
+                                      num_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
+                                      num_tokens: int) -> None:
+        _require_cuda(q, k, v, k_cache, v_cache, cos_sin, positions, slot_mapping)
+        _require_i32(positions, slot_mapping)
+        check(self.lib.rg_rope_reshape_and_cache(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cos_sin.data_ptr(),
+            positions.data_ptr(), slot_mapping.data_ptr(), num_heads, num_kv_heads, head_dim, block_size,
+            num_tokens, dtype_code(q), k_cache.stride(0), _stream(q)))
+
+    def launch_prefill_packed(self, query, key_cache, value_cache, block_table, context_lens, cu_seqlens,
+                              output, scale: float, num_heads: int, num_kv_heads: int, head_dim: int,
+                              block_size: int, max_blocks_per_seq: int, num_seqs: int, num_tokens: int,
+                              max_query_len: int) -> None:
+        _require_cuda(query, key_cache, value_cache, block_table, context_lens, cu_seqlens, output)
+        _require_i32(block_table, context_lens, cu_seqlens)
+        check(self.lib.rg_prefill_packed(
+            query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
+            context_lens.data_ptr(), cu_seqlens.data_ptr(), output.data_ptr(), float(scale), num_heads,
+            num_kv_heads, head_dim, block_size, max_blocks_per_seq, num_seqs, num_tokens, max_query_len,
+            dtype_code(query), key_cache.stride(0), _stream(query)))
+
+
+@dataclass
+class PagedAttentionOp:
+    """The custom op (crates/vllm-cuda/src/kernels/paged_attn_op.rs:12-19)."""
+
+    scale: float
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    block_size: int
+    kernels: PagedAttentionKernels = field(repr=False)
+
+    def execute(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                block_table: torch.Tensor, context_lens: torch.Tensor,
+                rotation_metadata: Optional[torch.Tensor], max_context_len: int) -> torch.Tensor:
+        """paged_attn_op.rs:45-166: q [B, H, D] -> new output [B, H, D].
+
+        ``max_context_len <= 4096`` runs v1 (single pass per partition group), longer runs
+        v2 split-K; both compute the same softmax attention.
+        """
+        if self.head_dim % 4 != 0:
+            raise RailgunError(_lib.RG_ERR_NOT_SUPPORTED,
+                               f"Head dimension ({self.head_dim}) must be a multiple of 4 for IsoQuant.")
+        if q.dim() != 3:
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, f"q must be [batch, heads, head_dim], got {tuple(q.shape)}")
+        _require_cuda(q, k_cache, v_cache, block_table, context_lens)
+        batch, num_heads, head_dim = (int(x) for x in q.shape)
+        num_kv_heads, block_size, _, _ = cache_geometry(k_cache, v_cache)
+        if num_kv_heads != self.num_kv_heads:
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT,
+                               f"cache has {num_kv_heads} kv heads, op expects {self.num_kv_heads}")
+        max_blocks = int(block_table.shape[1])
+        out = torch.zeros_like(q)
+        k = self.kernels
+        if max_context_len <= V1_MAX_CONTEXT:
+            ws_bytes = k.v1_workspace_bytes(batch, num_heads, head_dim, block_size, max_blocks)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+            k.launch_v1_plus(q, k_cache, v_cache, block_table, context_lens, out, rotation_metadata, self.scale,
+                             num_heads, self.num_kv_heads, head_dim, block_size, max_blocks, batch, workspace=ws)
+        else:
+            num_parts = math.ceil(max_context_len / V2_PARTITION_SIZE)
+            ws = torch.empty(k.v2_workspace_bytes(batch, num_heads, num_parts, head_dim), dtype=torch.uint8,
+                             device=q.device)
+            k.launch_v2(q, k_cache, v_cache, block_table, context_lens, out, self.scale, num_heads,
+                        self.num_kv_heads, head_dim, block_size, max_blocks, batch, max_context_len,
+                        V2_PARTITION_SIZE, ws)
+        return out
+
+    def reshape_and_cache(self, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                          slot_mapping: torch.Tensor, rotation_metadata: Optional[torch.Tensor],
+                          use_isoquant: bool) -> None:
+        """paged_attn_op.rs:168-233: k, v [T, H_kv, D] written into the caches in place."""
+        batch, num_kv_heads, head_dim = (int(x) for x in k.shape)
+        if use_isoquant:
+            self.kernels.launch_reshape_and_cache_isoquant(k, v, k_cache, v_cache, slot_mapping, rotation_metadata,
+                                                           num_kv_heads, head_dim, self.block_size, batch)
+        else:
+            self.kernels.launch_reshape_and_cache(k, v, k_cache, v_cache, slot_mapping, num_kv_heads, head_dim,
+                                                  self.block_size, batch)
+
+    def apply_rope(self, x: torch.Tensor, cos_sin: torch.Tensor, positions: torch.Tensor) -> None:
+        """paged_attn_op.rs:236-268: in-place RoPE on x [T, H, D]."""
+        num_tokens, num_heads, head_dim = (int(d) for d in x.shape)
+        self.kernels.launch_rope(x, cos_sin, positions, num_heads, head_dim, num_tokens)
+
+    def rope_reshape_and_cache(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                               v_cache: torch.Tensor, cos_sin: torch.Tensor, positions: torch.Tensor,
+                               slot_mapping: torch.Tensor) -> None:
+        """RoPE on q (in place) and k, then the cache write, in one pass over the new tokens."""
+        num_tokens = int(q.shape[0])
+        self.kernels.launch_rope_reshape_and_cache(q, k, v, k_cache, v_cache, cos_sin, positions, slot_mapping,
+                                                   self.num_heads, self.num_kv_heads, self.head_dim,
+                                                   self.block_size, num_tokens)
+
+    def prefill_packed(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       block_table: torch.Tensor, context_lens: torch.Tensor, cu_seqlens: torch.Tensor,
+                       max_query_len: int) -> torch.Tensor:
+        """Causal attention of the packed new tokens q [T, H, D] over the paged cache."""
+        num_tokens = int(q.shape[0])
+        out = torch.empty_like(q)
+        self.kernels.launch_prefill_packed(q, k_cache, v_cache, block_table, context_lens, cu_seqlens, out,
+                                           self.scale, self.num_heads, self.num_kv_heads, self.head_dim,
+                                           self.block_size, int(block_table.shape[1]), int(cu_seqlens.numel()) - 1,
+                                           num_tokens, max_query_len)
+        return out
+
+
+__all__ = ["PagedAttentionKernels", "PagedAttentionOp", "RailgunError", "cache_geometry", "dtype_code",
+           "rope_cos_sin_table", "V1_MAX_CONTEXT", "V2_PARTITION_SIZE"]

@@ -1,0 +1,213 @@
+"""Paged decode attention (v1, v1_plus, v2) on the GPU against the CPU oracle.
+
+The oracle restates crates/vllm-cuda/src/kernels/paged_attention.cu:33-107 (v1),
+paged_attention_v1_plus.cu:37-105 and paged_attention_v2_{partition,reduce}.cu; inputs are
+seeded, bf16/f16 inputs are rounded once and the oracle sees the same bits.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close, dev_f32, from_dev, i32, normal, to_dev
+from oracle import oracle as orc
+from railgun_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+def make_inputs(device, ctx, dt, H=32, Hkv=8, D=128, bs=16, seed=0, extra_blocks=3, fused=False, mb=None):
+    rng = np.random.default_rng(seed)
+    ctx = np.asarray(ctx, np.int32)
+    need = int(sum((int(c) + bs - 1) // bs for c in ctx))
+    nb = need + extra_blocks
+    mb = mb or max(1, max((int(c) + bs - 1) // bs for c in ctx))
+    bt = wl.assign_blocks(ctx, bs, nb, mb, rng)
+    q = normal(rng, (len(ctx), H, D), dt)
+    if fused:
+        pool = normal(rng, (nb, 2, Hkv, bs, D), dt)
+        kc, vc = pool[:, 0], pool[:, 1]
+        dpool = to_dev(pool, dt, device)
+        dkc, dvc = dpool[:, 0], dpool[:, 1]
+    else:
+        kc = normal(rng, (nb, Hkv, bs, D), dt)
+        vc = normal(rng, (nb, Hkv, bs, D), dt)
+        dkc, dvc = to_dev(kc, dt, device), to_dev(vc, dt, device)
+    return dict(ctx=ctx, bt=bt, q=q, kc=kc, vc=vc, H=H, Hkv=Hkv, D=D, bs=bs, mb=mb, dt=dt,
+                scale=1.0 / math.sqrt(D), dq=to_dev(q, dt, device), dkc=dkc, dvc=dvc,
+                dbt=i32(bt, device), dctx=i32(ctx, device))
+
+
+def oracle_v1_plus(inp):
+    return orc.paged_attention_v1_plus(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"],
+                                       inp["dt"])
+
+
+def gpu_v1(kernels, inp, workspace: bool, entry: str = "v1"):
+    B = len(inp["ctx"])
+    out = torch.full_like(inp["dq"], float("nan"))
+    ws = None
+    if workspace:
+        nbytes = kernels.v1_workspace_bytes(B, inp["H"], inp["D"], inp["bs"], inp["mb"])
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=inp["dq"].device)
+    args = (inp["dq"], inp["dkc"], inp["dvc"], inp["dbt"], inp["dctx"], out)
+    tail = (inp["scale"], inp["H"], inp["Hkv"], inp["D"], inp["bs"], inp["mb"], B)
+    if entry == "v1":
+        kernels.launch_v1(*args, *tail, workspace=ws)
+    else:
+        kernels.launch_v1_plus(*args, None, *tail, workspace=ws)
+    torch.cuda.synchronize()
+    return dev_f32(out)
+
+
+def gpu_v2(kernels, inp, P):
+    B = len(inp["ctx"])
+    out = torch.full_like(inp["dq"], float("nan"))
+    max_ctx = int(inp["ctx"].max())
+    np_ = max(1, math.ceil(max_ctx / P))
+    ws = torch.empty(kernels.v2_workspace_bytes(B, inp["H"], np_, inp["D"]), dtype=torch.uint8,
+                     device=inp["dq"].device)
+    kernels.launch_v2(inp["dq"], inp["dkc"], inp["dvc"], inp["dbt"], inp["dctx"], out, inp["scale"], inp["H"],
+                      inp["Hkv"], inp["D"], inp["bs"], inp["mb"], B, max_ctx, P, ws)
+    torch.cuda.synchronize()
+    return dev_f32(out)
+
+
+def test_config1_fp32_all_entries(device, kernels):
+    """Config 1 (fp32, ctx 17/64/130/255, 32/8 heads, D 64): every decode entry at 1e-4."""
+    w = wl.config1()
+    rng = np.random.default_rng(w.seed)
+    inp = make_inputs(device, w.context_lens, "f32", H=32, Hkv=8, D=64, seed=w.seed)
+    # The config's own table (256-block pool, seeded permutation) replaces the helper's.
+    inp["kc"] = normal(rng, (w.num_blocks, 8, 16, 64), "f32")
+    inp["vc"] = normal(rng, (w.num_blocks, 8, 16, 64), "f32")
+    inp["bt"], inp["mb"] = w.block_table, w.max_blocks
+    inp["dkc"], inp["dvc"] = to_dev(inp["kc"], "f32", device), to_dev(inp["vc"], "f32", device)
+    inp["dbt"] = i32(w.block_table, device)
+    want_v1 = orc.paged_attention_v1(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"], "f32")
+    want = oracle_v1_plus(inp)
+    np.testing.assert_allclose(want_v1, want, atol=1e-5, rtol=1e-5)
+    for ws in (False, True):
+        for entry in ("v1", "v1_plus"):
+            assert_close(gpu_v1(kernels, inp, ws, entry), want, "f32", f"{entry} ws={ws}")
+    for P in (16, 64, 256):
+        assert_close(gpu_v2(kernels, inp, P), want, "f32", f"v2 P={P}")
+
+
+CTX_RAGGED = [1, 15, 16, 17, 33, 300, 0, 511, 1024]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
+def test_mfma_path_shapes(device, kernels, dt, D, G):
+    """MFMA kernel (bf16/f16, block 16): every GQA ratio, ragged contexts incl. 0 and 1."""
+    Hkv = 2
+    inp = make_inputs(device, CTX_RAGGED, dt, H=Hkv * G, Hkv=Hkv, D=D, seed=10 * G + D)
+    want = oracle_v1_plus(inp)
+    for ws in (False, True):
+        assert_close(gpu_v1(kernels, inp, ws), want, dt, f"ws={ws}")
+    assert_close(gpu_v2(kernels, inp, 32), want, dt, "v2 P=32")
+
+
+@pytest.mark.parametrize("dt,D,bs,G", [("f32", 128, 16, 4), ("bf16", 96, 16, 4), ("bf16", 256, 16, 2),
+                                       ("f16", 32, 8, 3), ("bf16", 128, 32, 4), ("f32", 256, 8, 1)])
+def test_generic_path_shapes(device, kernels, dt, D, bs, G):
+    """Shapes outside the MFMA kernel (fp32, head_dim 32/96/256, block 8/32, GQA 3)."""
+    inp = make_inputs(device, [1, 7, 40, 129, 0], dt, H=2 * G, Hkv=2, D=D, bs=bs, seed=D + bs + G)
+    want = oracle_v1_plus(inp)
+    for ws in (False, True):
+        assert_close(gpu_v1(kernels, inp, ws), want, dt, f"ws={ws}")
+    assert_close(gpu_v2(kernels, inp, 2 * bs), want, dt, "v2")
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_fused_pool_layout(device, kernels, dt):
+    """Railgun's fused [NB, 2, H_kv, bs, D] pool via kv_block_stride (block.rs:70,89-95)."""
+    inp = make_inputs(device, [5, 70, 333], dt, seed=7, fused=True)
+    want = oracle_v1_plus(inp)
+    assert inp["dkc"].stride(0) == 2 * 8 * 16 * 128
+    assert_close(gpu_v1(kernels, inp, True), want, dt)
+    assert_close(gpu_v2(kernels, inp, 64), want, dt)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_tail_rows_never_leak(device, kernels, dt):
+    """NaN in the unused rows of each sequence's last block must not reach the output."""
+    inp = make_inputs(device, [3, 17, 250], dt, seed=11)
+    clean = gpu_v1(kernels, inp, True)
+    nan_bits = {"f32": np.float32(np.nan), "bf16": np.uint16(0x7FC0)}[dt]
+    for s, c in enumerate(inp["ctx"]):
+        c = int(c)
+        if c % inp["bs"]:
+            blk = int(inp["bt"][s, c // inp["bs"]])
+            inp["kc"][blk, :, c % inp["bs"]:] = nan_bits
+            inp["vc"][blk, :, c % inp["bs"]:] = nan_bits
+    inp["dkc"], inp["dvc"] = to_dev(inp["kc"], dt, device), to_dev(inp["vc"], dt, device)
+    for ws in (False, True):
+        got = gpu_v1(kernels, inp, ws)
+        assert np.isfinite(got).all()
+        np.testing.assert_array_equal(got, clean) if ws else assert_close(got, clean, dt)
+    assert np.isfinite(gpu_v2(kernels, inp, 32)).all()
+
+
+def test_v2_partition_contract(device, kernels):
+    """tmp_out / exp_sums / max_logits of v2_partition (fp32, P=256) against the oracle's."""
+    inp = make_inputs(device, [100, 256, 257, 700, 0], "f32", H=8, Hkv=2, D=64, seed=5)
+    P, NP = 256, 3
+    B = len(inp["ctx"])
+    tmp, es, ml = orc.paged_attention_v2_partition(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"],
+                                                   inp["scale"], "f32", NP, P)
+    d_tmp = torch.zeros((B, 8, NP, 64), dtype=torch.float32, device=device)
+    d_es = torch.zeros((B, 8, NP), dtype=torch.float32, device=device)
+    d_ml = torch.zeros((B, 8, NP), dtype=torch.float32, device=device)
+    kernels.launch_v2_partition(inp["dq"], inp["dkc"], inp["dvc"], inp["dbt"], inp["dctx"], d_tmp, d_es, d_ml,
+                                None, inp["scale"], 8, 2, 64, 16, inp["mb"], NP, B, P)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(dev_f32(d_ml), ml, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(dev_f32(d_es), es, atol=1e-4, rtol=1e-4)
+    np.testing.assert_allclose(dev_f32(d_tmp), tmp, atol=1e-4, rtol=1e-4)
+    out = torch.zeros((B, 8, 64), dtype=torch.float32, device=device)
+    kernels.launch_v2_reduce(out, d_es, d_ml, d_tmp, inp["dctx"], None, 8, 64, NP, B, P)
+    torch.cuda.synchronize()
+    assert_close(dev_f32(out), oracle_v1_plus(inp), "f32")
+
+
+def _config_pool(w, device, seed_offset=0):
+    rng = np.random.default_rng(w.seed + seed_offset)
+    shape = (w.num_blocks, w.num_kv_heads, w.block_size, w.head_dim)
+    kc, vc = normal(rng, shape, w.dtype), normal(rng, shape, w.dtype)
+    q = normal(rng, (w.batch, w.num_heads, w.head_dim), w.dtype)
+    return q, kc, vc
+
+
+def test_config2_full_decode(device, kernels):
+    """Config 2 at full size (B=64, ctx U[512,4096], bf16, D=128, 32/8): v1 vs oracle."""
+    w = wl.config2()
+    q, kc, vc = _config_pool(w, device)
+    inp = dict(ctx=w.context_lens, bt=w.block_table, q=q, kc=kc, vc=vc, H=w.num_heads, Hkv=w.num_kv_heads,
+               D=w.head_dim, bs=w.block_size, mb=w.max_blocks, dt=w.dtype, scale=w.scale,
+               dq=to_dev(q, w.dtype, device), dkc=to_dev(kc, w.dtype, device), dvc=to_dev(vc, w.dtype, device),
+               dbt=i32(w.block_table, device), dctx=i32(w.context_lens, device))
+    want = orc.cpu_attention_gathered(q, kc, vc, w.block_table, w.context_lens, w.scale, w.dtype, nthreads=8)
+    assert_close(gpu_v1(kernels, inp, True), want, "bf16", "v1 split")
+    assert_close(gpu_v1(kernels, inp, False), want, "bf16", "v1 single")
+    assert_close(gpu_v2(kernels, inp, 512), want, "bf16", "v2 P=512")
+
+
+def test_config3_v2_matches_v1(device, kernels):
+    """Config 3 (B=8 x 32768, P=512): v2 == v1 within tolerance; both against the oracle."""
+    w = wl.config3()
+    q, kc, vc = _config_pool(w, device)
+    inp = dict(ctx=w.context_lens, bt=w.block_table, q=q, kc=kc, vc=vc, H=w.num_heads, Hkv=w.num_kv_heads,
+               D=w.head_dim, bs=w.block_size, mb=w.max_blocks, dt=w.dtype, scale=w.scale,
+               dq=to_dev(q, w.dtype, device), dkc=to_dev(kc, w.dtype, device), dvc=to_dev(vc, w.dtype, device),
+               dbt=i32(w.block_table, device), dctx=i32(w.context_lens, device))
+    v2 = gpu_v2(kernels, inp, w.partition_size)
+    v1 = gpu_v1(kernels, inp, True)
+    assert_close(v2, v1, "bf16", "v2 vs v1")
+    want = orc.cpu_attention_gathered(q, kc, vc, w.block_table, w.context_lens, w.scale, w.dtype, nthreads=8)
+    assert_close(v2, want, "bf16", "v2 vs oracle")
