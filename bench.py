@@ -87,7 +87,7 @@ def decode_setup(w, device, gen):
     st["out"] = torch.empty_like(st["q"])
     if w.rope_theta:
         st["cos_sin"] = rope_cos_sin_table(int(w.context_lens.max()), w.head_dim, w.rope_theta, device)
-    nbytes = kernels.v1_workspace_bytes(w.batch, w.num_heads, w.head_dim, w.block_size, w.max_blocks)
+    nbytes = kernels.v1_workspace_bytes(w.batch, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size, w.max_blocks)
     st["ws"] = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
     return st
 

@@ -137,19 +137,22 @@ int rg_rope_reshape_and_cache(void* q, const void* k, const void* v,
 
 /* ------------------------------------------------------- decode, v1 -------- */
 
-/* Bytes of workspace rg_paged_attention_v1 / _v1_plus use for the given shape
- * (0 is a valid answer: then no workspace is needed). */
+/* Bytes of workspace rg_paged_attention_v1 / _v1_plus use for the given shape on the
+ * current device (0 is a valid answer: then no workspace is needed).  The workspace holds
+ * split-K partials; its contents need no initialisation. */
 size_t rg_paged_attention_v1_workspace_bytes(int32_t batch_size, int32_t num_heads,
-                                             int32_t head_dim, int32_t block_size,
-                                             int32_t max_blocks_per_seq);
+                                             int32_t num_kv_heads, int32_t head_dim,
+                                             int32_t block_size, int32_t max_blocks_per_seq);
 
 /* Decode attention, one query token per sequence:
  *   out[s,h,:] = sum_t softmax_t(scale * q[s,h,:].K_t) V_t  over t < context_lens[s]
  * q/out [batch, num_heads, head_dim].  context_lens[s] == 0 gives zeros.
  * With workspace == NULL the whole context of a sequence is processed by one
- * workgroup per kv-head; with a workspace of rg_paged_attention_v1_workspace_bytes
- * the context is split into partitions that run in parallel and are merged
- * (faster for ragged batches).  Both give the same result within fp32 rounding.
+ * workgroup per kv-head.  With a workspace of rg_paged_attention_v1_workspace_bytes the
+ * KV blocks of the whole batch are split evenly over all compute units (each wave gets
+ * the same number of blocks, whatever the context lengths) and the per-split partials are
+ * merged by a second kernel — the fast path for ragged batches.  Both give the same
+ * result within fp32 rounding.
  * Replaces launch_v1 (crates/vllm-cuda/src/kernels/mod.rs:305-348). */
 int rg_paged_attention_v1(const void* query, const void* key_cache,
                           const void* value_cache, const int32_t* block_table,
@@ -214,8 +217,11 @@ int rg_paged_attention_v2_reduce(void* output, const float* exp_sums,
                                  int32_t batch_size, int32_t partition_size,
                                  int32_t dtype, void* stream);
 
-/* v2_partition followed by v2_reduce, with the scratch carved out of
- * `workspace` (rg_v2_workspace_bytes).  num_partitions = ceil(max_context_len/P).
+/* The v2 computation in one call: split-K partials merged with the exp-sum/max-logit
+ * rule of v2_reduce.  With a workspace of at least
+ * max(rg_v2_workspace_bytes(B,H,ceil(max_context_len/P),D), rg_paged_attention_v1_workspace_bytes)
+ * bytes the splits are balanced across the compute units (as in v1); with at least
+ * rg_v2_workspace_bytes it runs v2_partition + v2_reduce with partition size P.
  * The host side of PagedAttentionOp::execute's v2 branch
  * (crates/vllm-cuda/src/kernels/paged_attn_op.rs:108-158). */
 int rg_paged_attention_v2(const void* query, const void* key_cache,

@@ -201,151 +201,119 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-// Orders LDS writes of one lane before LDS reads of another lane of the same
-// wave (and keeps the compiler from moving accesses across).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
+// Orders LDS writes of one lane before LDS reads of another lane of the same wave: waits
+// for the wave's LDS operations only (global loads in flight stay in flight) and keeps the
+// compiler from moving memory accesses across.
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-constexpr int kBS = 16;       // tokens per KV block on the MFMA path
-constexpr int kWaves = 4;     // waves per workgroup
+// 2^x with the hardware v_exp_f32 (results below 2^-126 flush to zero, which only drops
+// softmax weights that are already negligible).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+constexpr int kBS = 16;  // tokens per KV block on the MFMA path
+
+// Tuning knobs of the MFMA path (compile-time): waves per workgroup, blocks each wave keeps
+// in flight ahead of the one it computes, and an optional occupancy floor.
+#ifndef RG_DEC_WAVES
+#define RG_DEC_WAVES 4
+#endif
+#ifndef RG_DEC_PREFETCH
+#define RG_DEC_PREFETCH 2
+#endif
+constexpr int kWaves = RG_DEC_WAVES;
+constexpr int kPrefetch = RG_DEC_PREFETCH;
 constexpr int kThreads = kWaves * 64;
+#if defined(RG_DEC_WAVES_PER_EU) && RG_DEC_WAVES_PER_EU > 0
+#define RG_DEC_OCCUPANCY __attribute__((amdgpu_waves_per_eu(RG_DEC_WAVES_PER_EU)))
+#else
+#define RG_DEC_OCCUPANCY
+#endif
 
-// D: head_dim (64 or 128); G: q-heads per kv-head (1, 2, 4, 8 or 16).
+// Per-wave state and block step of the MFMA decode path, shared by the grid kernel and the
+// stream-K kernel.  One wave owns one (sequence, kv-head) segment at a time and processes
+// 16-token blocks:
+//   QK role (MFMA): lane (col = lane%16, seg = lane/16) holds K[col][seg*D/4 ...] and the
+//     q rows replicated so that MFMA row m is head m % G; the result gives every lane the
+//     scores of 4 heads (rows 4*seg+r) for token `col`.
+//   PV role (VALU): lane (vrow = lane/ROWV, vd0 = 8*(lane%ROWV)) holds V rows vrow + i*TPI,
+//     dims vd0..vd0+8, and accumulates acc[h][0..8) for all G heads.
+// The softmax runs in the exp2 domain with a wave-uniform running max per head; the
+// probabilities travel from the QK layout to the PV layout through a small LDS area.
 template <typename T, int D, int G>
-__global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
+struct DecodeTile {
   using MF = mfma16<T>;
   using S = uint16_t;
-  constexpr int NK = D / 32;           // MFMAs (and 16-byte K loads) per block
-  constexpr int ROWV = D / 8;          // 16-byte vectors per token row
-  constexpr int TPI = 64 / ROWV;       // tokens covered by one V load instruction
-  constexpr int NV = kBS / TPI;        // V loads per block
-  constexpr int GP = G < 4 ? 4 : G;    // padded heads per LDS row
-  constexpr int HG = (G + 3) / 4;      // rows of the MFMA output that hold distinct heads
+  static constexpr int NK = D / 32;         // MFMAs (and 16-byte K loads) per block
+  static constexpr int ROWV = D / 8;        // 16-byte vectors per token row
+  static constexpr int TPI = 64 / ROWV;     // tokens covered by one V load instruction
+  static constexpr int NV = kBS / TPI;      // V loads per block
+  static constexpr int GP = G < 4 ? 4 : G;  // padded heads per LDS row
+  static constexpr int HG = (G + 3) / 4;    // MFMA output rows holding distinct heads
 
-  __shared__ float p_lds[kWaves][2][kBS * GP];
-  __shared__ float alpha_lds[kWaves][2][GP];
-  __shared__ float acc_lds[kWaves][G * D];
-  __shared__ float ml_lds[kWaves][2][GP];
-
-  const int p = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int s = blockIdx.z;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-
-  const int ctx = max(0, min(a.context_lens[s], a.max_blocks * kBS));
-  const int P = a.partition_size;
-  const int np_s = min(num_parts_for(ctx, P), a.num_partitions);
-  const bool final_out = a.mode == MODE_FINAL || (a.mode == MODE_AUTO && np_s <= 1);
-  const int H = a.num_heads;
-
-  if (p >= np_s) {
-    if (ctx == 0 && p == 0 && final_out) {
-      S* o = static_cast<S*>(a.out) + ((int64_t)s * H + (int64_t)kvh * G) * D;
-      for (int i = tid; i < G * D; i += kThreads) o[i] = 0;
-    }
-    return;
-  }
-
-  // Blocks of this partition; wave w takes blocks b0+w, b0+w+4, ...
-  const int nblk_ctx = (ctx + kBS - 1) / kBS;
-  const int b0 = p * (P / kBS);
-  const int b1 = min(nblk_ctx, b0 + P / kBS);
-  const int nb = b0 + w < b1 ? (b1 - (b0 + w) + kWaves - 1) / kWaves : 0;
-
-  // QK role: column (token in block) and k-segment of this lane.
-  const int col = lane & 15;
-  const int seg = lane >> 4;
-  // PV role: token row within a V load and the 8-element slice of head_dim.
-  const int vrow = lane / ROWV;
-  const int vd0 = (lane % ROWV) * 8;
-
-  // A operand: q rows replicated so that MFMA row m holds head (m % G).
-  const S* qbase = static_cast<const S*>(a.q) + ((int64_t)s * H + (int64_t)kvh * G) * D;
+  int col, seg, vrow, vd0;
   uint4 qa[NK];
-  {
-    const uint4* qrow = reinterpret_cast<const uint4*>(qbase + (int64_t)(col % G) * D + seg * (D / 4));
+  float m_run[4], l_run[4];
+  float acc[G][8];
+
+  __device__ __forceinline__ void init(int lane) {
+    col = lane & 15;
+    seg = lane >> 4;
+    vrow = lane / ROWV;
+    vd0 = (lane % ROWV) * 8;
+  }
+  // q rows of the G heads of one kv-head ([G, D] contiguous).
+  __device__ __forceinline__ void load_q(const S* qg) {
+    const uint4* qrow = reinterpret_cast<const uint4*>(qg + (int64_t)(col % G) * D + seg * (D / 4));
 #pragma unroll
     for (int i = 0; i < NK; ++i) qa[i] = qrow[i];
   }
-
-  const S* kc = static_cast<const S*>(a.k_cache);
-  const S* vc = static_cast<const S*>(a.v_cache);
-  const int32_t* bt = a.block_table + (int64_t)s * a.max_blocks;
-  const int64_t head_off = (int64_t)kvh * kBS * D;
-
-  float m_run[4], l_run[4];
+  __device__ __forceinline__ void reset() {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    m_run[r] = -INFINITY;
-    l_run[r] = 0.f;
+    for (int r = 0; r < 4; ++r) {
+      m_run[r] = -INFINITY;
+      l_run[r] = 0.f;
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
   }
-  float acc[G][8];
-#pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
-
-  uint4 kr[NK], vr[NV];
-  auto load_block = [&](int bidx, uint4* kk, uint4* vv) {
-    const int64_t blk = bt[bidx];
-    const S* kb = kc + blk * a.kv_stride + head_off;
-    const S* vb = vc + blk * a.kv_stride + head_off;
+  // kb / vb: the [16, D] rows of one kv-head in one block.
+  __device__ __forceinline__ void load(const S* kb, const S* vb, uint4 (&kk)[NK], uint4 (&vv)[NV]) const {
     const uint4* kp = reinterpret_cast<const uint4*>(kb + col * D + seg * (D / 4));
 #pragma unroll
     for (int i = 0; i < NK; ++i) kk[i] = kp[i];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      vv[i] = *reinterpret_cast<const uint4*>(vb + (i * TPI + vrow) * D + vd0);
-    }
-  };
-
-  if (nb > 0) load_block(b0 + w, kr, vr);
-  for (int j = 0; j < nb; ++j) {
-    const int bidx = b0 + w + j * kWaves;
-    uint4 kn[NK], vn[NV];
-    const bool more = j + 1 < nb;
-    if (more) load_block(bidx + kWaves, kn, vn);
-    const int slot = j & 1;
-
-    // S = Q K^T for the 16 tokens of the block: lane holds rows 4*seg+r, column col.
+    for (int i = 0; i < NV; ++i) vv[i] = *reinterpret_cast<const uint4*>(vb + (i * TPI + vrow) * D + vd0);
+  }
+  // One block whose first token has context index tok0 (tokens >= ctx are masked).
+  __device__ __forceinline__ void step(const uint4 (&kr)[NK], const uint4 (&vr)[NV], int tok0, int ctx,
+                                       float scale_log2, float* p_lds, float* alpha_lds) {
     f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NK; ++i) c = MF::run(qa[i], kr[i], c);
-
-    const int tok0 = bidx * kBS;
     const bool tail = tok0 + kBS > ctx;
     const bool valid = tok0 + col < ctx;
     float pr[4], al[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float x = valid ? c[r] * a.scale_log2 : -INFINITY;
+      const float x = valid ? c[r] * scale_log2 : -INFINITY;
       const float bm = row16_max(x);
       const float m_new = fmaxf(m_run[r], bm);
-      al[r] = exp2f(m_run[r] - m_new);
-      pr[r] = exp2f(x - m_new);
+      al[r] = fast_exp2(m_run[r] - m_new);
+      pr[r] = fast_exp2(x - m_new);
       l_run[r] = l_run[r] * al[r] + pr[r];
       m_run[r] = m_new;
     }
     if (seg < HG) {
-      *reinterpret_cast<float4*>(&p_lds[w][slot][col * GP + 4 * seg]) =
-          make_float4(pr[0], pr[1], pr[2], pr[3]);
-      if (col == 0) {
-        *reinterpret_cast<float4*>(&alpha_lds[w][slot][4 * seg]) =
-            make_float4(al[0], al[1], al[2], al[3]);
-      }
+      *reinterpret_cast<float4*>(&p_lds[col * GP + 4 * seg]) = make_float4(pr[0], pr[1], pr[2], pr[3]);
+      if (col == 0) *reinterpret_cast<float4*>(&alpha_lds[4 * seg]) = make_float4(al[0], al[1], al[2], al[3]);
     }
     wave_lds_sync();
-
-    // O = alpha * O + P V on the VALU.
     {
       float alh[G];
 #pragma unroll
-      for (int h = 0; h < G; ++h) alh[h] = alpha_lds[w][slot][h];
+      for (int h = 0; h < G; ++h) alh[h] = alpha_lds[h];
 #pragma unroll
       for (int h = 0; h < G; ++h)
 #pragma unroll
@@ -363,51 +331,126 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
       }
       float ph[G];
 #pragma unroll
-      for (int h = 0; h < G; ++h) ph[h] = p_lds[w][slot][t * GP + h];
+      for (int h = 0; h < G; ++h) ph[h] = p_lds[t * GP + h];
 #pragma unroll
       for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] += ph[h] * vf[e];
     }
-    if (more) {
+  }
+  // Sums acc over the TPI token rows (result valid in lanes with vrow == 0) and l over the
+  // 16 columns (lsum[r] for head 4*seg+r, valid in every lane).
+  __device__ __forceinline__ void reduce(float (&lsum)[4]) {
 #pragma unroll
-      for (int i = 0; i < NK; ++i) kr[i] = kn[i];
+    for (int h = 0; h < G; ++h)
 #pragma unroll
-      for (int i = 0; i < NV; ++i) vr[i] = vn[i];
+      for (int e = 0; e < 8; ++e) {
+        float v = acc[h][e];
+#pragma unroll
+        for (int o = ROWV; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+        acc[h][e] = v;
+      }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lsum[r] = row16_sum(l_run[r]);
+  }
+};
+
+// Grid decomposition: workgroup = (partition p, kv-head, sequence), kWaves waves taking the
+// partition's blocks round-robin, merged through LDS at the end.
+template <typename T, int D, int G>
+__global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
+    DecodeArgs a, const uint16_t* __restrict__ q_ptr, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_table,
+    const int32_t* __restrict__ context_lens) {
+  using Tile = DecodeTile<T, D, G>;
+  using S = uint16_t;
+  constexpr int GP = Tile::GP;
+  constexpr int HG = Tile::HG;
+  constexpr int NK = Tile::NK;
+  constexpr int NV = Tile::NV;
+  constexpr int NBUF = kPrefetch + 1;
+
+  __shared__ float p_lds[kWaves][2][kBS * GP];
+  __shared__ float alpha_lds[kWaves][2][GP];
+  __shared__ float acc_lds[kWaves][G * D];
+  __shared__ float ml_lds[kWaves][2][GP];
+
+  const int p = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int s = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  const int ctx = max(0, min(context_lens[s], a.max_blocks * kBS));
+  const int P = a.partition_size;
+  const int np_s = min(num_parts_for(ctx, P), a.num_partitions);
+  const bool final_out = a.mode == MODE_FINAL || (a.mode == MODE_AUTO && np_s <= 1);
+  const int H = a.num_heads;
+
+  if (p >= np_s) {
+    if (ctx == 0 && p == 0 && final_out) {
+      S* o = static_cast<S*>(a.out) + ((int64_t)s * H + (int64_t)kvh * G) * D;
+      for (int i = tid; i < G * D; i += kThreads) o[i] = 0;
+    }
+    return;
+  }
+
+  // Blocks of this partition; wave w takes blocks b0+w, b0+w+kWaves, ...
+  const int nblk_ctx = (ctx + kBS - 1) / kBS;
+  const int b0 = p * (P / kBS);
+  const int b1 = min(nblk_ctx, b0 + P / kBS);
+  const int nb = b0 + w < b1 ? (b1 - (b0 + w) + kWaves - 1) / kWaves : 0;
+
+  Tile tile;
+  tile.init(lane);
+  tile.load_q(q_ptr + ((int64_t)s * H + (int64_t)kvh * G) * D);
+  tile.reset();
+  const int32_t* bt = block_table + (int64_t)s * a.max_blocks;
+  const int64_t head_off = (int64_t)kvh * kBS * D;
+  auto load_block = [&](int j, uint4 (&kk)[NK], uint4 (&vv)[NV]) {
+    const int64_t off = (int64_t)bt[b0 + w + j * kWaves] * a.kv_stride + head_off;
+    tile.load(kc + off, vc + off, kk, vv);
+  };
+
+  // Software pipeline: kPrefetch blocks in flight ahead of the one being computed; past
+  // the end the prefetch re-reads the wave's last block (a cache hit), so every step issues
+  // the same loads and the waits stay exact counts instead of full drains.
+  uint4 kbuf[NBUF][NK], vbuf[NBUF][NV];
+  if (nb > 0) {
+#pragma unroll
+    for (int u = 0; u < kPrefetch; ++u) load_block(min(u, nb - 1), kbuf[u], vbuf[u]);
+  }
+  for (int j0 = 0; j0 < nb; j0 += NBUF) {
+#pragma unroll
+    for (int u = 0; u < NBUF; ++u) {
+      const int j = j0 + u;
+      if (j < nb) {
+        load_block(min(j + kPrefetch, nb - 1), kbuf[(u + kPrefetch) % NBUF], vbuf[(u + kPrefetch) % NBUF]);
+        tile.step(kbuf[u], vbuf[u], (b0 + w + j * kWaves) * kBS, ctx, a.scale_log2, p_lds[w][j & 1],
+                  alpha_lds[w][j & 1]);
+      }
     }
   }
 
-  // Reduce the TPI token rows of the PV layout (lanes with equal lane % ROWV).
-#pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float v = acc[h][e];
-#pragma unroll
-      for (int o = ROWV; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
-      acc[h][e] = v;
-    }
-  if (vrow == 0) {
+  float lsum[4];
+  tile.reduce(lsum);
+  if (tile.vrow == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float4* dst = reinterpret_cast<float4*>(&acc_lds[w][h * D + vd0]);
-      dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-      dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+      float4* dst = reinterpret_cast<float4*>(&acc_lds[w][h * D + tile.vd0]);
+      dst[0] = make_float4(tile.acc[h][0], tile.acc[h][1], tile.acc[h][2], tile.acc[h][3]);
+      dst[1] = make_float4(tile.acc[h][4], tile.acc[h][5], tile.acc[h][6], tile.acc[h][7]);
     }
   }
-  // Softmax state per head: l summed over the 16 columns of a row.
-  float lsum[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) lsum[r] = row16_sum(l_run[r]);
-  if (seg < HG && col == 0) {
-    *reinterpret_cast<float4*>(&ml_lds[w][0][4 * seg]) =
-        make_float4(m_run[0], m_run[1], m_run[2], m_run[3]);
-    *reinterpret_cast<float4*>(&ml_lds[w][1][4 * seg]) =
-        make_float4(lsum[0], lsum[1], lsum[2], lsum[3]);
+  if (tile.seg < HG && tile.col == 0) {
+    *reinterpret_cast<float4*>(&ml_lds[w][0][4 * tile.seg]) =
+        make_float4(tile.m_run[0], tile.m_run[1], tile.m_run[2], tile.m_run[3]);
+    *reinterpret_cast<float4*>(&ml_lds[w][1][4 * tile.seg]) = make_float4(lsum[0], lsum[1], lsum[2], lsum[3]);
   }
   __syncthreads();
 
-  // Merge the four waves and write out two consecutive dims per thread.
+  // Merge the waves and write out two consecutive dims per thread.
   for (int idx = tid; idx < G * D / 2; idx += kThreads) {
     const int h = idx / (D / 2);
     const int d = (idx % (D / 2)) * 2;
@@ -441,6 +484,291 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
   }
 }
 
+// ------------------------------------------------------------- stream-K -----
+//
+// The decode work is the list of units (sequence s, kv-head, block b) ordered with b
+// fastest; segment g = s * num_kv_heads + kvh is the run of units of one (s, kv-head).
+// Worker k (one wave) takes units [k*U/W, (k+1)*U/W) of the U units, so every wave streams
+// the same number of KV blocks whatever the context lengths are.  A worker emits one partial
+// (m, l, acc) for every segment it touches, at partial index k + g (distinct for all
+// (worker, segment) pairs because each worker's segments and each segment's workers are
+// consecutive).  decode_stream_merge_kernel combines the partials of each segment.  When
+// U < W only the first U workers are used, so every worker of a segment's range owns units.
+
+struct StreamArgs {
+  void* out;
+  float* part_acc;   // [num_partials, G, D]
+  float* part_ml;    // [num_partials, G, 2]: (m in log2 units, l)
+  float scale_log2;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t max_blocks;
+  int32_t batch;
+  int32_t num_workers;
+  int64_t kv_stride;
+};
+
+__device__ __forceinline__ int64_t worker_start(int64_t k, int64_t U, int64_t W) { return k * U / W; }
+// The worker whose range contains unit u (the last k with worker_start(k) <= u).
+__device__ __forceinline__ int64_t worker_of(int64_t u, int64_t U, int64_t W) { return ((u + 1) * W - 1) / U; }
+
+// Units of sequence s: ceil(ctx/16) blocks per kv-head (context clamped to the table row).
+__device__ __forceinline__ int seq_blocks(const int32_t* ctxl, int s, int max_blocks) {
+  const int c = max(0, min(ctxl[s], max_blocks * kBS));
+  return (c + kBS - 1) / kBS;
+}
+
+// Wave-wide inclusive prefix sum.
+__device__ __forceinline__ int64_t wave_incl_scan(int64_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Total units U and, if `target` >= 0, the sequence containing unit `target` and the first
+// unit of that sequence.  Every lane returns the same values.
+__device__ __forceinline__ int64_t scan_units(const int32_t* ctxl, int batch, int max_blocks, int hkv,
+                                              int lane, int64_t target, int& seq_out, int64_t& seq_start) {
+  int64_t base = 0;
+  seq_out = -1;
+  seq_start = 0;
+  for (int c0 = 0; c0 < batch; c0 += 64) {
+    const int s = c0 + lane;
+    const int64_t n = s < batch ? (int64_t)seq_blocks(ctxl, s, max_blocks) * hkv : 0;
+    const int64_t incl = wave_incl_scan(n, lane) + base;
+    const int64_t excl = incl - n;
+    if (target >= 0 && seq_out < 0) {
+      const uint64_t hit = __ballot(n > 0 && excl <= target && target < incl);
+      if (hit) {
+        const int l = __ffsll((unsigned long long)hit) - 1;
+        seq_out = c0 + l;
+        seq_start = __shfl(excl, l, 64);
+      }
+    }
+    base = __shfl(incl, 63, 64);
+  }
+  return base;
+}
+
+template <typename T, int D, int G>
+__global__ __launch_bounds__(64) void decode_stream_kernel(
+    StreamArgs a, const uint16_t* __restrict__ q_ptr, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_table,
+    const int32_t* __restrict__ context_lens) {
+  using Tile = DecodeTile<T, D, G>;
+  constexpr int GP = Tile::GP;
+  constexpr int HG = Tile::HG;
+  constexpr int NK = Tile::NK;
+  constexpr int NV = Tile::NV;
+  constexpr int NBUF = kPrefetch + 1;
+  __shared__ float p_lds[2][kBS * GP];
+  __shared__ float alpha_lds[2][GP];
+
+  const int lane = threadIdx.x;
+  const int64_t k = blockIdx.x;
+  const int hkv = a.num_kv_heads;
+  int s_dummy;
+  int64_t st_dummy;
+  const int64_t U = scan_units(context_lens, a.batch, a.max_blocks, hkv, lane, -1, s_dummy, st_dummy);
+  // With fewer units than workers only the first U workers run (one unit each), so that every
+  // worker between a segment's first and last one owns a unit and writes a partial.
+  const int64_t W = min<int64_t>(a.num_workers, U);
+  if (k >= W) return;
+  const int64_t u0 = worker_start(k, U, W);
+  const int64_t u1 = worker_start(k + 1, U, W);
+  int s;
+  int64_t seq_start;
+  scan_units(context_lens, a.batch, a.max_blocks, hkv, lane, u0, s, seq_start);
+  s = __builtin_amdgcn_readfirstlane(s);
+
+  // Cursor of the unit being computed (cs, ckvh, cb) and of the unit being loaded.
+  struct Cursor {
+    int s, kvh, b, nblk;
+  };
+  Cursor cur;
+  cur.s = s;
+  cur.nblk = seq_blocks(context_lens, s, a.max_blocks);
+  {
+    const int64_t r = u0 - seq_start;
+    cur.kvh = (int)(r / cur.nblk);
+    cur.b = (int)(r - (int64_t)cur.kvh * cur.nblk);
+  }
+  auto advance = [&](Cursor& c) {
+    if (++c.b == c.nblk) {
+      c.b = 0;
+      if (++c.kvh == hkv) {
+        c.kvh = 0;
+        do {
+          ++c.s;
+          c.nblk = c.s < a.batch ? seq_blocks(context_lens, c.s, a.max_blocks) : 1;
+        } while (c.nblk == 0);
+      }
+    }
+  };
+  auto load_unit = [&](const Cursor& c, uint4 (&kk)[NK], uint4 (&vv)[NV], const Tile& t) {
+    const int64_t off = (int64_t)block_table[(int64_t)c.s * a.max_blocks + c.b] * a.kv_stride +
+                        (int64_t)c.kvh * kBS * D;
+    t.load(kc + off, vc + off, kk, vv);
+  };
+
+  Tile tile;
+  tile.init(lane);
+  const int H = a.num_heads;
+  auto begin_segment = [&](const Cursor& c) {
+    tile.load_q(q_ptr + ((int64_t)c.s * H + (int64_t)c.kvh * G) * D);
+    tile.reset();
+  };
+  auto end_segment = [&](const Cursor& c) {
+    float lsum[4];
+    tile.reduce(lsum);
+    const int64_t g = (int64_t)c.s * hkv + c.kvh;
+    const int64_t idx = k + g;
+    float* pa = a.part_acc + idx * (G * D);
+    if (tile.vrow == 0) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float4* dst = reinterpret_cast<float4*>(pa + h * D + tile.vd0);
+        dst[0] = make_float4(tile.acc[h][0], tile.acc[h][1], tile.acc[h][2], tile.acc[h][3]);
+        dst[1] = make_float4(tile.acc[h][4], tile.acc[h][5], tile.acc[h][6], tile.acc[h][7]);
+      }
+    }
+    if (tile.col == 0 && tile.seg < HG) {
+      float* pm = a.part_ml + idx * (2 * G);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int h = 4 * tile.seg + r;
+        if (h < G) {
+          pm[2 * h] = tile.m_run[r];
+          pm[2 * h + 1] = lsum[r];
+        }
+      }
+    }
+  };
+
+  const int64_t n = u1 - u0;
+  Cursor ld = cur;
+  uint4 kbuf[NBUF][NK], vbuf[NBUF][NV];
+  // Prologue: the first kPrefetch units (the last one repeated past the end of the range).
+#pragma unroll
+  for (int q = 0; q < kPrefetch; ++q) {
+    load_unit(ld, kbuf[q], vbuf[q], tile);
+    if (q + 1 < n) advance(ld);
+  }
+  int64_t loaded = min<int64_t>(kPrefetch, n);  // units whose loads have been issued
+  begin_segment(cur);
+  for (int64_t j0 = 0; j0 < n; j0 += NBUF) {
+#pragma unroll
+    for (int q = 0; q < NBUF; ++q) {
+      const int64_t j = j0 + q;
+      if (j < n) {
+        load_unit(ld, kbuf[(q + kPrefetch) % NBUF], vbuf[(q + kPrefetch) % NBUF], tile);
+        if (loaded < n) {
+          ++loaded;
+          if (loaded < n) advance(ld);
+        }
+        const int ctx = min(context_lens[cur.s], a.max_blocks * kBS);
+        tile.step(kbuf[q], vbuf[q], cur.b * kBS, ctx, a.scale_log2, p_lds[j & 1], alpha_lds[j & 1]);
+        const bool last_of_segment = cur.b + 1 == cur.nblk || j + 1 == n;
+        if (last_of_segment) {
+          end_segment(cur);
+          if (j + 1 < n) {
+            advance(cur);
+            begin_segment(cur);
+          }
+        } else {
+          advance(cur);
+        }
+      }
+    }
+  }
+}
+
+// One workgroup per segment (sequence, kv-head): merges the partials of workers
+// worker_of(first unit) .. worker_of(last unit) and writes the G output rows.
+template <typename T, int D, int G>
+__global__ __launch_bounds__(256) void decode_stream_merge_kernel(StreamArgs a,
+                                                                  const int32_t* __restrict__ context_lens) {
+  using S = uint16_t;
+  __shared__ float m_lds[G];
+  __shared__ float inv_lds[G];
+  const int kvh = blockIdx.x;
+  const int s = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int hkv = a.num_kv_heads;
+  S* out = static_cast<S*>(a.out) + ((int64_t)s * a.num_heads + (int64_t)kvh * G) * D;
+  const int nblk = seq_blocks(context_lens, s, a.max_blocks);
+  if (nblk == 0) {
+    for (int i = tid; i < G * D; i += 256) out[i] = 0;
+    return;
+  }
+  // Every wave scans (cheap) so that all threads know U and the segment's first unit.
+  int s_found;
+  int64_t seq_start;
+  const int64_t U = scan_units(context_lens, a.batch, a.max_blocks, hkv, lane, -1, s_found, seq_start);
+  int64_t ubeg = 0;
+  {
+    int64_t base = 0;
+    for (int c0 = 0; c0 < s; c0 += 64) {
+      const int ss = c0 + lane;
+      const int64_t n = ss < s ? (int64_t)seq_blocks(context_lens, ss, a.max_blocks) * hkv : 0;
+      base += __shfl(wave_incl_scan(n, lane), 63, 64);
+    }
+    ubeg = base + (int64_t)kvh * nblk;
+  }
+  const int64_t W = min<int64_t>(a.num_workers, U);
+  const int64_t first = worker_of(ubeg, U, W);
+  const int64_t last = worker_of(ubeg + nblk - 1, U, W);
+  const int64_t g = (int64_t)s * hkv + kvh;
+  const int np = (int)(last - first + 1);
+
+  // Per-head max and normaliser over the partials (every thread computes them; the loads
+  // are the same addresses across the workgroup).
+  float M[G], L[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    M[h] = -INFINITY;
+    L[h] = 0.f;
+  }
+  for (int q = 0; q < np; ++q) {
+    const float* pm = a.part_ml + (first + q + g) * (2 * G);
+#pragma unroll
+    for (int h = 0; h < G; ++h) M[h] = fmaxf(M[h], pm[2 * h]);
+  }
+  for (int q = 0; q < np; ++q) {
+    const float* pm = a.part_ml + (first + q + g) * (2 * G);
+#pragma unroll
+    for (int h = 0; h < G; ++h) L[h] += exp2f(pm[2 * h] - M[h]) * pm[2 * h + 1];
+  }
+  if (tid == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      m_lds[h] = M[h];
+      inv_lds[h] = L[h] != 0.f ? 1.f / L[h] : 1.f;
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < G * D / 2; idx += 256) {
+    const int h = idx / (D / 2);
+    const int d = (idx % (D / 2)) * 2;
+    const float Mh = m_lds[h];
+    float o0 = 0.f, o1 = 0.f;
+    for (int q = 0; q < np; ++q) {
+      const int64_t pi = first + q + g;
+      const float f = exp2f(a.part_ml[pi * (2 * G) + 2 * h] - Mh);
+      const float2 v = *reinterpret_cast<const float2*>(a.part_acc + pi * (G * D) + h * D + d);
+      o0 += f * v.x;
+      o1 += f * v.y;
+    }
+    const float inv = inv_lds[h];
+    const uint32_t packed = (uint32_t)elem<T>::from_f32(o0 * inv) | ((uint32_t)elem<T>::from_f32(o1 * inv) << 16);
+    *reinterpret_cast<uint32_t*>(out + h * D + d) = packed;
+  }
+}
+
 // ---------------------------------------------------------------- merge -----
 
 struct MergeArgs {
@@ -456,10 +784,14 @@ struct MergeArgs {
   int32_t skip_single;  // 1: sequences with one partition were written by the partition kernel
 };
 
+// One wave per (seq, q-head).  The partition weights e^(m_p - M) are computed once per
+// partition into LDS, then every lane accumulates its dims over the partitions.
 template <typename T>
 __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   using E = elem<T>;
   using S = typename E::storage;
+  constexpr int kChunk = 64;
+  __shared__ float w_lds[kChunk];
   const int h = blockIdx.x;
   const int s = blockIdx.y;
   const int lane = threadIdx.x;
@@ -483,27 +815,50 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   L = wave_sum(L);
   const float inv = L != 0.f ? 1.f / L : 1.f;
   const float* tp = a.tmp_out + sh * D;
-  for (int d0 = lane * 4; d0 < D; d0 += 256) {
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int q = 0; q < np_s; ++q) {
-      const float r = expf(ml[q] - M);
-      const float4 v = *reinterpret_cast<const float4*>(tp + (int64_t)q * D + d0);
-      acc.x += r * v.x;
-      acc.y += r * v.y;
-      acc.z += r * v.z;
-      acc.w += r * v.w;
+  // Lane owns dims lane*4 + 256*i (head_dim <= 1024, checked on the host).
+  float4 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int q0 = 0; q0 < np_s; q0 += kChunk) {
+    const int n = min(kChunk, np_s - q0);
+    __syncthreads();  // previous chunk's weights are no longer read
+    if (lane < n) w_lds[lane] = expf(ml[q0 + lane] - M);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d0 = lane * 4 + 256 * i;
+      if (d0 < D) {
+#pragma unroll 4
+        for (int q = 0; q < n; ++q) {
+          const float r = w_lds[q];
+          const float4 v = *reinterpret_cast<const float4*>(tp + (int64_t)(q0 + q) * D + d0);
+          acc[i].x += r * v.x;
+          acc[i].y += r * v.y;
+          acc[i].z += r * v.z;
+          acc[i].w += r * v.w;
+        }
+      }
     }
-    E::store(op, d0 + 0, acc.x * inv);
-    E::store(op, d0 + 1, acc.y * inv);
-    E::store(op, d0 + 2, acc.z * inv);
-    E::store(op, d0 + 3, acc.w * inv);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d0 = lane * 4 + 256 * i;
+    if (d0 < D) {
+      E::store(op, d0 + 0, acc[i].x * inv);
+      E::store(op, d0 + 1, acc[i].y * inv);
+      E::store(op, d0 + 2, acc[i].z * inv);
+      E::store(op, d0 + 3, acc[i].w * inv);
+    }
   }
 }
 
 // ------------------------------------------------------------ host side -----
 
 // Tokens per partition the v1 entries use when given a workspace.
-constexpr int kV1PartitionTokens = 256;
+#ifndef RG_V1_PARTITION
+#define RG_V1_PARTITION 256
+#endif
+constexpr int kV1PartitionTokens = RG_V1_PARTITION;
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -535,7 +890,9 @@ int check_decode_shape(const char* op, const Shape& sh, int32_t dtype, int64_t k
 
 template <typename T, int D, int G>
 void launch_mfma(const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((decode_mfma_kernel<T, D, G>), grid, dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((decode_mfma_kernel<T, D, G>), grid, dim3(kThreads), 0, s, a,
+                     static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.k_cache),
+                     static_cast<const uint16_t*>(a.v_cache), a.block_table, a.context_lens);
 }
 
 template <typename T, int D>
@@ -643,6 +1000,94 @@ int32_t v1_num_partitions(const Shape& sh) {
   return (int32_t)ceil_div(max_ctx, kV1PartitionTokens);
 }
 
+// ---- stream-K path ----
+
+// Waves per CU the stream-K decode launches (one worker per wave).
+#ifndef RG_SK_WAVES_PER_CU
+#define RG_SK_WAVES_PER_CU 8
+#endif
+
+int device_cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+    n = 256;
+  }
+  return n;
+}
+
+int32_t stream_workers(const Shape& sh) {
+  const int64_t want = (int64_t)device_cu_count() * RG_SK_WAVES_PER_CU;
+  const int64_t units_max = (int64_t)sh.B * sh.Hkv * std::max(sh.MB, 1);
+  return (int32_t)std::max<int64_t>(1, std::min(want, units_max));
+}
+
+struct StreamScratch {
+  float* acc;
+  float* ml;
+};
+
+size_t stream_bytes(const Shape& sh, int32_t workers, StreamScratch* carve, void* base) {
+  const int64_t G = sh.H / sh.Hkv;
+  const int64_t partials = (int64_t)workers + (int64_t)sh.B * sh.Hkv;
+  const size_t acc = align_up((size_t)(partials * G * sh.D) * 4, 256);
+  const size_t ml = align_up((size_t)(partials * G * 2) * 4, 256);
+  if (carve) {
+    carve->acc = static_cast<float*>(base);
+    carve->ml = reinterpret_cast<float*>(static_cast<char*>(base) + acc);
+  }
+  return acc + ml;
+}
+
+template <typename T, int D, int G>
+void launch_stream(const StreamArgs& sa, const DecodeArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((decode_stream_kernel<T, D, G>), dim3(sa.num_workers), dim3(64), 0, s, sa,
+                     static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.k_cache),
+                     static_cast<const uint16_t*>(a.v_cache), a.block_table, a.context_lens);
+  hipLaunchKernelGGL((decode_stream_merge_kernel<T, D, G>), dim3(sa.num_kv_heads, sa.batch), dim3(256), 0, s,
+                     sa, a.context_lens);
+}
+
+template <typename T, int D>
+void launch_stream_g(const StreamArgs& sa, const DecodeArgs& a, int G, hipStream_t s) {
+  switch (G) {
+    case 1: launch_stream<T, D, 1>(sa, a, s); break;
+    case 2: launch_stream<T, D, 2>(sa, a, s); break;
+    case 4: launch_stream<T, D, 4>(sa, a, s); break;
+    case 8: launch_stream<T, D, 8>(sa, a, s); break;
+    default: launch_stream<T, D, 16>(sa, a, s); break;
+  }
+}
+
+// Runs the stream-K decode if it applies and the workspace holds its scratch; returns
+// RG_ERR_WORKSPACE (without recording an error) when the workspace is too small.
+int run_stream(const char* op, const DecodeArgs& a, int32_t dtype, const Shape& sh, void* ws, size_t ws_bytes,
+               hipStream_t s) {
+  const int32_t workers = stream_workers(sh);
+  StreamScratch sc;
+  if (ws_bytes < stream_bytes(sh, workers, &sc, ws)) return RG_ERR_WORKSPACE;
+  StreamArgs sa;
+  sa.out = a.out;
+  sa.part_acc = sc.acc;
+  sa.part_ml = sc.ml;
+  sa.scale_log2 = a.scale_log2;
+  sa.num_heads = sh.H;
+  sa.num_kv_heads = sh.Hkv;
+  sa.max_blocks = sh.MB;
+  sa.batch = sh.B;
+  sa.num_workers = workers;
+  sa.kv_stride = a.kv_stride;
+  const int G = sh.H / sh.Hkv;
+  if (dtype == RG_DTYPE_BF16) {
+    if (sh.D == 128) launch_stream_g<bf16_t, 128>(sa, a, G, s);
+    else launch_stream_g<bf16_t, 64>(sa, a, G, s);
+  } else {
+    if (sh.D == 128) launch_stream_g<f16_t, 128>(sa, a, G, s);
+    else launch_stream_g<f16_t, 64>(sa, a, G, s);
+  }
+  return check_launch(op);
+}
+
 // Body shared by the v1 and v1_plus entries.
 int paged_v1(const char* op, const void* q, const void* kc, const void* vc, const int32_t* bt,
              const int32_t* cl, void* out, float scale, const Shape& sh, int32_t dtype,
@@ -654,6 +1099,15 @@ int paged_v1(const char* op, const void* q, const void* kc, const void* vc, cons
     return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
   }
   hipStream_t s = as_stream(stream);
+  if (ws != nullptr) {
+    DecodeArgs a = make_args(q, kc, vc, bt, cl, out, scale, sh, kv_stride, kBS, 1, MODE_AUTO);
+    if (mfma_applies(a, dtype) && sh.MB > 0) {
+      st = run_stream(op, a, dtype, sh, ws, ws_bytes, s);
+      if (st != RG_ERR_WORKSPACE) return st;
+      return fail(RG_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu required", op, ws_bytes,
+                  stream_bytes(sh, stream_workers(sh), nullptr, nullptr));
+    }
+  }
   const int32_t np = v1_num_partitions(sh);
   if (ws != nullptr && np > 1) {
     V2Scratch sc;
@@ -697,16 +1151,16 @@ int probe_decode_kernels() {
 using namespace rg;
 
 extern "C" size_t rg_paged_attention_v1_workspace_bytes(int32_t batch_size, int32_t num_heads,
-                                                        int32_t head_dim, int32_t block_size,
-                                                        int32_t max_blocks_per_seq) {
-  if (batch_size <= 0 || num_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
-      max_blocks_per_seq <= 0) {
+                                                        int32_t num_kv_heads, int32_t head_dim,
+                                                        int32_t block_size, int32_t max_blocks_per_seq) {
+  if (batch_size <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+      head_dim <= 0 || block_size <= 0 || max_blocks_per_seq <= 0) {
     return 0;
   }
-  const Shape sh{num_heads, 1, head_dim, block_size, max_blocks_per_seq, batch_size};
+  const Shape sh{num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, batch_size};
   const int32_t np = v1_num_partitions(sh);
-  if (np <= 1) return 0;
-  return v2_bytes(batch_size, num_heads, np, head_dim, nullptr, nullptr);
+  const size_t grid = np > 1 ? v2_bytes(batch_size, num_heads, np, head_dim, nullptr, nullptr) : 0;
+  return std::max(grid, stream_bytes(sh, stream_workers(sh), nullptr, nullptr));
 }
 
 extern "C" int rg_paged_attention_v1(const void* query, const void* key_cache,
@@ -831,6 +1285,17 @@ extern "C" int rg_paged_attention_v2(const void* query, const void* key_cache,
   if (!query || !key_cache || !value_cache || !block_table || !context_lens || !output) {
     return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
   }
+  hipStream_t s = as_stream(stream);
+  if (workspace != nullptr) {
+    // The stream-K decode computes the same merge of split-K partials with balanced splits;
+    // it runs whenever it applies and the workspace holds its scratch.
+    DecodeArgs a = make_args(query, key_cache, value_cache, block_table, context_lens, output, scale, sh,
+                             kv_block_stride, partition_size, 1, MODE_AUTO);
+    if (mfma_applies(a, dtype) && max_blocks_per_seq > 0) {
+      st = run_stream(op, a, dtype, sh, workspace, workspace_bytes, s);
+      if (st != RG_ERR_WORKSPACE) return st;
+    }
+  }
   const int32_t np = (int32_t)std::max<int64_t>(1, ceil_div(max_context_len, partition_size));
   V2Scratch sc;
   const size_t need = v2_bytes(batch_size, num_heads, np, head_dim, &sc, workspace);
@@ -838,7 +1303,6 @@ extern "C" int rg_paged_attention_v2(const void* query, const void* key_cache,
     return fail(RG_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu required", op,
                 workspace ? workspace_bytes : (size_t)0, need);
   }
-  hipStream_t s = as_stream(stream);
   DecodeArgs a = make_args(query, key_cache, value_cache, block_table, context_lens, output, scale,
                            sh, kv_block_stride, partition_size, np, MODE_AUTO);
   a.tmp_out = sc.tmp_out;

@@ -131,10 +131,10 @@ class PagedAttentionKernels:
             rotation_metadata.data_ptr(), num_kv_heads, head_dim, block_size, batch_size, dtype_code(k),
             k_cache.stride(0), _stream(k)))
 
-    def v1_workspace_bytes(self, batch_size: int, num_heads: int, head_dim: int, block_size: int,
-                           max_blocks_per_seq: int) -> int:
-        return int(self.lib.rg_paged_attention_v1_workspace_bytes(batch_size, num_heads, head_dim, block_size,
-                                                                  max_blocks_per_seq))
+    def v1_workspace_bytes(self, batch_size: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                           block_size: int, max_blocks_per_seq: int) -> int:
+        return int(self.lib.rg_paged_attention_v1_workspace_bytes(batch_size, num_heads, num_kv_heads, head_dim,
+                                                                  block_size, max_blocks_per_seq))
 
     # mod.rs:305-348 (+ optional workspace: the split-K form of the same computation)
     def launch_v1(self, query, key_cache, value_cache, block_table, context_lens, output, scale: float,
@@ -262,14 +262,15 @@ class PagedAttentionOp:
         out = torch.zeros_like(q)
         k = self.kernels
         if max_context_len <= V1_MAX_CONTEXT:
-            ws_bytes = k.v1_workspace_bytes(batch, num_heads, head_dim, block_size, max_blocks)
+            ws_bytes = k.v1_workspace_bytes(batch, num_heads, self.num_kv_heads, head_dim, block_size, max_blocks)
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
             k.launch_v1_plus(q, k_cache, v_cache, block_table, context_lens, out, rotation_metadata, self.scale,
                              num_heads, self.num_kv_heads, head_dim, block_size, max_blocks, batch, workspace=ws)
         else:
             num_parts = math.ceil(max_context_len / V2_PARTITION_SIZE)
-            ws = torch.empty(k.v2_workspace_bytes(batch, num_heads, num_parts, head_dim), dtype=torch.uint8,
-                             device=q.device)
+            ws_bytes = max(k.v2_workspace_bytes(batch, num_heads, num_parts, head_dim),
+                           k.v1_workspace_bytes(batch, num_heads, self.num_kv_heads, head_dim, block_size, max_blocks))
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
             k.launch_v2(q, k_cache, v_cache, block_table, context_lens, out, self.scale, num_heads,
                         self.num_kv_heads, head_dim, block_size, max_blocks, batch, max_context_len,
                         V2_PARTITION_SIZE, ws)

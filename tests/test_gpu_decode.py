@@ -51,7 +51,7 @@ def gpu_v1(kernels, inp, workspace: bool, entry: str = "v1"):
     out = torch.full_like(inp["dq"], float("nan"))
     ws = None
     if workspace:
-        nbytes = kernels.v1_workspace_bytes(B, inp["H"], inp["D"], inp["bs"], inp["mb"])
+        nbytes = kernels.v1_workspace_bytes(B, inp["H"], inp["Hkv"], inp["D"], inp["bs"], inp["mb"])
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=inp["dq"].device)
     args = (inp["dq"], inp["dkc"], inp["dvc"], inp["dbt"], inp["dctx"], out)
     tail = (inp["scale"], inp["H"], inp["Hkv"], inp["D"], inp["bs"], inp["mb"], B)
