@@ -40,6 +40,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-side", action="store_true", help="skip the config 3 / config 4 side figures")
+    ap.add_argument("--only", choices=["decode", "v2", "prefill"], default=None,
+                    help="run one workload only and print its figures (for profiling)")
     return ap.parse_args()
 
 
@@ -211,6 +213,12 @@ def main() -> int:
     torch.cuda.set_device(device)
     gen = torch.Generator(device=device)
     gen.manual_seed(1002)
+    if args.only == "v2":
+        print(json.dumps(side_v2(device, gen, args.steps)), flush=True)
+        return 0
+    if args.only == "prefill":
+        print(json.dumps(side_prefill(device, gen, args.steps)), flush=True)
+        return 0
     w = wl.config2()
     log(f"[bench] config2: B={w.batch} tokens={int(w.context_lens.sum())} pool={w.num_blocks} blocks")
     st = decode_setup(w, device, gen)
@@ -258,6 +266,9 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes": w.decode_bytes(), "us_per_launch": round(ms_v1 * 1e3, 2)},
     }
+    if args.only == "decode":
+        print(json.dumps(result), flush=True)
+        return 0
     if not args.no_side:
         log("[bench] config3 v2 ...")
         result["v2_long_context"] = side_v2(device, gen, max(3, args.steps // 5))

@@ -1,9 +1,10 @@
 // KV-cache scatter (reshape_and_cache), identity-IsoQuant metadata, RoPE and the
 // fused RoPE + scatter pass over the new tokens.
 //
-// All four are HBM-bound byte movers: one workgroup per new token, 16-byte
-// vector loads/stores along the contiguous head_dim rows wherever the row
-// length and the pointers allow it, and no LDS.
+// All four are HBM-bound byte movers with no LDS.  The scatter runs one workgroup per new
+// token with 16-byte vector moves along the contiguous head_dim rows wherever the row length
+// and the pointers allow it; the RoPE kernels run one wave per (token, head row) so that a
+// decode step's few tokens still spread over thousands of waves.
 #include "rg_common.hpp"
 
 namespace rg {
@@ -113,54 +114,43 @@ __device__ __forceinline__ void rotate_pair(float lo, float hi, float c, float s
   out_hi = e + f;
 }
 
-// Applies RoPE to `nheads` rows of `x` (row stride head_dim) for one token and
-// writes them to dst rows (dst may alias x).  Each thread handles VP
-// consecutive pairs.  dst_row(h) returns the element offset of row h.
-template <typename T, int VP, typename DstRow>
-__device__ __forceinline__ void rope_rows(const typename elem<T>::storage* __restrict__ x,
-                                          typename elem<T>::storage* dst, DstRow dst_row,
-                                          const float* __restrict__ cs, int nheads,
-                                          int head_dim) {
+// One wave per (token, head row); each lane rotates the pairs (i, i + D/2) for
+// i = lane, lane + 64, ...  `src` and `dst` are the row's element offsets (may alias).
+template <typename T>
+__device__ __forceinline__ void rope_row(const typename elem<T>::storage* __restrict__ src,
+                                         typename elem<T>::storage* dst, const float* __restrict__ cs,
+                                         int head_dim, int lane) {
   using E = elem<T>;
   const int half = head_dim / 2;
-  const int groups_per_row = half / VP;
-  const int total = nheads * groups_per_row;
-  for (int i = threadIdx.x; i < total; i += kCacheThreads) {
-    const int h = i / groups_per_row;
-    const int c0 = (i - h * groups_per_row) * VP;
-    const typename E::storage* src = x + (int64_t)h * head_dim;
-    float lo[VP], hi[VP];
-#pragma unroll
-    for (int u = 0; u < VP; ++u) {
-      lo[u] = E::to_f32(src[c0 + u]);
-      hi[u] = E::to_f32(src[half + c0 + u]);
-    }
-    const int64_t d0 = dst_row(h);
-#pragma unroll
-    for (int u = 0; u < VP; ++u) {
-      float ol, oh;
-      rotate_pair(lo[u], hi[u], cs[c0 + u], cs[half + c0 + u], ol, oh);
-      dst[d0 + c0 + u] = E::from_f32(ol);
-      dst[d0 + half + c0 + u] = E::from_f32(oh);
-    }
+  for (int i = lane; i < half; i += 64) {
+    const float lo = E::to_f32(src[i]);
+    const float hi = E::to_f32(src[half + i]);
+    float ol, oh;
+    rotate_pair(lo, hi, cs[i], cs[half + i], ol, oh);
+    dst[i] = E::from_f32(ol);
+    dst[half + i] = E::from_f32(oh);
   }
 }
 
-// In-place RoPE; one workgroup per token (rope.cu:11-42 semantics).
-template <typename T, int VP>
+constexpr int kRowsPerGroup = kCacheThreads / 64;
+
+// In-place RoPE (rope.cu:11-42 semantics); grid (tokens, ceil(heads / 4)), wave = one row.
+template <typename T>
 __global__ __launch_bounds__(kCacheThreads) void rope_inplace_kernel(
     typename elem<T>::storage* __restrict__ x, const float* __restrict__ cos_sin,
     const int32_t* __restrict__ positions, int num_heads, int head_dim) {
   const int t = blockIdx.x;
+  const int h = blockIdx.y * kRowsPerGroup + (threadIdx.x >> 6);
+  if (h >= num_heads) return;
   const int64_t pos = positions[t];
-  auto* row = x + (int64_t)t * num_heads * head_dim;
-  rope_rows<T, VP>(row, row, [=](int h) { return (int64_t)h * head_dim; },
-                   cos_sin + pos * head_dim, num_heads, head_dim);
+  auto* row = x + ((int64_t)t * num_heads + h) * head_dim;
+  rope_row<T>(row, row, cos_sin + pos * head_dim, head_dim, threadIdx.x & 63);
 }
 
-// Fused pass over one new token: rotate q in place, rotate k into the cache,
-// copy v into the cache.
-template <typename T, int VP>
+// Fused pass over the new tokens; grid (tokens, ceil((H + 2*H_kv) / 4)), wave = one row:
+// rows [0, H) rotate q in place, rows [H, H + H_kv) rotate k into the cache, rows
+// [H + H_kv, H + 2*H_kv) copy v into the cache.
+template <typename T>
 __global__ __launch_bounds__(kCacheThreads) void rope_cache_kernel(
     typename elem<T>::storage* __restrict__ q, const typename elem<T>::storage* __restrict__ k,
     const typename elem<T>::storage* __restrict__ v, typename elem<T>::storage* __restrict__ k_cache,
@@ -169,24 +159,31 @@ __global__ __launch_bounds__(kCacheThreads) void rope_cache_kernel(
     int num_heads, CacheGeom g) {
   using S = typename elem<T>::storage;
   const int t = blockIdx.x;
+  const int r = blockIdx.y * kRowsPerGroup + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int D = g.head_dim;
-  const int64_t pos = positions[t];
-  const float* cs = cos_sin + pos * D;
-  S* qrow = q + (int64_t)t * num_heads * D;
-  rope_rows<T, VP>(qrow, qrow, [=](int h) { return (int64_t)h * D; }, cs, num_heads, D);
-
+  const int hkv = g.num_kv_heads;
+  if (r >= num_heads + 2 * hkv) return;
+  if (r < num_heads) {
+    const int64_t pos = positions[t];
+    S* row = q + ((int64_t)t * num_heads + r) * D;
+    rope_row<T>(row, row, cos_sin + pos * D, D, lane);
+    return;
+  }
   const int32_t slot = slot_mapping[t];
-  if (slot < 0) return;
+  if (slot < 0) return;  // padding token (paged_attention.cu:127-128)
   const int64_t blk = slot / g.block_size;
   const int off = slot % g.block_size;
-  const S* krow = k + (int64_t)t * g.num_kv_heads * D;
-  rope_rows<T, VP>(krow, k_cache, [=](int h) { return cache_row(g, blk, h, off); }, cs,
-                   g.num_kv_heads, D);
-  const S* vrow = v + (int64_t)t * g.num_kv_heads * D;
-  for (int i = threadIdx.x; i < g.num_kv_heads * D; i += kCacheThreads) {
-    const int h = i / D;
-    const int d = i - h * D;
-    v_cache[cache_row(g, blk, h, off) + d] = vrow[i];
+  if (r < num_heads + hkv) {
+    const int h = r - num_heads;
+    const int64_t pos = positions[t];
+    rope_row<T>(k + ((int64_t)t * hkv + h) * D, k_cache + cache_row(g, blk, h, off), cos_sin + pos * D, D,
+                lane);
+  } else {
+    const int h = r - num_heads - hkv;
+    const S* src = v + ((int64_t)t * hkv + h) * D;
+    S* dst = v_cache + cache_row(g, blk, h, off);
+    for (int i = lane; i < D; i += 64) dst[i] = src[i];
   }
 }
 
@@ -249,33 +246,23 @@ int launch_scatter(const char* op, const void* k, const void* v, void* k_cache, 
 }
 
 template <typename T>
-int launch_rope_inplace(void* x, const float* cs, const int32_t* pos, int h, int d, int n,
-                        hipStream_t s) {
+int launch_rope_inplace(void* x, const float* cs, const int32_t* pos, int h, int d, int n, hipStream_t s) {
   using S = typename elem<T>::storage;
-  if ((d / 2) % 4 == 0) {
-    hipLaunchKernelGGL((rope_inplace_kernel<T, 4>), dim3(n), dim3(kCacheThreads), 0, s,
-                       static_cast<S*>(x), cs, pos, h, d);
-  } else {
-    hipLaunchKernelGGL((rope_inplace_kernel<T, 1>), dim3(n), dim3(kCacheThreads), 0, s,
-                       static_cast<S*>(x), cs, pos, h, d);
-  }
+  const dim3 grid(n, (h + kRowsPerGroup - 1) / kRowsPerGroup);
+  hipLaunchKernelGGL(rope_inplace_kernel<T>, grid, dim3(kCacheThreads), 0, s, static_cast<S*>(x), cs, pos, h,
+                     d);
   return check_launch("rope");
 }
 
 template <typename T>
 int launch_rope_cache(void* q, const void* k, const void* v, void* kc, void* vc, const float* cs,
-                      const int32_t* pos, const int32_t* slots, int h, CacheGeom g, int n,
-                      hipStream_t s) {
+                      const int32_t* pos, const int32_t* slots, int h, CacheGeom g, int n, hipStream_t s) {
   using S = typename elem<T>::storage;
-  if ((g.head_dim / 2) % 4 == 0) {
-    hipLaunchKernelGGL((rope_cache_kernel<T, 4>), dim3(n), dim3(kCacheThreads), 0, s,
-                       static_cast<S*>(q), static_cast<const S*>(k), static_cast<const S*>(v),
-                       static_cast<S*>(kc), static_cast<S*>(vc), cs, pos, slots, h, g);
-  } else {
-    hipLaunchKernelGGL((rope_cache_kernel<T, 1>), dim3(n), dim3(kCacheThreads), 0, s,
-                       static_cast<S*>(q), static_cast<const S*>(k), static_cast<const S*>(v),
-                       static_cast<S*>(kc), static_cast<S*>(vc), cs, pos, slots, h, g);
-  }
+  const int rows = h + 2 * g.num_kv_heads;
+  const dim3 grid(n, (rows + kRowsPerGroup - 1) / kRowsPerGroup);
+  hipLaunchKernelGGL(rope_cache_kernel<T>, grid, dim3(kCacheThreads), 0, s, static_cast<S*>(q),
+                     static_cast<const S*>(k), static_cast<const S*>(v), static_cast<S*>(kc), static_cast<S*>(vc),
+                     cs, pos, slots, h, g);
   return check_launch("rope_reshape_and_cache");
 }
 
@@ -284,7 +271,7 @@ int launch_rope_cache(void* q, const void* k, const void* v, void* kc, void* vc,
 int probe_cache_kernels() {
   hipFuncAttributes a;
   if (hipFuncGetAttributes(&a, reinterpret_cast<const void*>(scatter_kv_vec16)) != hipSuccess ||
-      hipFuncGetAttributes(&a, reinterpret_cast<const void*>(rope_cache_kernel<bf16_t, 4>)) !=
+      hipFuncGetAttributes(&a, reinterpret_cast<const void*>(rope_cache_kernel<bf16_t>)) !=
           hipSuccess) {
     return fail(RG_ERR_HIP, "failed to load the KV-cache kernels: %s",
                 hipGetErrorString(hipGetLastError()));

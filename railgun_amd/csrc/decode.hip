@@ -686,86 +686,90 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
   }
 }
 
-// One workgroup per segment (sequence, kv-head): merges the partials of workers
-// worker_of(first unit) .. worker_of(last unit) and writes the G output rows.
+// One workgroup per (segment, head of the group): merges the partials of workers
+// worker_of(first unit) .. worker_of(last unit) of the segment and writes one output row.
+// Threads split over (pairs of dims) x (groups of partials).  Each thread folds its strided
+// subset of partials with an online rescale, so the (m, l, acc) loads of all its partials are
+// issued together; the groups are then combined through LDS.
+constexpr int kMergeThreads = 256;
+
 template <typename T, int D, int G>
-__global__ __launch_bounds__(256) void decode_stream_merge_kernel(StreamArgs a,
-                                                                  const int32_t* __restrict__ context_lens) {
+__global__ __launch_bounds__(kMergeThreads) void decode_stream_merge_kernel(StreamArgs a,
+                                                                           const int32_t* __restrict__ context_lens) {
   using S = uint16_t;
-  __shared__ float m_lds[G];
-  __shared__ float inv_lds[G];
-  const int kvh = blockIdx.x;
+  constexpr int NPAIR = D / 2;                  // dim pairs per row
+  constexpr int NGRP = kMergeThreads / NPAIR;   // partial groups
+  __shared__ float2 acc_lds[NGRP][NPAIR];
+  __shared__ float ml_lds[NGRP][2];
+
+  const int h = blockIdx.x % G;
+  const int kvh = blockIdx.x / G;
   const int s = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int hkv = a.num_kv_heads;
-  S* out = static_cast<S*>(a.out) + ((int64_t)s * a.num_heads + (int64_t)kvh * G) * D;
+  S* out = static_cast<S*>(a.out) + ((int64_t)s * a.num_heads + (int64_t)kvh * G + h) * D;
   const int nblk = seq_blocks(context_lens, s, a.max_blocks);
   if (nblk == 0) {
-    for (int i = tid; i < G * D; i += 256) out[i] = 0;
+    for (int i = tid; i < D; i += kMergeThreads) out[i] = 0;
     return;
   }
-  // Every wave scans (cheap) so that all threads know U and the segment's first unit.
-  int s_found;
-  int64_t seq_start;
-  const int64_t U = scan_units(context_lens, a.batch, a.max_blocks, hkv, lane, -1, s_found, seq_start);
-  int64_t ubeg = 0;
-  {
-    int64_t base = 0;
-    for (int c0 = 0; c0 < s; c0 += 64) {
-      const int ss = c0 + lane;
-      const int64_t n = ss < s ? (int64_t)seq_blocks(context_lens, ss, a.max_blocks) * hkv : 0;
-      base += __shfl(wave_incl_scan(n, lane), 63, 64);
-    }
-    ubeg = base + (int64_t)kvh * nblk;
+  // Total units and the segment's first unit (one pass over the context lengths).
+  int64_t U = 0, before = 0;
+  for (int c0 = 0; c0 < a.batch; c0 += 64) {
+    const int ss = c0 + lane;
+    const int64_t n = ss < a.batch ? (int64_t)seq_blocks(context_lens, ss, a.max_blocks) * hkv : 0;
+    const int64_t incl = wave_incl_scan(n, lane);
+    if (c0 <= s && s < c0 + 64) before = U + __shfl(incl - n, s - c0, 64);
+    U += __shfl(incl, 63, 64);
   }
+  const int64_t ubeg = before + (int64_t)kvh * nblk;
   const int64_t W = min<int64_t>(a.num_workers, U);
   const int64_t first = worker_of(ubeg, U, W);
   const int64_t last = worker_of(ubeg + nblk - 1, U, W);
-  const int64_t g = (int64_t)s * hkv + kvh;
+  const int64_t pbase = first + (int64_t)s * hkv + kvh;  // partial index of worker `first`
   const int np = (int)(last - first + 1);
 
-  // Per-head max and normaliser over the partials (every thread computes them; the loads
-  // are the same addresses across the workgroup).
-  float M[G], L[G];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    M[h] = -INFINITY;
-    L[h] = 0.f;
+  const int pair = tid % NPAIR;
+  const int grp = tid / NPAIR;
+  float m = -INFINITY, l = 0.f;
+  float2 acc = make_float2(0.f, 0.f);
+#pragma unroll 4
+  for (int q = grp; q < np; q += NGRP) {
+    const int64_t pi = pbase + q;
+    const float mq = a.part_ml[pi * (2 * G) + 2 * h];
+    const float lq = a.part_ml[pi * (2 * G) + 2 * h + 1];
+    const float2 v = *reinterpret_cast<const float2*>(a.part_acc + pi * (G * D) + h * D + 2 * pair);
+    const float mn = fmaxf(m, mq);
+    const float fo = exp2f(m - mn);  // 0 for the first partial (m = -inf)
+    const float fq = exp2f(mq - mn);
+    l = l * fo + lq * fq;
+    acc.x = acc.x * fo + v.x * fq;
+    acc.y = acc.y * fo + v.y * fq;
+    m = mn;
   }
-  for (int q = 0; q < np; ++q) {
-    const float* pm = a.part_ml + (first + q + g) * (2 * G);
-#pragma unroll
-    for (int h = 0; h < G; ++h) M[h] = fmaxf(M[h], pm[2 * h]);
-  }
-  for (int q = 0; q < np; ++q) {
-    const float* pm = a.part_ml + (first + q + g) * (2 * G);
-#pragma unroll
-    for (int h = 0; h < G; ++h) L[h] += exp2f(pm[2 * h] - M[h]) * pm[2 * h + 1];
-  }
-  if (tid == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      m_lds[h] = M[h];
-      inv_lds[h] = L[h] != 0.f ? 1.f / L[h] : 1.f;
-    }
+  acc_lds[grp][pair] = acc;
+  if (pair == 0) {
+    ml_lds[grp][0] = m;
+    ml_lds[grp][1] = l;
   }
   __syncthreads();
-  for (int idx = tid; idx < G * D / 2; idx += 256) {
-    const int h = idx / (D / 2);
-    const int d = (idx % (D / 2)) * 2;
-    const float Mh = m_lds[h];
-    float o0 = 0.f, o1 = 0.f;
-    for (int q = 0; q < np; ++q) {
-      const int64_t pi = first + q + g;
-      const float f = exp2f(a.part_ml[pi * (2 * G) + 2 * h] - Mh);
-      const float2 v = *reinterpret_cast<const float2*>(a.part_acc + pi * (G * D) + h * D + d);
-      o0 += f * v.x;
-      o1 += f * v.y;
+  if (grp == 0) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int g2 = 0; g2 < NGRP; ++g2) M = fmaxf(M, ml_lds[g2][0]);
+    float L = 0.f, ox = 0.f, oy = 0.f;
+#pragma unroll
+    for (int g2 = 0; g2 < NGRP; ++g2) {
+      const float mg = ml_lds[g2][0];
+      const float f = mg == -INFINITY ? 0.f : exp2f(mg - M);
+      L += f * ml_lds[g2][1];
+      ox += f * acc_lds[g2][pair].x;
+      oy += f * acc_lds[g2][pair].y;
     }
-    const float inv = inv_lds[h];
-    const uint32_t packed = (uint32_t)elem<T>::from_f32(o0 * inv) | ((uint32_t)elem<T>::from_f32(o1 * inv) << 16);
-    *reinterpret_cast<uint32_t*>(out + h * D + d) = packed;
+    const float inv = L != 0.f ? 1.f / L : 1.f;
+    const uint32_t packed = (uint32_t)elem<T>::from_f32(ox * inv) | ((uint32_t)elem<T>::from_f32(oy * inv) << 16);
+    *reinterpret_cast<uint32_t*>(out + 2 * pair) = packed;
   }
 }
 
@@ -1044,8 +1048,8 @@ void launch_stream(const StreamArgs& sa, const DecodeArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((decode_stream_kernel<T, D, G>), dim3(sa.num_workers), dim3(64), 0, s, sa,
                      static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.k_cache),
                      static_cast<const uint16_t*>(a.v_cache), a.block_table, a.context_lens);
-  hipLaunchKernelGGL((decode_stream_merge_kernel<T, D, G>), dim3(sa.num_kv_heads, sa.batch), dim3(256), 0, s,
-                     sa, a.context_lens);
+  hipLaunchKernelGGL((decode_stream_merge_kernel<T, D, G>), dim3(sa.num_kv_heads * G, sa.batch),
+                     dim3(kMergeThreads), 0, s, sa, a.context_lens);
 }
 
 template <typename T, int D>
