@@ -180,10 +180,11 @@ template <> struct mfma16<f16_t> {
   }
 };
 
-// DPP helpers: `ctrl` is a DPP control word (quad_perm / row_ror).
+// DPP helpers: `ctrl` is a DPP control word (quad_perm / row_ror).  Every lane of the
+// patterns used here has a valid source lane, so no "old" value is needed.
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 // Max / sum over the 16 lanes of a row, result in every lane of the row.
 __device__ __forceinline__ float row16_max(float v) {
@@ -218,7 +219,7 @@ constexpr int kBS = 16;  // tokens per KV block on the MFMA path
 #define RG_DEC_WAVES 4
 #endif
 #ifndef RG_DEC_PREFETCH
-#define RG_DEC_PREFETCH 2
+#define RG_DEC_PREFETCH 1
 #endif
 constexpr int kWaves = RG_DEC_WAVES;
 constexpr int kPrefetch = RG_DEC_PREFETCH;
@@ -305,12 +306,15 @@ struct DecodeTile {
       l_run[r] = l_run[r] * al[r] + pr[r];
       m_run[r] = m_new;
     }
+    // The running max of a head moves on few blocks only: skip the rescale of acc when it
+    // moved for no head (a wave-uniform decision).
+    const bool rescale = __ballot(al[0] != 1.f || al[1] != 1.f || al[2] != 1.f || al[3] != 1.f) != 0;
     if (seg < HG) {
       *reinterpret_cast<float4*>(&p_lds[col * GP + 4 * seg]) = make_float4(pr[0], pr[1], pr[2], pr[3]);
       if (col == 0) *reinterpret_cast<float4*>(&alpha_lds[4 * seg]) = make_float4(al[0], al[1], al[2], al[3]);
     }
     wave_lds_sync();
-    {
+    if (rescale) {
       float alh[G];
 #pragma unroll
       for (int h = 0; h < G; ++h) alh[h] = alpha_lds[h];
@@ -319,23 +323,29 @@ struct DecodeTile {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] *= alh[h];
     }
+    float vf[NV][8];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) MF::unpack8(vr[i], vf[i]);
+    if (tail) {
+      // Rows past the context may hold any bit pattern; keep them out of 0*x.
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        if (tok0 + i * TPI + vrow >= ctx) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vf[i][e] = 0.f;
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int t = i * TPI + vrow;
-      float vf[8];
-      MF::unpack8(vr[i], vf);
-      if (tail && tok0 + t >= ctx) {
-        // Rows past the context may hold any bit pattern; keep them out of 0*x.
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vf[e] = 0.f;
-      }
       float ph[G];
 #pragma unroll
       for (int h = 0; h < G; ++h) ph[h] = p_lds[t * GP + h];
 #pragma unroll
       for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] += ph[h] * vf[e];
+        for (int e = 0; e < 8; ++e) acc[h][e] += ph[h] * vf[i][e];
     }
   }
   // Sums acc over the TPI token rows (result valid in lanes with vrow == 0) and l over the
@@ -495,6 +505,13 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 // consecutive).  decode_stream_merge_kernel combines the partials of each segment.  When
 // U < W only the first U workers are used, so every worker of a segment's range owns units.
 
+// Optional occupancy floor of the stream-K kernel (waves per SIMD).
+#if defined(RG_SK_OCC) && RG_SK_OCC > 0
+#define RG_SK_OCCUPANCY __attribute__((amdgpu_waves_per_eu(RG_SK_OCC)))
+#else
+#define RG_SK_OCCUPANCY
+#endif
+
 struct StreamArgs {
   void* out;
   float* part_acc;   // [num_partials, G, D]
@@ -554,7 +571,7 @@ __device__ __forceinline__ int64_t scan_units(const int32_t* ctxl, int batch, in
 }
 
 template <typename T, int D, int G>
-__global__ __launch_bounds__(64) void decode_stream_kernel(
+__global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
     StreamArgs a, const uint16_t* __restrict__ q_ptr, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens) {
