@@ -211,3 +211,55 @@ def test_config3_v2_matches_v1(device, kernels):
     assert_close(v2, v1, "bf16", "v2 vs v1")
     want = orc.cpu_attention_gathered(q, kc, vc, w.block_table, w.context_lens, w.scale, w.dtype, nthreads=8)
     assert_close(v2, want, "bf16", "v2 vs oracle")
+
+
+def _golden(name):
+    import os
+    import sys
+
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    if here not in sys.path:
+        sys.path.insert(0, here)
+    import make_fixtures  # noqa: E402
+
+    return make_fixtures, np.load(os.path.join(here, name))
+
+
+def test_config1_against_golden_fixture(device, kernels):
+    """BASELINE configs[0] on the GPU against the committed float64 fixture: every decode entry
+    at 1e-4, and reshape_and_cache of the 4 new tokens (with and without a slot of -1) bit-exact
+    by the SHA-256 of the whole resulting caches."""
+    import hashlib
+
+    mf, f = _golden("config1_fp32.npz")
+    w, q, kc, vc, k_new, v_new = mf.config1_inputs()
+    assert mf.sha(q, kc, vc, w.block_table, w.context_lens, k_new, v_new) == str(f["input_sha256"])
+    inp = dict(ctx=w.context_lens, bt=w.block_table, q=q, kc=kc, vc=vc, H=32, Hkv=8, D=64, bs=16, mb=w.max_blocks,
+               dt="f32", scale=w.scale, dq=to_dev(q, "f32", device), dkc=to_dev(kc, "f32", device),
+               dvc=to_dev(vc, "f32", device), dbt=i32(w.block_table, device), dctx=i32(w.context_lens, device))
+    want = f["expected_out_f64"]
+    for ws in (False, True):
+        for entry in ("v1", "v1_plus"):
+            assert_close(gpu_v1(kernels, inp, ws, entry), want, "f32", f"{entry} ws={ws}")
+    assert_close(gpu_v2(kernels, inp, 64), want, "f32", "v2")
+    for slots, key in ((f["slot_mapping"], "cache_after_sha256"), (f["slot_mapping_skip"], "cache_after_skip_sha256")):
+        dkc, dvc = to_dev(kc, "f32", device), to_dev(vc, "f32", device)
+        kernels.launch_reshape_and_cache(to_dev(k_new, "f32", device), to_dev(v_new, "f32", device), dkc, dvc,
+                                         i32(slots, device), 8, 64, 16, 4)
+        torch.cuda.synchronize()
+        h = hashlib.sha256()
+        h.update(np.ascontiguousarray(dkc.cpu().numpy()).tobytes())
+        h.update(np.ascontiguousarray(dvc.cpu().numpy()).tobytes())
+        assert h.hexdigest() == str(f[key])
+
+
+def test_bf16_decode_against_golden_fixture(device, kernels):
+    mf, f = _golden("decode_bf16_small.npz")
+    ctx, bt, q, kc, vc = mf.small_bf16_inputs()
+    assert mf.sha(q, kc, vc, bt, ctx) == str(f["input_sha256"])
+    inp = dict(ctx=ctx, bt=bt, q=q, kc=kc, vc=vc, H=32, Hkv=8, D=128, bs=16, mb=bt.shape[1], dt="bf16",
+               scale=1 / math.sqrt(128), dq=to_dev(q, "bf16", device), dkc=to_dev(kc, "bf16", device),
+               dvc=to_dev(vc, "bf16", device), dbt=i32(bt, device), dctx=i32(ctx, device))
+    for ws in (False, True):
+        assert_close(gpu_v1(kernels, inp, ws), f["expected_out_f64"], "bf16", f"ws={ws}")
+    assert_close(gpu_v2(kernels, inp, 32), f["expected_out_f64"], "bf16", "v2")
