@@ -150,7 +150,7 @@ template <> struct mfma32<f16_t> {
 constexpr int kPT = 32;               // queries per tile and keys per key tile
 constexpr int kPWaves = 4;            // one wave per q-head of the group (GQA 4)
 constexpr int kPThreads = kPWaves * 64;
-constexpr int kVtRow = kPT + 2;       // V^T row stride in elements (odd dword count: no bank conflicts)
+constexpr int kBlk = 16;              // KV block size on the MFMA path (two blocks per key tile)
 
 // Tile `ti` of the longest-first order: rank r = 0 holds the last tile of every sequence,
 // rank 1 the one before, ...; within a rank, sequences in order.  Returns false if `ti` is
@@ -187,6 +187,43 @@ __device__ __forceinline__ bool tile_of(const int32_t* cu, int num_seqs, int ti,
   return false;
 }
 
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+#define RG_LDS __attribute__((address_space(3)))
+
+#ifndef RG_PF_STAGES
+#define RG_PF_STAGES 3
+#endif
+
+// 16 bytes per lane from global memory straight into LDS at lds_addr + 16 * lane (the
+// vector memory counter tracks completion).  Issued through asm so that the compiler does
+// not add a full vector-memory wait in front of every LDS read; the kernel orders the
+// copies itself with wait_tiles + tile_barrier.
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
+}
+// Workgroup barrier without the memory fence of __syncthreads (which would also wait for
+// every prefetch in flight); the asm statements keep the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void tile_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+constexpr int kPStages = RG_PF_STAGES;  // K/V tiles in flight (ring in LDS)
+
+// LDS image of one key tile: K as the MFMA A-operand image (chunk i of lane l at
+// i*1024 + l*16), V row-major [key][D] with the 16-byte chunks of row `key` XOR-swizzled by
+// 2*(key & 3) so that the transposing reads of four consecutive rows hit distinct banks.
+template <int D>
+struct PTile {
+  static constexpr int NKC = D / 16;
+  static constexpr int KBYTES = NKC * 1024;
+  static constexpr int VBYTES = kPT * D * 2;
+  static constexpr int BYTES = KBYTES + VBYTES;
+  static constexpr int VCHUNKS = D / 8;  // 16-byte chunks per V row
+  __device__ static __forceinline__ int vchunk(int key, int c) { return c ^ (2 * (key & 3)); }
+};
+
 template <typename T, int D>
 __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(
     PrefillArgs a, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
@@ -194,16 +231,19 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(
     const int32_t* __restrict__ context_lens, const int32_t* __restrict__ cu_seqlens) {
   using MF = mfma32<T>;
   using S = uint16_t;
+  using TL = PTile<D>;
   constexpr int G = kPWaves;
-  constexpr int NKC = D / 16;      // 16-element d chunks = QK MFMAs per key tile
+  constexpr int NKC = TL::NKC;     // 16-element d chunks = QK MFMAs per key tile
   constexpr int NDB = D / 32;      // 32-row d blocks of O^T
-  constexpr int VITEMS = 16 * (D / 8);  // (key pair, 8-d chunk) items of a V tile
-  constexpr int VPER = (VITEMS + kPThreads - 1) / kPThreads;
-  __shared__ uint32_t vt_lds[2][D * kVtRow / 2];
+  constexpr int KI = NKC;          // global->LDS instructions for K (1 KB each)
+  constexpr int VI = TL::VBYTES / 1024;  // ... and for V
+  static_assert(KI % kPWaves == 0 && VI % kPWaves == 0, "tile loads split evenly over the waves");
+  constexpr int LOADS_PER_WAVE = (KI + VI) / kPWaves;
+  __shared__ __attribute__((aligned(16))) char lds[kPStages * TL::BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hkv = a.num_kv_heads;
   const int kvh = blockIdx.x % hkv;
   const int ti = blockIdx.x / hkv;
@@ -234,49 +274,37 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < NKC; ++i) qb[i] = q_valid ? qr[2 * i + hh] : make_uint4(0, 0, 0, 0);
   }
+  // Settle Q here, once: otherwise the first use inside the tile loop would wait for every
+  // vector-memory operation in flight (the tile prefetches included) on every iteration.
+  __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
   const int32_t* bt = block_table + (int64_t)s * a.max_blocks;
-  const int bs = a.block_size;
-  const int64_t head_off = (int64_t)kvh * bs * D;
-  auto key_row = [&](int key) -> int64_t {
-    const int b = min(key / bs, a.max_blocks - 1);
-    return (int64_t)bt[b] * a.kv_stride + head_off + (int64_t)(key % bs) * D;
-  };
-  // K operand (A) of key tile kt: lane holds K[key 32kt + j][16i + 8hh .. +8].
-  auto load_k = [&](int kt, uint4 (&kr)[NKC]) {
-    const uint4* kp = reinterpret_cast<const uint4*>(kc + key_row(kt * kPT + j));
+  const int64_t head_off = (int64_t)kvh * kBlk * D;
+  const int nkt = pos_max / kPT + 1;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)((RG_LDS char*)lds);
+
+  // Issues this wave's share of the global->LDS copies of key tile kt into ring stage st.
+  // A key tile spans the two 16-token blocks bt[2kt], bt[2kt+1] (scalar loads); keys past
+  // the last position read the last valid key instead (they are masked).
+  auto issue_tile = [&](int kt, int st) {
+    const int last_blk = pos_max / kBlk;
+    const int64_t blk0 = (int64_t)bt[min(2 * kt, last_blk)] * a.kv_stride + head_off;
+    const int64_t blk1 = (int64_t)bt[min(2 * kt + 1, last_blk)] * a.kv_stride + head_off;
+    auto row = [&](int kl) -> int64_t {  // kl: key within the tile
+      const int key = min(kt * kPT + kl, pos_max) - kt * kPT;
+      return (key < kBlk ? blk0 : blk1) + (int64_t)(key & (kBlk - 1)) * D;
+    };
+    const uint32_t sbase = lds_base + st * TL::BYTES;
 #pragma unroll
-    for (int i = 0; i < NKC; ++i) kr[i] = kp[2 * i + hh];
-  };
-  // V rows of the tile for this thread's items: keys 2kp and 2kp+1, dims 8dc..8dc+8.
-  auto load_v = [&](int kt, uint4 (&v0)[VPER], uint4 (&v1)[VPER]) {
-#pragma unroll
-    for (int u = 0; u < VPER; ++u) {
-      const int item = tid + u * kPThreads;
-      const int kp = item & 15;
-      const int dc = item >> 4;
-      const int key = kt * kPT + 2 * kp;
-      if (item >= VITEMS) break;
-      v0[u] = key <= pos_max ? *reinterpret_cast<const uint4*>(vc + key_row(key) + 8 * dc) : make_uint4(0, 0, 0, 0);
-      v1[u] = key + 1 <= pos_max ? *reinterpret_cast<const uint4*>(vc + key_row(key + 1) + 8 * dc)
-                                 : make_uint4(0, 0, 0, 0);
-    }
-  };
-  // Transposed store: V^T[8dc + e][2kp .. 2kp+1] = (V[2kp][8dc+e], V[2kp+1][8dc+e]).
-  auto store_vt = [&](int buf, const uint4 (&v0)[VPER], const uint4 (&v1)[VPER]) {
-#pragma unroll
-    for (int u = 0; u < VPER; ++u) {
-      const int item = tid + u * kPThreads;
-      const int kp = item & 15;
-      const int dc = item >> 4;
-      if (item >= VITEMS) break;
-      const uint32_t a4[4] = {v0[u].x, v0[u].y, v0[u].z, v0[u].w};
-      const uint32_t b4[4] = {v1[u].x, v1[u].y, v1[u].z, v1[u].w};
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        const uint32_t lo = (a4[e2] & 0xffffu) | (b4[e2] << 16);
-        const uint32_t hi = (a4[e2] >> 16) | (b4[e2] & 0xffff0000u);
-        vt_lds[buf][((8 * dc + 2 * e2) * kVtRow) / 2 + kp] = lo;
-        vt_lds[buf][((8 * dc + 2 * e2 + 1) * kVtRow) / 2 + kp] = hi;
+    for (int u = 0; u < LOADS_PER_WAVE; ++u) {
+      const int ins = w + u * kPWaves;
+      if (ins < KI) {
+        lds_dma16(kc + row(j) + 16 * ins + 8 * hh, __builtin_amdgcn_readfirstlane(sbase + ins * 1024));
+      } else {
+        const int vi = ins - KI;
+        const int kl = vi * (1024 / (D * 2)) + lane / TL::VCHUNKS;  // key within the tile
+        const int pch = lane % TL::VCHUNKS;                          // physical chunk position
+        lds_dma16(vc + row(kl) + 8 * TL::vchunk(kl, pch),
+                  __builtin_amdgcn_readfirstlane(sbase + TL::KBYTES + vi * 1024));
       }
     }
   };
@@ -288,28 +316,30 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(
     for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  const int nkt = pos_max / kPT + 1;
-  uint4 kr[NKC];
-  uint4 v0[VPER], v1[VPER];
-  load_k(0, kr);
-  load_v(0, v0, v1);
-  store_vt(0, v0, v1);
-  __syncthreads();
+  // Prologue: stages 0 .. kPStages-2 (tiles past the end repeat the last tile).
+#pragma unroll
+  for (int p = 0; p < kPStages - 1; ++p) issue_tile(min(p, nkt - 1), p);
 
   for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < nkt;
-    uint4 kn[NKC];
-    if (more) {
-      load_k(kt + 1, kn);
-      load_v(kt + 1, v0, v1);
-    }
+    const int st = kt % kPStages;
+    // This wave's loads of tile kt are the oldest kPStages-1 groups outstanding: wait for
+    // them, then the barrier makes every wave's part visible (and retires stage kt-1).
+    static_assert(LOADS_PER_WAVE * (kPStages - 2) < 16, "vmcnt immediate");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((LOADS_PER_WAVE * (kPStages - 2)) | 0x70 | 0xF00);
+    tile_barrier();
+    issue_tile(min(kt + kPStages - 1, nkt - 1), (kt + kPStages - 1) % kPStages);
+
+    const char* base = lds + st * TL::BYTES;
     // S^T = K Q^T: c[4jb + r] is key 8jb + 4hh + r of the tile for query j.
     f32x16_t c;
 #pragma unroll
     for (int v = 0; v < 16; ++v) c[v] = 0.f;
 #pragma unroll
-    for (int i = 0; i < NKC; ++i) c = MF::run(kr[i], qb[i], c);
+    for (int i = 0; i < NKC; ++i) {
+      const uint4 ka = *reinterpret_cast<const uint4*>(base + i * 1024 + lane * 16);
+      c = MF::run(ka, qb[i], c);
+    }
 
     const int k0 = kt * kPT;
     const bool masked = k0 + kPT - 1 > pos_min;
@@ -343,26 +373,34 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
     }
-    // O^T += V^T P^T over the tile's keys, in two 16-key MFMA steps.
-    const uint32_t* vt = vt_lds[buf];
+    // O^T += V^T P^T in two 16-key MFMA steps.  The A operand is read with the transposing
+    // LDS load: in each 16-lane group, lane 4e+q points at V[key0 + e][d0 + 4q .. +4] and
+    // lane i receives V[key0 .. key0+3][d0 + i].
+    const char* vbase = base + TL::KBYTES;
+    const int grp = lane >> 4;
+    const int e = (lane >> 2) & 3;
+    const int qq = lane & 3;
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       const uint4 pb = make_uint4(pk[4 * n], pk[4 * n + 1], pk[4 * n + 2], pk[4 * n + 3]);
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const int d = 32 * db + j;
-        const int e0 = (d * kVtRow + 16 * n + 4 * hh) / 2;   // keys 16n+4hh .. +4
-        const int e1 = (d * kVtRow + 16 * n + 8 + 4 * hh) / 2;  // keys 16n+8+4hh .. +4
-        const uint4 va = make_uint4(vt[e0], vt[e0 + 1], vt[e1], vt[e1 + 1]);
+        const int d = 32 * db + 16 * (grp & 1) + 4 * qq;   // this lane's address column
+        v4i16_t part[2];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int key = 16 * n + 8 * half + 4 * (grp >> 1) + e;
+          const int off = key * (D * 2) + TL::vchunk(key, d >> 3) * 16 + (d & 7) * 2;
+          part[half] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((RG_LDS v4i16_t*)(vbase + off));
+        }
+        uint4 va;
+        va.x = (uint32_t)(uint16_t)part[0][0] | ((uint32_t)(uint16_t)part[0][1] << 16);
+        va.y = (uint32_t)(uint16_t)part[0][2] | ((uint32_t)(uint16_t)part[0][3] << 16);
+        va.z = (uint32_t)(uint16_t)part[1][0] | ((uint32_t)(uint16_t)part[1][1] << 16);
+        va.w = (uint32_t)(uint16_t)part[1][2] | ((uint32_t)(uint16_t)part[1][3] << 16);
         o[db] = MF::run(va, pb, o[db]);
       }
     }
-    if (more) {
-      store_vt(buf ^ 1, v0, v1);
-#pragma unroll
-      for (int i = 0; i < NKC; ++i) kr[i] = kn[i];
-    }
-    __syncthreads();
   }
 
   // Normalise (the two halves of a query's keys live in lanes l and l ^ 32) and write.
@@ -440,7 +478,7 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
                 max_blocks_per_seq, num_seqs, num_tokens, stride};
   hipStream_t s = as_stream(stream);
   const int eb = dtype_bytes(dtype);
-  if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && num_heads == 4 * num_kv_heads &&
+  if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && num_heads == 4 * num_kv_heads && block_size == kBlk &&
       (head_dim == 64 || head_dim == 128) && max_blocks_per_seq > 0 && aligned16(query) &&
       aligned16(key_cache) && aligned16(value_cache) && (stride * eb) % 16 == 0 &&
       (reinterpret_cast<uintptr_t>(output) & 7u) == 0) {
