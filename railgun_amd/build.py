@@ -29,6 +29,10 @@ HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", f"-I{ROOT}/include",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall",
 ]
+# Per-source additions.  prefill.hip keeps its MFMA accumulators in ordinary VGPRs: with the
+# default heuristic they land in AGPRs and are copied to VGPRs around the softmax rescale
+# on every key tile.
+SOURCE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 CPP_TESTS = ["test_paged_attention_op"]
 
 
@@ -45,7 +49,8 @@ def _run(cmd: list[str], cwd: str | None = None) -> None:
 def build_library() -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     objs = [os.path.join(BUILD_DIR, os.path.splitext(s)[0] + ".o") for s in HIP_SOURCES]
-    jobs = [[HIPCC, *HIPCC_FLAGS, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(HIP_SOURCES, objs)]
+    jobs = [[HIPCC, *HIPCC_FLAGS, *SOURCE_FLAGS.get(s, []), "-c", os.path.join(CSRC, s), "-o", o]
+            for s, o in zip(HIP_SOURCES, objs)]
     with ThreadPoolExecutor(max_workers=min(4, len(jobs))) as ex:
         for f in [ex.submit(_run, j) for j in jobs]:
             f.result()

@@ -1028,15 +1028,6 @@ int32_t v1_num_partitions(const Shape& sh) {
 #define RG_SK_WAVES_PER_CU 8
 #endif
 
-int device_cu_count() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
-    n = 256;
-  }
-  return n;
-}
-
 int32_t stream_workers(const Shape& sh) {
   const int64_t want = (int64_t)device_cu_count() * RG_SK_WAVES_PER_CU;
   const int64_t units_max = (int64_t)sh.B * sh.Hkv * std::max(sh.MB, 1);

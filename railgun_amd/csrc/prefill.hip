@@ -37,6 +37,7 @@ struct PrefillArgs {
   int32_t max_blocks;
   int32_t num_seqs;
   int32_t num_tokens;
+  int32_t rank_tiles;  // ceil(max_query_len / 32): tile ranks launched per sequence (MFMA path)
   int64_t kv_stride;
 };
 
@@ -152,46 +153,11 @@ constexpr int kPWaves = 4;            // one wave per q-head of the group (GQA 4
 constexpr int kPThreads = kPWaves * 64;
 constexpr int kBlk = 16;              // KV block size on the MFMA path (two blocks per key tile)
 
-// Tile `ti` of the longest-first order: rank r = 0 holds the last tile of every sequence,
-// rank 1 the one before, ...; within a rank, sequences in order.  Returns false if `ti` is
-// past the last tile.  All lanes of the wave get the same (s, t).
-__device__ __forceinline__ bool tile_of(const int32_t* cu, int num_seqs, int ti, int lane, int& s_out,
-                                        int& t_out) {
-  int maxn = 0;
-  for (int c0 = 0; c0 < num_seqs; c0 += 64) {
-    const int sidx = c0 + lane;
-    const int n = sidx < num_seqs ? (cu[sidx + 1] - cu[sidx] + kPT - 1) / kPT : 0;
-    maxn = max(maxn, n);
-  }
-  maxn = (int)wave_max((float)maxn);
-  int base = 0;
-  for (int r = 0; r < maxn; ++r) {
-    for (int c0 = 0; c0 < num_seqs; c0 += 64) {
-      const int sidx = c0 + lane;
-      const int n = sidx < num_seqs ? (cu[sidx + 1] - cu[sidx] + kPT - 1) / kPT : 0;
-      const uint64_t has = __ballot(n > r);
-      const int cnt = __popcll(has);
-      if (ti < base + cnt) {
-        // the (ti - base)-th set bit
-        uint64_t m = has;
-        for (int k = 0; k < ti - base; ++k) m &= m - 1;
-        const int l = __ffsll((unsigned long long)m) - 1;
-        s_out = c0 + l;
-        const int nl = __shfl(n, l, 64);
-        t_out = nl - 1 - r;
-        return true;
-      }
-      base += cnt;
-    }
-  }
-  return false;
-}
-
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 #define RG_LDS __attribute__((address_space(3)))
 
 #ifndef RG_PF_STAGES
-#define RG_PF_STAGES 3
+#define RG_PF_STAGES 4
 #endif
 
 // 16 bytes per lane from global memory straight into LDS at lds_addr + 16 * lane (the
@@ -210,6 +176,18 @@ __device__ __forceinline__ void tile_barrier() {
   asm volatile("" ::: "memory");
 }
 constexpr int kPStages = RG_PF_STAGES;  // K/V tiles in flight (ring in LDS)
+constexpr float kSlack = 8.f;           // log2 headroom of the lazy softmax rescale
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+// Two probabilities as one packed operand word (v_cvt_pk_*_f32, round to nearest even).
+template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
+}
+template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)lo, (_Float16)hi});
+}
 
 // LDS image of one key tile: K as the MFMA A-operand image (chunk i of lane l at
 // i*1024 + l*16), V row-major [key][D] with the 16-byte chunks of row `key` XOR-swizzled by
@@ -225,7 +203,7 @@ struct PTile {
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(
+__global__ __launch_bounds__(kPThreads, 2) void prefill_mfma_kernel(
     PrefillArgs a, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, const int32_t* __restrict__ cu_seqlens) {
@@ -245,17 +223,30 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hkv = a.num_kv_heads;
+  // Persistent workgroups: workgroup g serves kv-head g % hkv (so, with workgroups placed on
+  // the XCDs round-robin, each head's K/V stays in few L2s) and, among the Q = gridDim / hkv
+  // workgroups of that head, takes the work items (rank r, sequence s) = u = r * num_seqs + s
+  // of round i in snake order (u = i * Q + q, or i * Q + Q - 1 - q on odd rounds).  Rank r
+  // is the r-th query tile of s counted from its last one, so the longest tiles come first;
+  // the last rank also takes every tile further from the end (when max_query_len
+  // understates a sequence).
   const int kvh = blockIdx.x % hkv;
-  const int ti = blockIdx.x / hkv;
-  int s, t;
-  if (!tile_of(cu_seqlens, a.num_seqs, ti, lane, s, t)) return;
-  s = __builtin_amdgcn_readfirstlane(s);
-  t = __builtin_amdgcn_readfirstlane(t);
-
+  const int nq_wg = gridDim.x / hkv;
+  const int qw = blockIdx.x / hkv;
+  const int n_items = a.rank_tiles * a.num_seqs;
+  for (int round = 0; round * nq_wg < n_items; ++round) {
+  const int u = round * nq_wg + ((round & 1) ? nq_wg - 1 - qw : qw);
+  if (u >= n_items) continue;
+  const int s = u % a.num_seqs;
+  const int rank = u / a.num_seqs;
   const int row0 = cu_seqlens[s];
   const int L = cu_seqlens[s + 1] - row0;
+  const int ntile = (L + kPT - 1) / kPT;
+  if (rank >= ntile) continue;
+  const int t_stop = rank == a.rank_tiles - 1 ? -1 : ntile - 2 - rank;
   const int ctx = min(context_lens[s], a.max_blocks * a.block_size);
   const int prior = ctx - L;
+  for (int t = ntile - 1 - rank; t > t_stop; --t) {
   const int q0 = t * kPT;                      // first query of the tile (within the sequence)
   const int nq = min(kPT, L - q0);
   const int pos_min = prior + q0;
@@ -267,6 +258,19 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(
   const bool q_valid = j < nq && pos_min >= 0;
   const int my_pos = pos_min + j;
 
+  const int32_t* bt = block_table + (int64_t)s * a.max_blocks;
+  const int last_blk = pos_max / kBlk;
+  // Block-table window in registers: lane i holds the numbers of blocks 2 * wb + i and
+  // 2 * wb + 64 + i (clamped to the sequence's last block), i.e. of key tiles wb .. wb + 63;
+  // a tile's two block numbers are then v_readlane's, with no memory wait in the tile loop.
+  int wb = 0;
+  int btw0, btw1;
+  auto load_window = [&]() {
+    btw0 = bt[min(2 * wb + lane, last_blk)];
+    btw1 = bt[min(2 * wb + 64 + lane, last_blk)];
+  };
+  load_window();
+
   // Q^T operand (B): lane holds q[query j][16i + 8hh .. +8] for every d chunk i.
   uint4 qb[NKC];
   {
@@ -274,29 +278,31 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < NKC; ++i) qb[i] = q_valid ? qr[2 * i + hh] : make_uint4(0, 0, 0, 0);
   }
-  // Settle Q here, once: otherwise the first use inside the tile loop would wait for every
-  // vector-memory operation in flight (the tile prefetches included) on every iteration.
+  // Settle Q and the window here, once: otherwise the first use inside the tile loop would
+  // wait for every vector-memory operation in flight (the tile prefetches included) on every
+  // iteration.
   __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
-  const int32_t* bt = block_table + (int64_t)s * a.max_blocks;
   const int64_t head_off = (int64_t)kvh * kBlk * D;
   const int nkt = pos_max / kPT + 1;
   const uint32_t lds_base = (uint32_t)(uintptr_t)((RG_LDS char*)lds);
 
-  // Issues this wave's share of the global->LDS copies of key tile kt into ring stage st.
-  // A key tile spans the two 16-token blocks bt[2kt], bt[2kt+1] (scalar loads); keys past
-  // the last position read the last valid key instead (they are masked).
+  // Issues this wave's share of the global->LDS copies of key tile kt (wb <= kt < wb + 64)
+  // into ring stage st.  Keys past the last position read the last valid key instead (they
+  // are masked).
   auto issue_tile = [&](int kt, int st) {
-    const int last_blk = pos_max / kBlk;
-    const int64_t blk0 = (int64_t)bt[min(2 * kt, last_blk)] * a.kv_stride + head_off;
-    const int64_t blk1 = (int64_t)bt[min(2 * kt + 1, last_blk)] * a.kv_stride + head_off;
+    const int r = 2 * (kt - wb);  // even: both blocks sit in the same window register
+    const int e0 = __builtin_amdgcn_readlane(r < 64 ? btw0 : btw1, r & 63);
+    const int e1 = __builtin_amdgcn_readlane(r < 64 ? btw0 : btw1, (r & 63) + 1);
+    const int64_t blk0 = (int64_t)e0 * a.kv_stride + head_off;
+    const int64_t blk1 = (int64_t)e1 * a.kv_stride + head_off;
     auto row = [&](int kl) -> int64_t {  // kl: key within the tile
       const int key = min(kt * kPT + kl, pos_max) - kt * kPT;
       return (key < kBlk ? blk0 : blk1) + (int64_t)(key & (kBlk - 1)) * D;
     };
     const uint32_t sbase = lds_base + st * TL::BYTES;
 #pragma unroll
-    for (int u = 0; u < LOADS_PER_WAVE; ++u) {
-      const int ins = w + u * kPWaves;
+    for (int ld = 0; ld < LOADS_PER_WAVE; ++ld) {
+      const int ins = w + ld * kPWaves;
       if (ins < KI) {
         lds_dma16(kc + row(j) + 16 * ins + 8 * hh, __builtin_amdgcn_readfirstlane(sbase + ins * 1024));
       } else {
@@ -316,96 +322,145 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(
     for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  // Prologue: stages 0 .. kPStages-2 (tiles past the end repeat the last tile).
-#pragma unroll
-  for (int p = 0; p < kPStages - 1; ++p) issue_tile(min(p, nkt - 1), p);
+  // The tile loop is software-pipelined: iteration kt turns the scores of tile kt into
+  // probabilities while the MFMA unit computes the scores of tile kt+1, then accumulates
+  // O^T += V^T P^T of tile kt while the VALU masks and reduces the scores of tile kt+1.
+  // Ring: tile kt+1's K and tile kt's V are read during iteration kt; copies of tiles
+  // kt+2 .. kt+kPStages-1 are in flight.
+  static_assert(kPStages >= 3 && kPStages <= 64, "ring depth");
+  const char* vlds = lds + TL::KBYTES;
+  const int grp = lane >> 4;
+  const int e_row = (lane >> 2) & 3;
+  const int qq = lane & 3;
+  const int kt_mask = pos_min / kPT;  // tiles from here on may hold keys past a query
 
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int st = kt % kPStages;
-    // This wave's loads of tile kt are the oldest kPStages-1 groups outstanding: wait for
-    // them, then the barrier makes every wave's part visible (and retires stage kt-1).
-    static_assert(LOADS_PER_WAVE * (kPStages - 2) < 16, "vmcnt immediate");
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((LOADS_PER_WAVE * (kPStages - 2)) | 0x70 | 0xF00);
-    tile_barrier();
-    issue_tile(min(kt + kPStages - 1, nkt - 1), (kt + kPStages - 1) % kPStages);
-
+  // S^T = K Q^T of the tile in stage st: c[4jb + r] is key 8jb + 4hh + r for query j.
+  auto scores = [&](int st) {
     const char* base = lds + st * TL::BYTES;
-    // S^T = K Q^T: c[4jb + r] is key 8jb + 4hh + r of the tile for query j.
+    uint4 ka[NKC];
+#pragma unroll
+    for (int i = 0; i < NKC; ++i) ka[i] = *reinterpret_cast<const uint4*>(base + i * 1024 + lane * 16);
     f32x16_t c;
 #pragma unroll
     for (int v = 0; v < 16; ++v) c[v] = 0.f;
 #pragma unroll
-    for (int i = 0; i < NKC; ++i) {
-      const uint4 ka = *reinterpret_cast<const uint4*>(base + i * 1024 + lane * 16);
-      c = MF::run(ka, qb[i], c);
-    }
-
-    const int k0 = kt * kPT;
-    const bool masked = k0 + kPT - 1 > pos_min;
-    float sc[16];
-    float tmax = -INFINITY;
+    for (int i = 0; i < NKC; ++i) c = MF::run(ka[i], qb[i], c);
+    return c;
+  };
+  // Masks keys past each query's position (tiles from kt_mask on, branch-free) and returns
+  // the tile's maximum in the exp2 domain (both halves of the query's keys).
+  auto mask_max = [&](f32x16_t& c, int kt) {
+    const int lim = kt >= kt_mask ? my_pos - kt * kPT : 1 << 30;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int key = k0 + 8 * (v >> 2) + 4 * hh + (v & 3);
-      float x = c[v] * a.scale_log2;
-      if (masked && key > my_pos) x = -INFINITY;
-      sc[v] = x;
-      tmax = fmaxf(tmax, x);
+      const int key = 8 * (v >> 2) + 4 * hh + (v & 3);
+      c[v] = key > lim ? -INFINITY : c[v];
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    float psum = 0.f;
-    uint32_t pk[8];
+    float tmax = c[0];
 #pragma unroll
-    for (int v = 0; v < 16; v += 2) {
-      const float p0 = __builtin_amdgcn_exp2f(sc[v] - m_new);
-      const float p1 = __builtin_amdgcn_exp2f(sc[v + 1] - m_new);
-      psum += p0 + p1;
-      pk[v / 2] = (uint32_t)elem<T>::from_f32(p0) | ((uint32_t)elem<T>::from_f32(p1) << 16);
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    if (__ballot(alpha != 1.f)) {
+    for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, c[v]);
+    return fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * a.scale_log2;
+  };
+  // Online softmax with a lazy maximum: m_run only moves when a tile's maximum exceeds it by
+  // more than kSlack, so p = 2^(x - m_run) stays below 2^kSlack and the O^T rescale is rare.
+  auto update_max = [&](float tmax) {
+    const bool grow = tmax > m_run + kSlack;
+    if (__ballot(grow)) {
+      const float m_new = grow ? tmax : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
     }
-    // O^T += V^T P^T in two 16-key MFMA steps.  The A operand is read with the transposing
-    // LDS load: in each 16-lane group, lane 4e+q points at V[key0 + e][d0 + 4q .. +4] and
-    // lane i receives V[key0 .. key0+3][d0 + i].
-    const char* vbase = base + TL::KBYTES;
-    const int grp = lane >> 4;
-    const int e = (lane >> 2) & 3;
-    const int qq = lane & 3;
+  };
+  // Probabilities of tile scores c as the packed B operand of the PV product (keys 16n+4hh+r
+  // and 16n+8+4hh+r in k-slots 8hh..8hh+7 for n = 0, 1).
+  auto probs = [&](const f32x16_t& c, uint32_t (&pk)[8]) {
+    float psum = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(c[v], a.scale_log2, -m_run));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(c[v + 1], a.scale_log2, -m_run));
+      psum += p0 + p1;
+      pk[v / 2] = pack2<T>(p0, p1);
+    }
+    l_run += psum;
+  };
+  // O^T += V^T P^T for the tile in stage st, in two 16-key MFMA steps.  The A operand comes
+  // from the transposing LDS read: in each 16-lane group, lane 4e+q points at
+  // V[key0 + e][d0 + 4q .. +4] and lane i receives V[key0 .. key0+3][d0 + i].
+  auto accumulate = [&](int st, const uint32_t (&pk)[8]) {
+    const char* vbase = vlds + st * TL::BYTES;
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       const uint4 pb = make_uint4(pk[4 * n], pk[4 * n + 1], pk[4 * n + 2], pk[4 * n + 3]);
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const int d = 32 * db + 16 * (grp & 1) + 4 * qq;   // this lane's address column
+        const int d = 32 * db + 16 * (grp & 1) + 4 * qq;  // this lane's address column
         v4i16_t part[2];
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          const int key = 16 * n + 8 * half + 4 * (grp >> 1) + e;
+          const int key = 16 * n + 8 * half + 4 * (grp >> 1) + e_row;
           const int off = key * (D * 2) + TL::vchunk(key, d >> 3) * 16 + (d & 7) * 2;
           part[half] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((RG_LDS v4i16_t*)(vbase + off));
         }
-        uint4 va;
-        va.x = (uint32_t)(uint16_t)part[0][0] | ((uint32_t)(uint16_t)part[0][1] << 16);
-        va.y = (uint32_t)(uint16_t)part[0][2] | ((uint32_t)(uint16_t)part[0][3] << 16);
-        va.z = (uint32_t)(uint16_t)part[1][0] | ((uint32_t)(uint16_t)part[1][1] << 16);
-        va.w = (uint32_t)(uint16_t)part[1][2] | ((uint32_t)(uint16_t)part[1][3] << 16);
-        o[db] = MF::run(va, pb, o[db]);
+        const uint2 lo = __builtin_bit_cast(uint2, part[0]);
+        const uint2 hi = __builtin_bit_cast(uint2, part[1]);
+        o[db] = MF::run(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[db]);
       }
     }
+  };
+  // This wave's copies of tile `need` have landed (all but the newest `pending` groups),
+  // then the barrier shows every wave's copies and retires the stages read before it.
+  auto wait_tiles = [&](auto pending) {
+    static_assert(LOADS_PER_WAVE * decltype(pending)::value < 16, "vmcnt immediate");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((LOADS_PER_WAVE * decltype(pending)::value) | 0x70 | 0xF00);
+    tile_barrier();
+  };
+
+  // Prologue: tiles 0 .. kPStages-1 in flight (past the end: repeats of the last tile); with
+  // tiles 0 and 1 in LDS, the scores and maximum of tile 0.
+#pragma unroll
+  for (int p = 0; p < kPStages; ++p) issue_tile(min(p, nkt - 1), p);
+  wait_tiles(std::integral_constant<int, kPStages - 2>{});
+  f32x16_t c = scores(0);
+  update_max(mask_max(c, 0));
+
+  int kt = 0;
+  for (;;) {
+  // Iterations whose refill tile kt + kPStages lies in the current block-table window.
+  const int kend = min(nkt, wb + 64 - kPStages);
+  for (; kt < kend; ++kt) {
+    const int kn = min(kt + 1, nkt - 1);  // past the end: tile nkt-1 again (no new maximum)
+    f32x16_t cn = scores(kn % kPStages);
+    uint32_t pk[8];
+    probs(c, pk);
+    accumulate(kt % kPStages, pk);
+    const float tmax = mask_max(cn, kn);
+    update_max(tmax);
+    c = cn;
+    // Tile kt+2 in LDS; every wave is done with stage kt, which takes tile kt + kPStages.
+    wait_tiles(std::integral_constant<int, kPStages - 3>{});
+    issue_tile(min(kt + kPStages, nkt - 1), kt % kPStages);
+  }
+  if (kt >= nkt) break;
+  // Next 64 tiles (sequences past 2048 positions): the wait drains the copies in flight once.
+  wb += 64;
+  load_window();
+  __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
   }
 
+  // Every copy issued (the ring's tail repeats the last tile) lands before the LDS is reused
+  // or released.
+  __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
+  tile_barrier();
   // Normalise (the two halves of a query's keys live in lanes l and l ^ 32) and write.
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if (!q_valid) return;
+  if (q_valid) {
   const float inv = 1.f / l_tot;
   S* orow = static_cast<S*>(a.out) + ((int64_t)(row0 + q0 + j) * H + head) * D;
 #pragma unroll
@@ -413,12 +468,13 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
       const int d0 = 32 * db + 8 * jb + 4 * hh;
-      const uint32_t w0 = (uint32_t)elem<T>::from_f32(o[db][4 * jb] * inv) |
-                          ((uint32_t)elem<T>::from_f32(o[db][4 * jb + 1] * inv) << 16);
-      const uint32_t w1 = (uint32_t)elem<T>::from_f32(o[db][4 * jb + 2] * inv) |
-                          ((uint32_t)elem<T>::from_f32(o[db][4 * jb + 3] * inv) << 16);
+      const uint32_t w0 = pack2<T>(o[db][4 * jb] * inv, o[db][4 * jb + 1] * inv);
+      const uint32_t w1 = pack2<T>(o[db][4 * jb + 2] * inv, o[db][4 * jb + 3] * inv);
       *reinterpret_cast<uint2*>(orow + d0) = make_uint2(w0, w1);
     }
+  }
+  }  // tiles of this work item
+  }  // work items of this workgroup
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -447,7 +503,6 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
                                  int32_t num_seqs, int32_t num_tokens, int32_t max_query_len,
                                  int32_t dtype, int64_t kv_block_stride, void* stream) {
   const char* op = "prefill_packed";
-  (void)max_query_len;
   if (dtype_bytes(dtype) == 0) return fail(RG_ERR_NOT_SUPPORTED, "%s: unknown dtype %d", op, dtype);
   if (head_dim <= 0 || head_dim % 4 != 0 || head_dim > RG_MAX_HEAD_DIM) {
     return fail(RG_ERR_NOT_SUPPORTED,
@@ -475,16 +530,22 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
   }
   PrefillArgs a{query, key_cache, value_cache, block_table, context_lens, cu_seqlens, output,
                 scale * kLog2e, num_heads, num_kv_heads, head_dim, block_size,
-                max_blocks_per_seq, num_seqs, num_tokens, stride};
+                max_blocks_per_seq, num_seqs, num_tokens, 0, stride};
   hipStream_t s = as_stream(stream);
   const int eb = dtype_bytes(dtype);
-  if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && num_heads == 4 * num_kv_heads && block_size == kBlk &&
+  if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && scale > 0.f && num_heads == 4 * num_kv_heads &&
+      block_size == kBlk &&
       (head_dim == 64 || head_dim == 128) && max_blocks_per_seq > 0 && aligned16(query) &&
       aligned16(key_cache) && aligned16(value_cache) && (stride * eb) % 16 == 0 &&
       (reinterpret_cast<uintptr_t>(output) & 7u) == 0) {
-    // Upper bound of the number of 32-query tiles: every sequence adds at most one partial.
-    const int64_t tiles = (int64_t)(num_tokens + kPT - 1) / kPT + num_seqs;
-    const dim3 grid((unsigned)(tiles * num_kv_heads));
+    // Tile ranks per sequence from max_query_len (a hint: the kernel's last rank covers any
+    // tiles beyond it; no query run is longer than num_tokens).
+    const int64_t qmax = std::min<int64_t>(std::max<int32_t>(max_query_len, 1), num_tokens);
+    a.rank_tiles = (int32_t)((qmax + kPT - 1) / kPT);
+    // Two resident workgroups per CU, split evenly over the kv-heads, at most one per item.
+    const int64_t items = (int64_t)a.rank_tiles * num_seqs;
+    const int64_t per_head = std::min<int64_t>(items, std::max<int64_t>(1, 2 * device_cu_count() / num_kv_heads));
+    const dim3 grid((unsigned)(per_head * num_kv_heads));
     auto go = [&](auto tag, auto dtag) {
       using T = decltype(tag);
       constexpr int D = decltype(dtag)::value;

@@ -19,6 +19,8 @@ int ok();
 
 // Converts a launch's hipError_t (hipGetLastError) into a status code.
 int check_launch(const char* what);
+// Compute units of the current device (256 if the query fails).
+int device_cu_count();
 
 // ------------------------------------------------------------ element types --
 

@@ -34,6 +34,15 @@ int check_launch(const char* what) {
   return ok();
 }
 
+int device_cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+    n = 256;
+  }
+  return n;
+}
+
 }  // namespace rg
 
 extern "C" const char* rg_last_error(void) { return rg::t_last_error.c_str(); }

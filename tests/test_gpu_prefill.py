@@ -20,7 +20,7 @@ from railgun_amd.ops import rope_cos_sin_table
 pytestmark = pytest.mark.gpu
 
 
-def _run(device, kernels, w: wl.PrefillWorkload, seed: int, check_seqs=None):
+def _run(device, kernels, w: wl.PrefillWorkload, seed: int, check_seqs=None, max_query_len=None):
     dt = w.dtype
     rng = np.random.default_rng(seed)
     T, H, hkv, D, bs = w.num_tokens, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
@@ -38,7 +38,7 @@ def _run(device, kernels, w: wl.PrefillWorkload, seed: int, check_seqs=None):
     cu = w.cu_seqlens
     kernels.launch_prefill_packed(dq, dkc, dvc, i32(w.block_table, device), i32(w.context_lens, device),
                                   i32(cu, device), out, w.scale, H, hkv, D, bs, w.max_blocks, w.num_seqs, T,
-                                  int(w.seq_lens.max()))
+                                  int(w.seq_lens.max()) if max_query_len is None else max_query_len)
     torch.cuda.synchronize()
     got = dev_f32(out)
     orc.rope_reshape_and_cache(q, k, v, kc, vc, table.numpy(), pos, slots, dt, bs)
@@ -67,3 +67,16 @@ def test_prefill_config4(device, kernels):
     w = wl.config4()
     order = np.argsort(w.seq_lens)[:3]
     _run(device, kernels, w, seed=w.seed, check_seqs=[int(s) for s in order])
+
+
+@pytest.mark.parametrize("max_query_len", [None, 1])
+def test_prefill_long_prior_context(device, kernels, max_query_len):
+    """Chunks after up to 4000 cached positions (the block-table window of the MFMA kernel moves
+    past 128 blocks), bf16 D 128; with max_query_len = 1 the last tile rank of each sequence
+    takes every tile, which must give the same result."""
+    rng = np.random.default_rng(7)
+    lens = np.array([33, 70, 5, 96], np.int32)
+    prior = np.array([3000, 2100, 4000, 0], np.int32)
+    bt = wl.assign_blocks(prior + lens, 16, 1000, 260, rng)
+    w = wl.PrefillWorkload("long_prior", "bf16", 32, 8, 128, 16, 1000, lens, bt, 4, prior=prior)
+    _run(device, kernels, w, seed=77, max_query_len=max_query_len)
