@@ -29,6 +29,16 @@ HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2516.6
 
 
+def measured_traffic(key: str):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (copy-calibrated) for
+    this workload, as committed in profiles/traffic.json; None if absent."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f).get(key)
+    except (OSError, ValueError):
+        return None
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -40,8 +50,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-side", action="store_true", help="skip the config 3 / config 4 side figures")
-    ap.add_argument("--only", choices=["decode", "v2", "prefill"], default=None,
-                    help="run one workload only and print its figures (for profiling)")
+    ap.add_argument("--only", choices=["decode", "v2", "prefill", "copy"], default=None,
+                    help="run one workload only and print its figures (for profiling); 'copy' is the plain "
+                         "1 GiB device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -163,7 +174,8 @@ def side_v2(device, gen, steps: int) -> dict:
     del st, ws
     torch.cuda.empty_cache()
     return {"workload": w.name, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": w.decode_bytes()}
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": w.decode_bytes(),
+            "traffic": measured_traffic("paged_attention_v2_config3")}
 
 
 def side_prefill(device, gen, steps: int) -> dict:
@@ -196,7 +208,21 @@ def side_prefill(device, gen, steps: int) -> dict:
     ms = time_events(call, steps, 2)
     tflops = w.causal_flops() / (ms * 1e-3) / 1e12
     return {"workload": w.name, "tokens": T, "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 2),
-            "frac_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops": w.causal_flops()}
+            "frac_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops": w.causal_flops(),
+            "traffic": measured_traffic("prefill_config4")}
+
+
+def copy_calibration(device, steps: int) -> dict:
+    """A plain device copy of 1 GiB (torch's copy kernel): reads and writes exactly 1 GiB per
+    launch, which is what the HBM counters of a profile are scaled against."""
+    import torch
+
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    ms = time_events(lambda: dst.copy_(src), steps, 2)
+    return {"workload": "copy_1GiB", "bytes_read": n, "bytes_written": n, "us": round(ms * 1e3, 2),
+            "GB/s": round(2 * n / (ms * 1e-3) / 1e9, 1)}
 
 
 def main() -> int:
@@ -218,6 +244,9 @@ def main() -> int:
         return 0
     if args.only == "prefill":
         print(json.dumps(side_prefill(device, gen, args.steps)), flush=True)
+        return 0
+    if args.only == "copy":
+        print(json.dumps(copy_calibration(device, args.steps)), flush=True)
         return 0
     w = wl.config2()
     log(f"[bench] config2: B={w.batch} tokens={int(w.context_lens.sum())} pool={w.num_blocks} blocks")
@@ -263,7 +292,9 @@ def main() -> int:
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "kernel": "paged_attention_v1 (decode partition + merge)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("paged_attention_v1_config2"),
+                     "traffic_source": "profiles/hbm_traffic_counters.txt (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE)",
                      "algorithmic_bytes": w.decode_bytes(), "us_per_launch": round(ms_v1 * 1e3, 2)},
     }
     if args.only == "decode":
@@ -273,7 +304,7 @@ def main() -> int:
         log("[bench] config3 v2 ...")
         result["v2_long_context"] = side_v2(device, gen, max(3, args.steps // 5))
         log("[bench] config4 prefill ...")
-        result["prefill"] = side_prefill(device, gen, 3)
+        result["prefill"] = side_prefill(device, gen, 10)
     if not args.no_cpu:
         log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w)
