@@ -51,6 +51,16 @@ def test_header_compiles_standalone(lang, tmp_path):
     assert r.returncode == 0, r.stderr
 
 
+def test_cpp_mirror_header_compiles(tmp_path):
+    """include/railgun_hip.hpp (the C++ mirror of PagedAttentionKernels / PagedAttentionOp)
+    compiles standalone as C++17 against the HIP runtime headers."""
+    src = tmp_path / "t.cpp"
+    src.write_text('#include "railgun_hip.hpp"\nint main() { return railgun::dtype_size(railgun::DType::BF16) == 2 ? 0 : 1; }\n')
+    r = subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__",
+                        "-I/opt/rocm/include", f"-I{ROOT}/include", str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
 def call(name, *args):
     lib = railgun_amd.load_library()
     return getattr(lib, name)(*args), _lib.last_error()
