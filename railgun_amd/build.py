@@ -26,7 +26,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_SOURCES = ["rg_status.hip", "cache_ops.hip", "decode.hip", "prefill.hip"]
 # -packed-fp32-ops: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.
 HIPCC_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", f"-I{ROOT}/include",
+    "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++20", f"-I{ROOT}/include",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall",
 ]
 # Per-source additions.  prefill.hip keeps its MFMA accumulators in ordinary VGPRs: with the
@@ -73,7 +73,7 @@ def build_cpp_tests() -> list[str]:
         if not os.path.exists(src):
             continue
         exe = os.path.join(src_dir, name)
-        _run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", f"-I{ROOT}/include", src, "-o", exe,
+        _run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++20", f"-I{ROOT}/include", src, "-o", exe,
               f"-L{PKG}", "-lrailgun_hip", f"-Wl,-rpath,{PKG}", "-Wl,-rpath,$ORIGIN/../../railgun_amd"])
         out.append(exe)
     return out

@@ -26,6 +26,8 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 #include "rg_common.hpp"
 
@@ -262,11 +264,12 @@ struct DecodeTile {
     vrow = lane / ROWV;
     vd0 = (lane % ROWV) * 8;
   }
-  // q rows of the G heads of one kv-head ([G, D] contiguous).
+  // q rows of the G heads of one kv-head ([G, D] contiguous).  MFMA i takes dims
+  // [32i, 32i + 32): lane (col, seg) holds dims 32i + 8seg .. +8 of head col % G.
   __device__ __forceinline__ void load_q(const S* qg) {
-    const uint4* qrow = reinterpret_cast<const uint4*>(qg + (int64_t)(col % G) * D + seg * (D / 4));
+    const uint4* qrow = reinterpret_cast<const uint4*>(qg + (int64_t)(col % G) * D + seg * 8);
 #pragma unroll
-    for (int i = 0; i < NK; ++i) qa[i] = qrow[i];
+    for (int i = 0; i < NK; ++i) qa[i] = qrow[4 * i];
   }
   __device__ __forceinline__ void reset() {
 #pragma unroll
@@ -280,10 +283,11 @@ struct DecodeTile {
       for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
   }
   // kb / vb: the [16, D] rows of one kv-head in one block.
+  // Load i of K reads dims 32i .. 32i + 32 of all 16 rows: 64 contiguous bytes per row.
   __device__ __forceinline__ void load(const S* kb, const S* vb, uint4 (&kk)[NK], uint4 (&vv)[NV]) const {
-    const uint4* kp = reinterpret_cast<const uint4*>(kb + col * D + seg * (D / 4));
+    const uint4* kp = reinterpret_cast<const uint4*>(kb + col * D + seg * 8);
 #pragma unroll
-    for (int i = 0; i < NK; ++i) kk[i] = kp[i];
+    for (int i = 0; i < NK; ++i) kk[i] = kp[4 * i];
 #pragma unroll
     for (int i = 0; i < NV; ++i) vv[i] = *reinterpret_cast<const uint4*>(vb + (i * TPI + vrow) * D + vd0);
   }
@@ -505,6 +509,16 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 // consecutive).  decode_stream_merge_kernel combines the partials of each segment.  When
 // U < W only the first U workers are used, so every worker of a segment's range owns units.
 
+// Units in flight ahead of the one being computed, per stream-K worker.  The workers are
+// one wave per SIMD (RG_SK_WAVES_PER_CU = 4): two waves sharing a SIMD progress at
+// different rates (the older one wins issue arbitration), which leaves the younger half
+// of a static split running alone at the end; one wave per SIMD with three 8 KB units in
+// flight streams at the same rate without that tail.
+#ifndef RG_SK_PREFETCH
+#define RG_SK_PREFETCH 3
+#endif
+constexpr int kSkPrefetch = RG_SK_PREFETCH;
+
 // Optional occupancy floor of the stream-K kernel (waves per SIMD).
 #if defined(RG_SK_OCC) && RG_SK_OCC > 0
 #define RG_SK_OCCUPANCY __attribute__((amdgpu_waves_per_eu(RG_SK_OCC)))
@@ -533,6 +547,13 @@ __device__ __forceinline__ int64_t worker_of(int64_t u, int64_t U, int64_t W) { 
 __device__ __forceinline__ int seq_blocks(const int32_t* ctxl, int s, int max_blocks) {
   const int c = max(0, min(ctxl[s], max_blocks * kBS));
   return (c + kBS - 1) / kBS;
+}
+
+// A wave-uniform 64-bit value made visibly uniform to the compiler.
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 // Wave-wide inclusive prefix sum.
@@ -580,38 +601,58 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   constexpr int HG = Tile::HG;
   constexpr int NK = Tile::NK;
   constexpr int NV = Tile::NV;
-  constexpr int NBUF = kPrefetch + 1;
+  constexpr int NBUF = kSkPrefetch + 1;
   __shared__ float p_lds[2][kBS * GP];
   __shared__ float alpha_lds[2][GP];
 
   const int lane = threadIdx.x;
   const int64_t k = blockIdx.x;
   const int hkv = a.num_kv_heads;
-  int s_dummy;
-  int64_t st_dummy;
-  const int64_t U = scan_units(context_lens, a.batch, a.max_blocks, hkv, lane, -1, s_dummy, st_dummy);
-  // With fewer units than workers only the first U workers run (one unit each), so that every
-  // worker between a segment's first and last one owns a unit and writes a partial.
-  const int64_t W = min<int64_t>(a.num_workers, U);
-  if (k >= W) return;
-  const int64_t u0 = worker_start(k, U, W);
-  const int64_t u1 = worker_start(k + 1, U, W);
+  // Total units U, this worker's range [u0, u1) and the sequence holding u0.  Up to 64
+  // sequences take one pass (one context length per lane); larger batches scan twice.
+  int64_t U, W, u0, u1, seq_start;
   int s;
-  int64_t seq_start;
-  scan_units(context_lens, a.batch, a.max_blocks, hkv, lane, u0, s, seq_start);
-  s = __builtin_amdgcn_readfirstlane(s);
+  if (a.batch <= 64) {
+    const int64_t n = lane < a.batch ? (int64_t)seq_blocks(context_lens, lane, a.max_blocks) * hkv : 0;
+    const int64_t incl = wave_incl_scan(n, lane);
+    const int64_t excl = incl - n;
+    U = uniform64(__shfl(incl, 63, 64));
+    // With fewer units than workers only the first U workers run (one unit each), so that
+    // every worker between a segment's first and last one owns a unit and writes a partial.
+    W = min<int64_t>(a.num_workers, U);
+    if (k >= W) return;
+    u0 = worker_start(k, U, W);
+    u1 = worker_start(k + 1, U, W);
+    const uint64_t hit = __ballot(n > 0 && excl <= u0 && u0 < incl);
+    s = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)hit) - 1);
+    seq_start = uniform64(__shfl(excl, s, 64));
+  } else {
+    int s_dummy;
+    int64_t st_dummy;
+    U = uniform64(scan_units(context_lens, a.batch, a.max_blocks, hkv, lane, -1, s_dummy, st_dummy));
+    W = min<int64_t>(a.num_workers, U);
+    if (k >= W) return;
+    u0 = worker_start(k, U, W);
+    u1 = worker_start(k + 1, U, W);
+    scan_units(context_lens, a.batch, a.max_blocks, hkv, lane, u0, s, seq_start);
+    s = __builtin_amdgcn_readfirstlane(s);
+    seq_start = uniform64(seq_start);
+  }
 
   // Cursor of the unit being computed (cs, ckvh, cb) and of the unit being loaded.
   struct Cursor {
     int s, kvh, b, nblk;
   };
+  // The cursors are wave-uniform; readfirstlane tells the compiler so (seq_start comes out of
+  // a cross-lane shuffle), which keeps every block-table and context-length read a scalar
+  // load instead of a vector load whose wait would also drain the K/V prefetches.
   Cursor cur;
   cur.s = s;
-  cur.nblk = seq_blocks(context_lens, s, a.max_blocks);
+  cur.nblk = __builtin_amdgcn_readfirstlane(seq_blocks(context_lens, s, a.max_blocks));
   {
-    const int64_t r = u0 - seq_start;
-    cur.kvh = (int)(r / cur.nblk);
-    cur.b = (int)(r - (int64_t)cur.kvh * cur.nblk);
+    const int r = __builtin_amdgcn_readfirstlane((int)(u0 - seq_start));
+    cur.kvh = __builtin_amdgcn_readfirstlane(r / cur.nblk);
+    cur.b = __builtin_amdgcn_readfirstlane(r - cur.kvh * cur.nblk);
   }
   auto advance = [&](Cursor& c) {
     if (++c.b == c.nblk) {
@@ -625,9 +666,36 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
       }
     }
   };
-  auto load_unit = [&](const Cursor& c, uint4 (&kk)[NK], uint4 (&vv)[NV], const Tile& t) {
-    const int64_t off = (int64_t)block_table[(int64_t)c.s * a.max_blocks + c.b] * a.kv_stride +
-                        (int64_t)c.kvh * kBS * D;
+  // Block numbers of the worker's units in a register window: lane i holds the block of
+  // unit wbase + i (units counted from u0).  Filling it walks each lane's cursor i units on
+  // (a few steps: ranges cross few segments) and reads all 64 entries with one load, so the
+  // per-unit address needs a v_readlane instead of a scalar load waited on in the loop.
+  int64_t wbase = 0;
+  int btw = 0;
+  auto fill_window = [&](const Cursor& c0, int64_t base) {
+    int ss = c0.s, kh = c0.kvh, b = c0.b + lane, nb = c0.nblk;
+    while (b >= nb && ss < a.batch) {
+      b -= nb;
+      if (++kh == hkv) {
+        kh = 0;
+        do {
+          ++ss;
+          nb = ss < a.batch ? seq_blocks(context_lens, ss, a.max_blocks) : 1;
+        } while (nb == 0);
+      }
+    }
+    btw = base + lane < u1 - u0 && ss < a.batch ? block_table[(int64_t)ss * a.max_blocks + b] : 0;
+  };
+  // ldi: index of the unit cursor c points at.  A window refill (every 64 units) waits for
+  // everything in flight once.
+  auto load_unit = [&](const Cursor& c, int64_t ldi, uint4 (&kk)[NK], uint4 (&vv)[NV], const Tile& t) {
+    if (ldi - wbase >= 64) {
+      wbase = ldi;
+      fill_window(c, ldi);
+      __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
+    }
+    const int e = __builtin_amdgcn_readlane(btw, (int)(ldi - wbase));
+    const int64_t off = (int64_t)e * a.kv_stride + (int64_t)c.kvh * kBS * D;
     t.load(kc + off, vc + off, kk, vv);
   };
 
@@ -667,40 +735,57 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
 
   const int64_t n = u1 - u0;
   Cursor ld = cur;
+  int64_t ldi = 0;
+  int ctx_cur = min(context_lens[cur.s], a.max_blocks * kBS);
+  fill_window(cur, 0);
   uint4 kbuf[NBUF][NK], vbuf[NBUF][NV];
-  // Prologue: the first kPrefetch units (the last one repeated past the end of the range).
+  // Prologue: the first kSkPrefetch units (the last one repeated past the end of the range).
 #pragma unroll
-  for (int q = 0; q < kPrefetch; ++q) {
-    load_unit(ld, kbuf[q], vbuf[q], tile);
-    if (q + 1 < n) advance(ld);
-  }
-  int64_t loaded = min<int64_t>(kPrefetch, n);  // units whose loads have been issued
-  begin_segment(cur);
-  for (int64_t j0 = 0; j0 < n; j0 += NBUF) {
-#pragma unroll
-    for (int q = 0; q < NBUF; ++q) {
-      const int64_t j = j0 + q;
-      if (j < n) {
-        load_unit(ld, kbuf[(q + kPrefetch) % NBUF], vbuf[(q + kPrefetch) % NBUF], tile);
-        if (loaded < n) {
-          ++loaded;
-          if (loaded < n) advance(ld);
-        }
-        const int ctx = min(context_lens[cur.s], a.max_blocks * kBS);
-        tile.step(kbuf[q], vbuf[q], cur.b * kBS, ctx, a.scale_log2, p_lds[j & 1], alpha_lds[j & 1]);
-        const bool last_of_segment = cur.b + 1 == cur.nblk || j + 1 == n;
-        if (last_of_segment) {
-          end_segment(cur);
-          if (j + 1 < n) {
-            advance(cur);
-            begin_segment(cur);
-          }
-        } else {
-          advance(cur);
-        }
-      }
+  for (int q = 0; q < kSkPrefetch; ++q) {
+    load_unit(ld, ldi, kbuf[q], vbuf[q], tile);
+    if (q + 1 < n) {
+      advance(ld);
+      ++ldi;
     }
   }
+  int64_t loaded = min<int64_t>(kSkPrefetch, n);  // units whose loads have been issued
+  begin_segment(cur);
+  // Unit j computes from ring slot j % NBUF while the loads of unit j + kSkPrefetch go to
+  // slot (j + kSkPrefetch) % NBUF.  Whole rounds of NBUF units run without a bounds test, so the
+  // loop has no path that skips a round's loads (such a path makes the compiler drain every
+  // load in flight at the loop head); the last n % NBUF units run after it.
+  auto unit = [&](int64_t j, auto qc) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value;
+    load_unit(ld, ldi, kbuf[(q + kSkPrefetch) % NBUF], vbuf[(q + kSkPrefetch) % NBUF], tile);
+    if (loaded < n) {
+      ++loaded;
+      if (loaded < n) {
+        advance(ld);
+        ++ldi;
+      }
+    }
+    tile.step(kbuf[q], vbuf[q], cur.b * kBS, ctx_cur, a.scale_log2, p_lds[j & 1], alpha_lds[j & 1]);
+    const bool last_of_segment = cur.b + 1 == cur.nblk || j + 1 == n;
+    if (last_of_segment) {
+      end_segment(cur);
+      if (j + 1 < n) {
+        advance(cur);
+        begin_segment(cur);
+        ctx_cur = min(context_lens[cur.s], a.max_blocks * kBS);
+      }
+    } else {
+      advance(cur);
+    }
+  };
+  int64_t j0 = 0;
+  for (; j0 + NBUF <= n; j0 += NBUF) {
+    [&]<int... Q>(std::integer_sequence<int, Q...>) {
+      (unit(j0 + Q, std::integral_constant<int, Q>{}), ...);
+    }(std::make_integer_sequence<int, NBUF>{});
+  }
+  [&]<int... Q>(std::integer_sequence<int, Q...>) {
+    ((j0 + Q < n ? unit(j0 + Q, std::integral_constant<int, Q>{}) : void()), ...);
+  }(std::make_integer_sequence<int, NBUF - 1>{});
 }
 
 // One workgroup per (segment, head of the group): merges the partials of workers
@@ -1025,7 +1110,7 @@ int32_t v1_num_partitions(const Shape& sh) {
 
 // Waves per CU the stream-K decode launches (one worker per wave).
 #ifndef RG_SK_WAVES_PER_CU
-#define RG_SK_WAVES_PER_CU 8
+#define RG_SK_WAVES_PER_CU 4
 #endif
 
 int32_t stream_workers(const Shape& sh) {
