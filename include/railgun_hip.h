@@ -135,6 +135,49 @@ int rg_rope_reshape_and_cache(void* q, const void* k, const void* v,
                               int32_t num_tokens, int32_t dtype,
                               int64_t kv_block_stride, void* stream);
 
+/* rg_rope_reshape_and_cache for the output of one fused q/k/v projection:
+ * token t's q, k and v rows are read from qkv + t*qkv_token_stride at
+ * columns [0, H*D), [H*D, (H+H_kv)*D) and [(H+H_kv)*D, (H+2*H_kv)*D)
+ * (qkv_token_stride >= (H+2*H_kv)*D elements); the rotated q rows are
+ * written to q_out [num_tokens, num_heads, head_dim] (qkv is not modified),
+ * rotated k and v go to the paged caches as in rg_rope_reshape_and_cache.
+ * Same arithmetic, one pass.  New entry: it serves the decode step of a model
+ * whose q/k/v projections are one GEMM (the reference projects q, k and v
+ * separately and never applies RoPE,
+ * crates/vllm-models/src/llama/attention.rs:104-125). */
+int rg_qkv_rope_reshape_and_cache(const void* qkv, int64_t qkv_token_stride,
+                                  void* q_out, void* k_cache, void* v_cache,
+                                  const float* cos_sin, const int32_t* positions,
+                                  const int32_t* slot_mapping, int32_t num_heads,
+                                  int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t block_size, int32_t num_tokens,
+                                  int32_t dtype, int64_t kv_block_stride,
+                                  void* stream);
+
+/* ------------------------------------------------- model element-wise ops -- */
+
+/* Fused residual add + RMSNorm over rows of hidden_size elements:
+ *   residual != NULL: residual <- round(residual + x);  y = residual
+ *   residual == NULL: y = x
+ *   out = round(y / sqrt(mean(y^2) + eps) * weight), the mean and the
+ *   normalisation in fp32.
+ * x, residual, out: [num_rows, hidden_size]; weight: [hidden_size]; out may
+ * not alias x or residual.  Replaces the candle RmsNorm and residual add
+ * around each sublayer (crates/vllm-models/src/llama/architecture.rs:38-59,
+ * :141-156; candle_nn::RmsNorm). */
+int rg_rms_norm(const void* x, void* residual, const void* weight, void* out,
+                float eps, int32_t num_rows, int32_t hidden_size, int32_t dtype,
+                void* stream);
+
+/* SwiGLU gate: out[r, i] = round(round(silu(g)) * u), g = gate_up[r, i],
+ * u = gate_up[r, intermediate_size + i], silu(g) = g / (1 + exp(-g)).
+ * gate_up: [num_rows, 2*intermediate_size] (the gate and up projections as
+ * one GEMM), out: [num_rows, intermediate_size], num_rows <= 65535.
+ * Replaces silu(gate_proj(x)) * up_proj(x) of LlamaMLP::forward
+ * (crates/vllm-models/src/llama/architecture.rs:80-84). */
+int rg_silu_and_mul(const void* gate_up, void* out, int32_t num_rows,
+                    int32_t intermediate_size, int32_t dtype, void* stream);
+
 /* ------------------------------------------------------- decode, v1 -------- */
 
 /* Bytes of workspace rg_paged_attention_v1 / _v1_plus use for the given shape on the

@@ -147,13 +147,25 @@ __global__ __launch_bounds__(kCacheThreads) void rope_inplace_kernel(
   rope_row<T>(row, row, cos_sin + pos * head_dim, head_dim, threadIdx.x & 63);
 }
 
+// Where the fused pass finds each token's rows: q rows are read from q_src and written,
+// rotated, to q_dst (the same place for the in-place entry); k and v rows are read from
+// k_src / v_src.  Strides are elements between consecutive tokens, so the q, k and v column
+// ranges of one fused QKV projection output [T, (H + 2 H_kv) D] are read where they lie.
+template <typename S>
+struct RopeRows {
+  const S* q_src;
+  S* q_dst;
+  const S* k_src;
+  const S* v_src;
+  int64_t q_src_stride, q_dst_stride, k_src_stride, v_src_stride;
+};
+
 // Fused pass over the new tokens; grid (tokens, ceil((H + 2*H_kv) / 4)), wave = one row:
-// rows [0, H) rotate q in place, rows [H, H + H_kv) rotate k into the cache, rows
+// rows [0, H) rotate q, rows [H, H + H_kv) rotate k into the cache, rows
 // [H + H_kv, H + 2*H_kv) copy v into the cache.
 template <typename T>
 __global__ __launch_bounds__(kCacheThreads) void rope_cache_kernel(
-    typename elem<T>::storage* __restrict__ q, const typename elem<T>::storage* __restrict__ k,
-    const typename elem<T>::storage* __restrict__ v, typename elem<T>::storage* __restrict__ k_cache,
+    RopeRows<typename elem<T>::storage> io, typename elem<T>::storage* __restrict__ k_cache,
     typename elem<T>::storage* __restrict__ v_cache, const float* __restrict__ cos_sin,
     const int32_t* __restrict__ positions, const int32_t* __restrict__ slot_mapping,
     int num_heads, CacheGeom g) {
@@ -166,8 +178,8 @@ __global__ __launch_bounds__(kCacheThreads) void rope_cache_kernel(
   if (r >= num_heads + 2 * hkv) return;
   if (r < num_heads) {
     const int64_t pos = positions[t];
-    S* row = q + ((int64_t)t * num_heads + r) * D;
-    rope_row<T>(row, row, cos_sin + pos * D, D, lane);
+    rope_row<T>(io.q_src + t * io.q_src_stride + (int64_t)r * D, io.q_dst + t * io.q_dst_stride + (int64_t)r * D,
+                cos_sin + pos * D, D, lane);
     return;
   }
   const int32_t slot = slot_mapping[t];
@@ -177,11 +189,11 @@ __global__ __launch_bounds__(kCacheThreads) void rope_cache_kernel(
   if (r < num_heads + hkv) {
     const int h = r - num_heads;
     const int64_t pos = positions[t];
-    rope_row<T>(k + ((int64_t)t * hkv + h) * D, k_cache + cache_row(g, blk, h, off), cos_sin + pos * D, D,
-                lane);
+    rope_row<T>(io.k_src + t * io.k_src_stride + (int64_t)h * D, k_cache + cache_row(g, blk, h, off),
+                cos_sin + pos * D, D, lane);
   } else {
     const int h = r - num_heads - hkv;
-    const S* src = v + ((int64_t)t * hkv + h) * D;
+    const S* src = io.v_src + t * io.v_src_stride + (int64_t)h * D;
     S* dst = v_cache + cache_row(g, blk, h, off);
     for (int i = lane; i < D; i += 64) dst[i] = src[i];
   }
@@ -255,15 +267,31 @@ int launch_rope_inplace(void* x, const float* cs, const int32_t* pos, int h, int
 }
 
 template <typename T>
-int launch_rope_cache(void* q, const void* k, const void* v, void* kc, void* vc, const float* cs,
-                      const int32_t* pos, const int32_t* slots, int h, CacheGeom g, int n, hipStream_t s) {
+int launch_rope_cache(const RopeRows<typename elem<T>::storage>& io, void* kc, void* vc, const float* cs,
+                      const int32_t* pos, const int32_t* slots, int h, CacheGeom g, int n, hipStream_t s,
+                      const char* op) {
   using S = typename elem<T>::storage;
   const int rows = h + 2 * g.num_kv_heads;
   const dim3 grid(n, (rows + kRowsPerGroup - 1) / kRowsPerGroup);
-  hipLaunchKernelGGL(rope_cache_kernel<T>, grid, dim3(kCacheThreads), 0, s, static_cast<S*>(q),
-                     static_cast<const S*>(k), static_cast<const S*>(v), static_cast<S*>(kc), static_cast<S*>(vc),
-                     cs, pos, slots, h, g);
-  return check_launch("rope_reshape_and_cache");
+  hipLaunchKernelGGL(rope_cache_kernel<T>, grid, dim3(kCacheThreads), 0, s, io, static_cast<S*>(kc),
+                     static_cast<S*>(vc), cs, pos, slots, h, g);
+  return check_launch(op);
+}
+
+// Argument checks shared by the two fused entries.
+int check_rope_cache_args(const char* op, const void* q, const void* k, const void* v, const void* kc,
+                          const void* vc, const float* cs, const int32_t* pos, const int32_t* slots, int32_t h,
+                          int32_t hkv, int32_t d, int32_t bs, int32_t n, int32_t dtype, int64_t stride) {
+  int st = check_cache_args(op, k, v, kc, vc, slots, hkv, d, bs, n, dtype, stride);
+  if (st != RG_OK) return st;
+  if (h <= 0 || d % 2 != 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: need num_heads > 0 and an even head_dim", op);
+  }
+  if (h % hkv != 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: num_heads %d not a multiple of num_kv_heads %d", op, h, hkv);
+  }
+  if (n > 0 && (!q || !cs || !pos)) return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer", op);
+  return RG_OK;
 }
 
 }  // namespace
@@ -331,23 +359,51 @@ extern "C" int rg_rope_reshape_and_cache(void* q, const void* k, const void* v, 
                                          int32_t num_tokens, int32_t dtype,
                                          int64_t kv_block_stride, void* stream) {
   const char* op = "rope_reshape_and_cache";
-  int st = check_cache_args(op, k, v, k_cache, v_cache, slot_mapping, num_kv_heads, head_dim,
-                            block_size, num_tokens, dtype, kv_block_stride);
-  if (st != RG_OK) return st;
-  if (num_heads <= 0 || head_dim % 2 != 0) {
-    return fail(RG_ERR_INVALID_ARGUMENT, "%s: need num_heads > 0 and an even head_dim", op);
-  }
-  if (num_heads % num_kv_heads != 0) {
-    return fail(RG_ERR_INVALID_ARGUMENT, "%s: num_heads %d not a multiple of num_kv_heads %d", op,
-                num_heads, num_kv_heads);
-  }
-  if (num_tokens == 0) return ok();
-  if (!q || !cos_sin || !positions) return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer", op);
+  int st = check_rope_cache_args(op, q, k, v, k_cache, v_cache, cos_sin, positions, slot_mapping, num_heads,
+                                 num_kv_heads, head_dim, block_size, num_tokens, dtype, kv_block_stride);
+  if (st != RG_OK || num_tokens == 0) return st == RG_OK ? ok() : st;
   CacheGeom g{num_kv_heads, head_dim, block_size,
               kv_block_stride ? kv_block_stride : (int64_t)num_kv_heads * block_size * head_dim};
   hipStream_t s = as_stream(stream);
   return dispatch_dtype(dtype, [&](auto tag) {
-    return launch_rope_cache<decltype(tag)>(q, k, v, k_cache, v_cache, cos_sin, positions,
-                                            slot_mapping, num_heads, g, num_tokens, s);
+    using T = decltype(tag);
+    using S = typename elem<T>::storage;
+    const int64_t qs = (int64_t)num_heads * head_dim, kvs = (int64_t)num_kv_heads * head_dim;
+    const RopeRows<S> io{static_cast<const S*>(q), static_cast<S*>(q), static_cast<const S*>(k),
+                         static_cast<const S*>(v), qs, qs, kvs, kvs};
+    return launch_rope_cache<T>(io, k_cache, v_cache, cos_sin, positions, slot_mapping, num_heads, g, num_tokens,
+                                s, op);
+  });
+}
+
+extern "C" int rg_qkv_rope_reshape_and_cache(const void* qkv, int64_t qkv_token_stride, void* q_out,
+                                             void* k_cache, void* v_cache, const float* cos_sin,
+                                             const int32_t* positions, const int32_t* slot_mapping,
+                                             int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                             int32_t block_size, int32_t num_tokens, int32_t dtype,
+                                             int64_t kv_block_stride, void* stream) {
+  const char* op = "qkv_rope_reshape_and_cache";
+  const int64_t row = (int64_t)(num_heads + 2 * num_kv_heads) * head_dim;
+  int st = check_rope_cache_args(op, q_out, qkv, qkv, k_cache, v_cache, cos_sin, positions, slot_mapping,
+                                 num_heads, num_kv_heads, head_dim, block_size, num_tokens, dtype,
+                                 kv_block_stride);
+  if (st != RG_OK) return st;
+  if (qkv_token_stride < row) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: qkv_token_stride %lld shorter than a token's q, k and v (%lld)",
+                op, (long long)qkv_token_stride, (long long)row);
+  }
+  if (num_tokens == 0) return ok();
+  CacheGeom g{num_kv_heads, head_dim, block_size,
+              kv_block_stride ? kv_block_stride : (int64_t)num_kv_heads * block_size * head_dim};
+  hipStream_t s = as_stream(stream);
+  return dispatch_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    using S = typename elem<T>::storage;
+    const S* base = static_cast<const S*>(qkv);
+    const int64_t qd = (int64_t)num_heads * head_dim, kd = (int64_t)num_kv_heads * head_dim;
+    const RopeRows<S> io{base, static_cast<S*>(q_out), base + qd, base + qd + kd, qkv_token_stride, qd,
+                         qkv_token_stride, qkv_token_stride};
+    return launch_rope_cache<T>(io, k_cache, v_cache, cos_sin, positions, slot_mapping, num_heads, g, num_tokens,
+                                s, op);
   });
 }

@@ -1,0 +1,263 @@
+"""Llama forward pass (packed prefill + decode) over the attention hot path.
+
+Mirrors Railgun's model code (crates/vllm-models/src/llama/architecture.rs:11-165,
+attention.rs:85-155): ``RailgunLlama`` = embedding, ``LlamaLayer`` x N, final RMSNorm and
+the (tied) LM head; a layer is RMSNorm -> ``PagedSelfAttention`` -> residual add ->
+RMSNorm -> ``LlamaMLP`` (SwiGLU) -> residual add.  One engine step (prefill chunks first,
+then decode slots, :mod:`railgun_amd.batch`) runs as:
+
+* q, k and v from one GEMM with the concatenated projection weights, then
+  ``rg_qkv_rope_reshape_and_cache``: RoPE on q and k, k and v into this layer's paged cache,
+  one pass (the reference writes the cache but never applies RoPE, defect D10);
+* attention: ``rg_prefill_packed`` for the prefill rows (causal, MFMA), the stream-K
+  ``rg_paged_attention_v1`` for the decode rows (the reference sends prefill rows through
+  the decode op, D7);
+* ``rg_rms_norm`` fuses each residual add with the next RMSNorm; ``rg_silu_and_mul`` is the
+  SwiGLU gate; the GEMMs are hipBLASLt through torch (``F.linear``).
+
+Every layer owns a KV pool in Railgun's fused layout ``[NB, 2, H_kv, bs, D]``
+(crates/vllm-paged-attention/src/block.rs:70,89-95); the reference shares one pool across
+layers (D11).  Activations are bf16 (or the weights' dtype), arithmetic inside each kernel
+fp32, every op's result rounded once to the activation dtype, as in candle.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from .batch import StepBatch
+from .ops import PagedAttentionKernels, rms_norm, rope_cos_sin_table, silu_and_mul
+
+
+@dataclass(frozen=True)
+class LlamaConfig:
+    """The fields of candle's llama Config the model reads (crates/vllm-models/src/config.rs:30-67)."""
+
+    hidden_size: int = 2048
+    intermediate_size: int = 8192
+    num_hidden_layers: int = 16
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    vocab_size: int = 128256
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 500000.0
+    tie_word_embeddings: bool = True
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+    @property
+    def qkv_size(self) -> int:
+        return (self.num_attention_heads + 2 * self.num_key_value_heads) * self.head_dim
+
+
+LLAMA_3_2_1B = LlamaConfig()
+
+
+@dataclass
+class LayerWeights:
+    input_norm: torch.Tensor   # [hidden]
+    wqkv: torch.Tensor         # [(H + 2 H_kv) D, hidden]: q_proj, k_proj, v_proj stacked
+    wo: torch.Tensor           # [hidden, H D]
+    post_norm: torch.Tensor    # [hidden]
+    w_gate_up: torch.Tensor    # [2 I, hidden]: gate_proj, up_proj stacked
+    w_down: torch.Tensor       # [hidden, I]
+
+
+@dataclass
+class LlamaWeights:
+    embed: torch.Tensor        # [vocab, hidden]
+    layers: list
+    norm: torch.Tensor         # [hidden]
+    lm_head: torch.Tensor      # [vocab, hidden] (the embedding when tied)
+
+    @staticmethod
+    def random(cfg: LlamaConfig, seed: int, device, dtype=torch.bfloat16, std: float = 0.02,
+               norm_jitter: float = 0.0) -> "LlamaWeights":
+        """Random init: projections and embedding ~ N(0, std); norm weights 1 (+ N(0, jitter))."""
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+
+        def normal(*shape, s=std):
+            return (torch.randn(shape, generator=g, device=device, dtype=torch.float32) * s).to(dtype)
+
+        def norm_w():
+            w = torch.ones(cfg.hidden_size, device=device, dtype=torch.float32)
+            if norm_jitter:
+                w += torch.randn(cfg.hidden_size, generator=g, device=device) * norm_jitter
+            return w.to(dtype)
+
+        hd, inter = cfg.hidden_size, cfg.intermediate_size
+        embed = normal(cfg.vocab_size, hd)
+        layers = [LayerWeights(norm_w(), normal(cfg.qkv_size, hd), normal(hd, cfg.num_attention_heads * cfg.head_dim),
+                               norm_w(), normal(2 * inter, hd), normal(hd, inter))
+                  for _ in range(cfg.num_hidden_layers)]
+        norm = norm_w()
+        lm_head = embed if cfg.tie_word_embeddings else normal(cfg.vocab_size, hd)
+        return LlamaWeights(embed, layers, norm, lm_head)
+
+    @staticmethod
+    def from_state_dict(cfg: LlamaConfig, sd: dict, device, dtype=torch.bfloat16) -> "LlamaWeights":
+        """From Hugging Face Llama parameter names (the names architecture.rs loads, :24-28, :101-118)."""
+        def t(name):
+            return sd[name].to(device=device, dtype=dtype).contiguous()
+
+        layers = []
+        for i in range(cfg.num_hidden_layers):
+            p = f"model.layers.{i}."
+            wqkv = torch.cat([t(p + "self_attn.q_proj.weight"), t(p + "self_attn.k_proj.weight"),
+                              t(p + "self_attn.v_proj.weight")], 0).contiguous()
+            wgu = torch.cat([t(p + "mlp.gate_proj.weight"), t(p + "mlp.up_proj.weight")], 0).contiguous()
+            layers.append(LayerWeights(t(p + "input_layernorm.weight"), wqkv, t(p + "self_attn.o_proj.weight"),
+                                       t(p + "post_attention_layernorm.weight"), wgu, t(p + "mlp.down_proj.weight")))
+        embed = t("model.embed_tokens.weight")
+        lm_head = embed if cfg.tie_word_embeddings or "lm_head.weight" not in sd else t("lm_head.weight")
+        return LlamaWeights(embed, layers, t("model.norm.weight"), lm_head)
+
+    def nbytes(self) -> int:
+        """Bytes one forward reads: every weight once (the tied LM head counted again: the
+        embedding gather touches only the batch's rows, the LM head reads the whole matrix)."""
+        n = sum(w.numel() * w.element_size() for L in self.layers
+                for w in (L.input_norm, L.wqkv, L.wo, L.post_norm, L.w_gate_up, L.w_down))
+        return n + self.norm.numel() * self.norm.element_size() + self.lm_head.numel() * self.lm_head.element_size()
+
+
+class GpuBlockPool:
+    """Paged KV storage of every layer: ``[layers, NB, 2, H_kv, bs, D]``; layer l's K and V
+    caches are the views ``[l, :, 0]`` and ``[l, :, 1]`` of Railgun's fused per-block layout
+    (block.rs:70,89-95), block stride ``2 H_kv bs D`` elements."""
+
+    def __init__(self, cfg: LlamaConfig, num_blocks: int, block_size: int, device, dtype=torch.bfloat16,
+                 fill: Optional[torch.Generator] = None):
+        shape = (cfg.num_hidden_layers, num_blocks, 2, cfg.num_key_value_heads, block_size, cfg.head_dim)
+        if fill is None:
+            self.storage = torch.zeros(shape, device=device, dtype=dtype)
+        else:  # N(0, 1) contents, for measurements over a pre-filled context
+            self.storage = torch.empty(shape, device=device, dtype=dtype)
+            for layer in range(shape[0]):
+                self.storage[layer].copy_(torch.randn(shape[1:], generator=fill, device=device,
+                                                      dtype=torch.float32).to(dtype))
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+
+    def k_cache(self, layer: int) -> torch.Tensor:
+        return self.storage[layer, :, 0]
+
+    def v_cache(self, layer: int) -> torch.Tensor:
+        return self.storage[layer, :, 1]
+
+
+@dataclass
+class DeviceStep:
+    """A :class:`StepBatch` copied to the device, with the prefill / decode split views."""
+
+    host: StepBatch
+    tokens: torch.Tensor
+    positions: torch.Tensor
+    slot_mapping: torch.Tensor
+    context_lens: torch.Tensor
+    block_table: torch.Tensor
+    cu_seqlens: torch.Tensor
+    last_rows: torch.Tensor
+
+    @staticmethod
+    def from_host(b: StepBatch, device) -> "DeviceStep":
+        def d(a):
+            return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+        return DeviceStep(b, d(b.tokens), d(b.positions), d(b.slot_mapping), d(b.context_lens), d(b.block_table),
+                          d(b.cu_seqlens), d(b.last_rows))
+
+
+class RailgunLlama:
+    """architecture.rs:86-165 on the gfx950 kernels.  ``forward`` runs one packed engine
+    step and returns the logits of each request's last token ``[requests, vocab]``
+    (engine.rs:238-245 samples from those)."""
+
+    def __init__(self, cfg: LlamaConfig, weights: LlamaWeights, pool: GpuBlockPool,
+                 kernels: Optional[PagedAttentionKernels] = None, max_position: Optional[int] = None):
+        self.cfg = cfg
+        self.w = weights
+        self.pool = pool
+        self.device = weights.embed.device
+        self.dtype = weights.embed.dtype
+        self.kernels = kernels or PagedAttentionKernels(self.device)
+        max_pos = max_position or pool.num_blocks * pool.block_size
+        self.cos_sin = rope_cos_sin_table(max_pos, cfg.head_dim, cfg.rope_theta, self.device)
+        self.scale = 1.0 / math.sqrt(cfg.head_dim)  # attention.rs:69-70
+        self._ws = torch.empty(0, dtype=torch.uint8, device=self.device)
+        # Hook for measurements: called as attention_hook("begin"/"end", layer) around each
+        # layer's attention kernels (None in normal use).
+        self.attention_hook = None
+
+    def _workspace(self, nbytes: int) -> torch.Tensor:
+        if self._ws.numel() < nbytes:
+            self._ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    def _attention(self, layer: int, q: torch.Tensor, out: torch.Tensor, st: DeviceStep) -> None:
+        cfg, b, k = self.cfg, st.host, self.kernels
+        kc, vc = self.pool.k_cache(layer), self.pool.v_cache(layer)
+        H, Hkv, D, bs = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, self.pool.block_size
+        mb = int(st.block_table.shape[1])
+        P, TP = b.num_prefill_seqs, b.num_prefill_tokens
+        if P:
+            k.launch_prefill_packed(q[:TP], kc, vc, st.block_table[:P], st.context_lens[:P], st.cu_seqlens,
+                                    out[:TP], self.scale, H, Hkv, D, bs, mb, P, TP, b.max_query_len)
+        nd = b.num_decode
+        if nd:
+            ws = self._workspace(k.v1_workspace_bytes(nd, H, Hkv, D, bs, mb))
+            k.launch_v1(q[TP:], kc, vc, st.block_table[P:], st.context_lens[P:], out[TP:], self.scale, H, Hkv, D,
+                        bs, mb, nd, workspace=ws if ws.numel() else None)
+
+    def check_step(self, b: StepBatch) -> None:
+        """The kernels trust their indices (as the reference's do): check them on the host."""
+        if b.num_tokens and int(b.positions.max()) >= self.cos_sin.shape[0]:
+            raise ValueError(f"position {int(b.positions.max())} beyond the RoPE table ({self.cos_sin.shape[0]})")
+        if b.block_table.size and (int(b.block_table.max()) >= self.pool.num_blocks or int(b.block_table.min()) < 0):
+            raise ValueError(f"block id outside the pool of {self.pool.num_blocks} blocks")
+        if b.num_tokens and int(b.slot_mapping.max()) >= self.pool.num_blocks * self.pool.block_size:
+            raise ValueError("slot outside the pool")
+
+    @torch.no_grad()
+    def forward(self, st: DeviceStep) -> torch.Tensor:
+        cfg, w = self.cfg, self.w
+        self.check_step(st.host)
+        T = st.host.num_tokens
+        H, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        eps = cfg.rms_norm_eps
+        x = F.embedding(st.tokens, w.embed)                     # residual stream [T, hidden]
+        h = torch.empty_like(x)
+        q = torch.empty((T, H, D), device=self.device, dtype=self.dtype)
+        attn = torch.empty_like(q)
+        act = torch.empty((T, cfg.intermediate_size), device=self.device, dtype=self.dtype)
+        delta = None
+        for i, L in enumerate(w.layers):
+            # input_layernorm (with the previous MLP's residual add), architecture.rs:49-50
+            rms_norm(delta if delta is not None else x, L.input_norm, h, eps, residual=x if delta is not None else None)
+            qkv = F.linear(h, L.wqkv)
+            self.kernels.launch_qkv_rope_reshape_and_cache(qkv, q, self.pool.k_cache(i), self.pool.v_cache(i),
+                                                          self.cos_sin, st.positions, st.slot_mapping, H, Hkv, D,
+                                                          self.pool.block_size, T)
+            if self.attention_hook:
+                self.attention_hook("begin", i)
+            self._attention(i, q, attn, st)
+            if self.attention_hook:
+                self.attention_hook("end", i)
+            delta = F.linear(attn.view(T, H * D), L.wo)
+            # residual add + post_attention_layernorm, architecture.rs:53-57
+            rms_norm(delta, L.post_norm, h, eps, residual=x)
+            silu_and_mul(F.linear(h, L.w_gate_up), act)         # LlamaMLP, architecture.rs:80-84
+            delta = F.linear(act, L.w_down)
+        rms_norm(delta, w.norm, h, eps, residual=x)            # last residual add + model.norm
+        return F.linear(h.index_select(0, st.last_rows), w.lm_head)
+
+
+__all__ = ["DeviceStep", "GpuBlockPool", "LLAMA_3_2_1B", "LayerWeights", "LlamaConfig", "LlamaWeights",
+           "RailgunLlama"]

@@ -215,6 +215,21 @@ class PagedAttentionKernels:
             positions.data_ptr(), slot_mapping.data_ptr(), num_heads, num_kv_heads, head_dim, block_size,
             num_tokens, dtype_code(q), k_cache.stride(0), _stream(q)))
 
+    def launch_qkv_rope_reshape_and_cache(self, qkv, q_out, k_cache, v_cache, cos_sin, positions, slot_mapping,
+                                          num_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
+                                          num_tokens: int) -> None:
+        """Fused RoPE + cache write reading q/k/v from one fused projection output qkv
+        [T, >= (H + 2 H_kv) D] (row stride qkv.stride(0)); rotated q goes to q_out [T, H, D]."""
+        _require_cuda(qkv, q_out, k_cache, v_cache, cos_sin, positions, slot_mapping)
+        _require_i32(positions, slot_mapping)
+        if qkv.dim() != 2 or qkv.stride(1) != 1 or not q_out.is_contiguous():
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "qkv must be [T, N] with unit column stride and "
+                                                             "q_out contiguous")
+        check(self.lib.rg_qkv_rope_reshape_and_cache(
+            qkv.data_ptr(), qkv.stride(0), q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+            cos_sin.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(), num_heads, num_kv_heads, head_dim,
+            block_size, num_tokens, dtype_code(qkv), k_cache.stride(0), _stream(qkv)))
+
     def launch_prefill_packed(self, query, key_cache, value_cache, block_table, context_lens, cu_seqlens,
                               output, scale: float, num_heads: int, num_kv_heads: int, head_dim: int,
                               block_size: int, max_blocks_per_seq: int, num_seqs: int, num_tokens: int,
@@ -315,5 +330,34 @@ class PagedAttentionOp:
         return out
 
 
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, eps: float,
+             residual: Optional[torch.Tensor] = None) -> None:
+    """Fused residual add + RMSNorm over the rows of x [rows, hidden] (rg_rms_norm): with a
+    residual, residual <- residual + x and out <- rmsnorm(residual) * weight; without,
+    out <- rmsnorm(x) * weight."""
+    _require_cuda(x, weight, out, residual)
+    for t in (x, weight, out, residual):
+        if t is not None and (not t.is_contiguous() or t.dtype != x.dtype):
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "rms_norm: tensors must be contiguous and share a dtype")
+    hidden = int(x.shape[-1])
+    rows = x.numel() // hidden if hidden else 0
+    if weight.numel() != hidden or out.shape != x.shape or (residual is not None and residual.shape != x.shape):
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "rms_norm: shape mismatch")
+    check(load_library().rg_rms_norm(x.data_ptr(), _ptr(residual), weight.data_ptr(), out.data_ptr(), float(eps),
+                                     rows, hidden, dtype_code(x), _stream(x)))
+
+
+def silu_and_mul(gate_up: torch.Tensor, out: torch.Tensor) -> None:
+    """out [rows, I] = silu(gate_up[:, :I]) * gate_up[:, I:] (rg_silu_and_mul)."""
+    _require_cuda(gate_up, out)
+    if not gate_up.is_contiguous() or not out.is_contiguous() or gate_up.dtype != out.dtype:
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "silu_and_mul: tensors must be contiguous, one dtype")
+    rows, inter = int(out.shape[0]), int(out.shape[-1])
+    if tuple(gate_up.shape) != (rows, 2 * inter):
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "silu_and_mul: gate_up must be [rows, 2 * I]")
+    check(load_library().rg_silu_and_mul(gate_up.data_ptr(), out.data_ptr(), rows, inter, dtype_code(out),
+                                         _stream(out)))
+
+
 __all__ = ["PagedAttentionKernels", "PagedAttentionOp", "RailgunError", "cache_geometry", "dtype_code",
-           "rope_cos_sin_table", "V1_MAX_CONTEXT", "V2_PARTITION_SIZE"]
+           "rms_norm", "rope_cos_sin_table", "silu_and_mul", "V1_MAX_CONTEXT", "V2_PARTITION_SIZE"]
