@@ -50,7 +50,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-side", action="store_true", help="skip the config 3 / config 4 side figures")
-    ap.add_argument("--only", choices=["decode", "v2", "prefill", "copy"], default=None,
+    ap.add_argument("--only", choices=["decode", "v2", "prefill", "model", "copy"], default=None,
                     help="run one workload only and print its figures (for profiling); 'copy' is the plain "
                          "1 GiB device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
@@ -212,6 +212,72 @@ def side_prefill(device, gen, steps: int) -> dict:
             "traffic": measured_traffic("prefill_config4")}
 
 
+def side_model(device, steps: int) -> dict:
+    """Config 5: one decode step of a random-init Llama-3.2-1B (16 layers, bf16 weights ~ N(0, 0.02))
+    for 128 sequences with contexts U[64, 8192] over per-layer paged pools pre-filled with N(0, 1).
+    The step runs as a captured HIP graph when its replays reproduce the eager logits bit for
+    bit (eager otherwise); the attention share is the 16 layers' attention calls timed alone."""
+    import numpy as np
+    import torch
+
+    from railgun_amd import workloads as wl
+    from railgun_amd.batch import DecodeSlot, pack_step
+    from railgun_amd.llama import LLAMA_3_2_1B as cfg
+    from railgun_amd.llama import DeviceStep, GpuBlockPool, LlamaWeights, RailgunLlama
+
+    w = wl.config5()
+    weights = LlamaWeights.random(cfg, 5, device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(w.seed)
+    pool = GpuBlockPool(cfg, w.num_blocks, w.block_size, device, fill=gen)
+    model = RailgunLlama(cfg, weights, pool, max_position=int(w.context_lens.max()))
+    rng = np.random.default_rng(w.seed)
+    toks = rng.integers(0, cfg.vocab_size, w.batch)
+    slots = [DecodeSlot(int(t), int(c), w.block_table[s, :(int(c) + w.block_size - 1) // w.block_size].tolist())
+             for s, (t, c) in enumerate(zip(toks, w.context_lens))]
+    st = DeviceStep.from_host(pack_step([], slots, w.block_size, max_blocks=w.block_table.shape[1]), device)
+
+    eager_ms = time_events(lambda: model.forward(st), steps, 3)
+    ref = model.forward(st)
+    mode, step_ms = "eager", eager_ms
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        model.forward(st)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(graph):
+        out = model.forward(st)
+    same = True
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        same &= bool(torch.equal(out, ref))
+        model.forward(st)  # eager work between replays
+        torch.cuda.synchronize()
+    if same:
+        graph_ms = time_events(graph.replay, steps, 2)
+        if graph_ms < eager_ms:
+            mode, step_ms = "hip_graph", graph_ms
+    # attention alone: the same 16 layers' decode attention calls back to back
+    H, D = cfg.num_attention_heads, cfg.head_dim
+    q = torch.randn((w.batch, H, D), device=device, dtype=torch.float32).to(torch.bfloat16)
+    o = torch.empty_like(q)
+    attn_ms = time_events(lambda: [model._attention(i, q, o, st) for i in range(cfg.num_hidden_layers)], steps, 2)
+    kv = w.kv_bytes(cfg.num_hidden_layers, cfg.num_key_value_heads, D)
+    step_bytes = weights.nbytes() + kv
+    del model, pool, weights, graph
+    torch.cuda.empty_cache()
+    return {"workload": w.name, "model": "llama-3.2-1b (random init, bf16)", "batch": w.batch,
+            "context": "U[64,8192]", "context_tokens": int(w.context_lens.sum()), "mode": mode,
+            "step_us": round(step_ms * 1e3, 1), "eager_step_us": round(eager_ms * 1e3, 1),
+            "graph_matches_eager": same, "tokens_per_s": round(w.batch / (step_ms * 1e-3), 1),
+            "attention_us": round(attn_ms * 1e3, 1), "attention_share": round(attn_ms / step_ms, 4),
+            "attention_GB/s": round(kv / (attn_ms * 1e-3) / 1e9, 1),
+            "step_bytes": step_bytes, "step_GB/s": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(step_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def copy_calibration(device, steps: int) -> dict:
     """A plain device copy of 1 GiB (torch's copy kernel): reads and writes exactly 1 GiB per
     launch, which is what the HBM counters of a profile are scaled against."""
@@ -244,6 +310,9 @@ def main() -> int:
         return 0
     if args.only == "prefill":
         print(json.dumps(side_prefill(device, gen, args.steps)), flush=True)
+        return 0
+    if args.only == "model":
+        print(json.dumps(side_model(device, args.steps)), flush=True)
         return 0
     if args.only == "copy":
         print(json.dumps(copy_calibration(device, args.steps)), flush=True)
@@ -305,6 +374,8 @@ def main() -> int:
         result["v2_long_context"] = side_v2(device, gen, max(3, args.steps // 5))
         log("[bench] config4 prefill ...")
         result["prefill"] = side_prefill(device, gen, 10)
+        log("[bench] config5 model step ...")
+        result["model_step"] = side_model(device, 10)
     if not args.no_cpu:
         log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w)

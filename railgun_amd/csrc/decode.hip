@@ -517,7 +517,13 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 #ifndef RG_SK_PREFETCH
 #define RG_SK_PREFETCH 3
 #endif
-constexpr int kSkPrefetch = RG_SK_PREFETCH;
+// head_dim 64 halves a unit's bytes (2 KB of K + 2 KB of V), so twice as many units stay in
+// flight for the same bytes per wave.
+#ifndef RG_SK_PREFETCH_D64
+#define RG_SK_PREFETCH_D64 4
+#endif
+template <int D>
+constexpr int sk_prefetch() { return D <= 64 ? RG_SK_PREFETCH_D64 : RG_SK_PREFETCH; }
 
 // Optional occupancy floor of the stream-K kernel (waves per SIMD).
 #if defined(RG_SK_OCC) && RG_SK_OCC > 0
@@ -601,6 +607,7 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   constexpr int HG = Tile::HG;
   constexpr int NK = Tile::NK;
   constexpr int NV = Tile::NV;
+  constexpr int kSkPrefetch = sk_prefetch<D>();
   constexpr int NBUF = kSkPrefetch + 1;
   __shared__ float p_lds[2][kBS * GP];
   __shared__ float alpha_lds[2][GP];
@@ -788,32 +795,28 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   }(std::make_integer_sequence<int, NBUF - 1>{});
 }
 
-// One workgroup per (segment, head of the group): merges the partials of workers
-// worker_of(first unit) .. worker_of(last unit) of the segment and writes one output row.
-// Threads split over (pairs of dims) x (groups of partials).  Each thread folds its strided
-// subset of partials with an online rescale, so the (m, l, acc) loads of all its partials are
-// issued together; the groups are then combined through LDS.
-constexpr int kMergeThreads = 256;
-
+// One workgroup per segment (sequence, kv-head), one wave per head of the group: merges the
+// partials of workers worker_of(first unit) .. worker_of(last unit) of the segment and writes
+// the G output rows.  Lane l of wave h holds dims [l*D/64, (l+1)*D/64) of head h, so each
+// partial's [G, D] accumulator is read as one contiguous row by the whole workgroup; every
+// lane folds the partials in order with an online rescale (loads of consecutive partials
+// are independent, so they are issued ahead of the folds).
 template <typename T, int D, int G>
-__global__ __launch_bounds__(kMergeThreads) void decode_stream_merge_kernel(StreamArgs a,
-                                                                           const int32_t* __restrict__ context_lens) {
+__global__ __launch_bounds__(64 * G) void decode_stream_merge_kernel(StreamArgs a,
+                                                                    const int32_t* __restrict__ context_lens) {
   using S = uint16_t;
-  constexpr int NPAIR = D / 2;                  // dim pairs per row
-  constexpr int NGRP = kMergeThreads / NPAIR;   // partial groups
-  __shared__ float2 acc_lds[NGRP][NPAIR];
-  __shared__ float ml_lds[NGRP][2];
-
-  const int h = blockIdx.x % G;
-  const int kvh = blockIdx.x / G;
+  constexpr int PER = D / 64;  // dims per lane
+  static_assert(PER == 1 || PER == 2, "head_dim 64 or 128");
+  const int kvh = blockIdx.x;
   const int s = blockIdx.y;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
+  const int h = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int hkv = a.num_kv_heads;
-  S* out = static_cast<S*>(a.out) + ((int64_t)s * a.num_heads + (int64_t)kvh * G + h) * D;
+  S* out = static_cast<S*>(a.out) + ((int64_t)s * a.num_heads + (int64_t)kvh * G + h) * D + lane * PER;
   const int nblk = seq_blocks(context_lens, s, a.max_blocks);
   if (nblk == 0) {
-    for (int i = tid; i < D; i += kMergeThreads) out[i] = 0;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) out[e] = 0;
     return;
   }
   // Total units and the segment's first unit (one pass over the context lengths).
@@ -832,46 +835,37 @@ __global__ __launch_bounds__(kMergeThreads) void decode_stream_merge_kernel(Stre
   const int64_t pbase = first + (int64_t)s * hkv + kvh;  // partial index of worker `first`
   const int np = (int)(last - first + 1);
 
-  const int pair = tid % NPAIR;
-  const int grp = tid / NPAIR;
   float m = -INFINITY, l = 0.f;
-  float2 acc = make_float2(0.f, 0.f);
+  float acc[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) acc[e] = 0.f;
 #pragma unroll 4
-  for (int q = grp; q < np; q += NGRP) {
+  for (int q = 0; q < np; ++q) {
     const int64_t pi = pbase + q;
-    const float mq = a.part_ml[pi * (2 * G) + 2 * h];
-    const float lq = a.part_ml[pi * (2 * G) + 2 * h + 1];
-    const float2 v = *reinterpret_cast<const float2*>(a.part_acc + pi * (G * D) + h * D + 2 * pair);
-    const float mn = fmaxf(m, mq);
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + pi * (2 * G) + 2 * h);
+    const float* pa = a.part_acc + pi * (G * D) + h * D + lane * PER;
+    float v[PER];
+    if constexpr (PER == 2) {
+      const float2 t = *reinterpret_cast<const float2*>(pa);
+      v[0] = t.x;
+      v[1] = t.y;
+    } else {
+      v[0] = pa[0];
+    }
+    const float mn = fmaxf(m, ml.x);
     const float fo = exp2f(m - mn);  // 0 for the first partial (m = -inf)
-    const float fq = exp2f(mq - mn);
-    l = l * fo + lq * fq;
-    acc.x = acc.x * fo + v.x * fq;
-    acc.y = acc.y * fo + v.y * fq;
+    const float fq = exp2f(ml.x - mn);
+    l = l * fo + ml.y * fq;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) acc[e] = acc[e] * fo + v[e] * fq;
     m = mn;
   }
-  acc_lds[grp][pair] = acc;
-  if (pair == 0) {
-    ml_lds[grp][0] = m;
-    ml_lds[grp][1] = l;
-  }
-  __syncthreads();
-  if (grp == 0) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int g2 = 0; g2 < NGRP; ++g2) M = fmaxf(M, ml_lds[g2][0]);
-    float L = 0.f, ox = 0.f, oy = 0.f;
-#pragma unroll
-    for (int g2 = 0; g2 < NGRP; ++g2) {
-      const float mg = ml_lds[g2][0];
-      const float f = mg == -INFINITY ? 0.f : exp2f(mg - M);
-      L += f * ml_lds[g2][1];
-      ox += f * acc_lds[g2][pair].x;
-      oy += f * acc_lds[g2][pair].y;
-    }
-    const float inv = L != 0.f ? 1.f / L : 1.f;
-    const uint32_t packed = (uint32_t)elem<T>::from_f32(ox * inv) | ((uint32_t)elem<T>::from_f32(oy * inv) << 16);
-    *reinterpret_cast<uint32_t*>(out + 2 * pair) = packed;
+  const float inv = l != 0.f ? 1.f / l : 1.f;
+  if constexpr (PER == 2) {
+    const uint32_t packed = (uint32_t)elem<T>::from_f32(acc[0] * inv) | ((uint32_t)elem<T>::from_f32(acc[1] * inv) << 16);
+    *reinterpret_cast<uint32_t*>(out) = packed;
+  } else {
+    out[0] = elem<T>::from_f32(acc[0] * inv);
   }
 }
 
@@ -1141,8 +1135,8 @@ void launch_stream(const StreamArgs& sa, const DecodeArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((decode_stream_kernel<T, D, G>), dim3(sa.num_workers), dim3(64), 0, s, sa,
                      static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.k_cache),
                      static_cast<const uint16_t*>(a.v_cache), a.block_table, a.context_lens);
-  hipLaunchKernelGGL((decode_stream_merge_kernel<T, D, G>), dim3(sa.num_kv_heads * G, sa.batch),
-                     dim3(kMergeThreads), 0, s, sa, a.context_lens);
+  hipLaunchKernelGGL((decode_stream_merge_kernel<T, D, G>), dim3(sa.num_kv_heads, sa.batch), dim3(64 * G), 0, s,
+                     sa, a.context_lens);
 }
 
 template <typename T, int D>
