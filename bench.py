@@ -223,13 +223,14 @@ def side_model(device, steps: int) -> dict:
     from railgun_amd import workloads as wl
     from railgun_amd.batch import DecodeSlot, pack_step
     from railgun_amd.llama import LLAMA_3_2_1B as cfg
-    from railgun_amd.llama import DeviceStep, GpuBlockPool, LlamaWeights, RailgunLlama
+    from railgun_amd.kv_pool import GpuBlockPool
+    from railgun_amd.llama import DeviceStep, LlamaWeights, RailgunLlama
 
     w = wl.config5()
     weights = LlamaWeights.random(cfg, 5, device)
     gen = torch.Generator(device=device)
     gen.manual_seed(w.seed)
-    pool = GpuBlockPool(cfg, w.num_blocks, w.block_size, device, fill=gen)
+    pool = GpuBlockPool.for_model(cfg, w.num_blocks, w.block_size, device, fill=gen)
     model = RailgunLlama(cfg, weights, pool, max_position=int(w.context_lens.max()))
     rng = np.random.default_rng(w.seed)
     toks = rng.integers(0, cfg.vocab_size, w.batch)

@@ -154,6 +154,25 @@ int rg_qkv_rope_reshape_and_cache(const void* qkv, int64_t qkv_token_stride,
                                   int32_t dtype, int64_t kv_block_stride,
                                   void* stream);
 
+/* Copies whole KV blocks between two pools: for i < num_pairs and every layer
+ * l < num_layers, the block_bytes bytes at
+ *   src_pool + l*src_layer_stride_bytes + block_mapping[2i]*src_block_stride_bytes
+ * go to
+ *   dst_pool + l*dst_layer_stride_bytes + block_mapping[2i+1]*dst_block_stride_bytes.
+ * A bit-exact copy.  The pools may be device memory or device-accessible pinned host
+ * memory (hipHostMalloc), so one entry serves GPU -> CPU swap-out, CPU -> GPU swap-in and
+ * GPU -> GPU copy-on-write; block_mapping must be device-accessible too.  Sizes and
+ * strides are multiples of 16 bytes, pools 16-byte aligned; destinations must not overlap
+ * each other or the sources.  With Railgun's fused pool [NB, 2, H_kv, bs, D] one block
+ * (K and V) is contiguous: block_bytes = stride = 2*H_kv*bs*D*elem.  New entry: the
+ * reference's swap_out / swap_in move block ids between free lists but copy no data
+ * (crates/vllm-paged-attention/src/allocator.rs:102-153, "TODO ... physical update"). */
+int rg_copy_blocks(const void* src_pool, void* dst_pool, const int32_t* block_mapping,
+                   int32_t num_pairs, int64_t block_bytes, int64_t src_block_stride_bytes,
+                   int64_t dst_block_stride_bytes, int32_t num_layers,
+                   int64_t src_layer_stride_bytes, int64_t dst_layer_stride_bytes,
+                   void* stream);
+
 /* ------------------------------------------------- model element-wise ops -- */
 
 /* Fused residual add + RMSNorm over rows of hidden_size elements:

@@ -5,6 +5,8 @@
 // token with 16-byte vector moves along the contiguous head_dim rows wherever the row length
 // and the pointers allow it; the RoPE kernels run one wave per (token, head row) so that a
 // decode step's few tokens still spread over thousands of waves.
+#include <algorithm>
+
 #include "rg_common.hpp"
 
 namespace rg {
@@ -197,6 +199,28 @@ __global__ __launch_bounds__(kCacheThreads) void rope_cache_kernel(
     S* dst = v_cache + cache_row(g, blk, h, off);
     for (int i = lane; i < D; i += 64) dst[i] = src[i];
   }
+}
+
+// ---------------------------------------------------------------- block copy ----
+
+// Whole-block copies between two pools: grid (pairs, layers, slices).  Pair i copies block
+// mapping[2i] of the source to block mapping[2i+1] of the destination in every layer; a
+// block's bytes are split into `slices` ranges so that large blocks spread over several
+// workgroups.  16-byte moves (sizes and strides checked to be multiples of 16 on the host).
+__global__ __launch_bounds__(kCacheThreads) void copy_blocks_kernel(const uint4* __restrict__ src,
+                                                                    uint4* __restrict__ dst,
+                                                                    const int32_t* __restrict__ mapping,
+                                                                    int64_t block_vecs, int64_t src_block_vecs,
+                                                                    int64_t dst_block_vecs, int64_t src_layer_vecs,
+                                                                    int64_t dst_layer_vecs, int64_t slice_vecs) {
+  const int64_t pair = blockIdx.x;
+  const int64_t layer = blockIdx.y;
+  const int64_t b0 = (int64_t)blockIdx.z * slice_vecs;
+  const int64_t b1 = min(b0 + slice_vecs, block_vecs);
+  const int64_t sb = mapping[2 * pair], db = mapping[2 * pair + 1];
+  const uint4* s = src + layer * src_layer_vecs + sb * src_block_vecs;
+  uint4* d = dst + layer * dst_layer_vecs + db * dst_block_vecs;
+  for (int64_t i = b0 + threadIdx.x; i < b1; i += kCacheThreads) d[i] = s[i];
 }
 
 // ------------------------------------------------------------ host side ----
@@ -406,4 +430,54 @@ extern "C" int rg_qkv_rope_reshape_and_cache(const void* qkv, int64_t qkv_token_
     return launch_rope_cache<T>(io, k_cache, v_cache, cos_sin, positions, slot_mapping, num_heads, g, num_tokens,
                                 s, op);
   });
+}
+
+extern "C" int rg_copy_blocks(const void* src_pool, void* dst_pool, const int32_t* block_mapping,
+                              int32_t num_pairs, int64_t block_bytes, int64_t src_block_stride_bytes,
+                              int64_t dst_block_stride_bytes, int32_t num_layers, int64_t src_layer_stride_bytes,
+                              int64_t dst_layer_stride_bytes, void* stream) {
+  const char* op = "copy_blocks";
+  if (num_pairs < 0 || num_layers < 0 || block_bytes < 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: negative num_pairs, num_layers or block_bytes", op);
+  }
+  if (num_pairs == 0 || num_layers == 0 || block_bytes == 0) return ok();
+  if (!src_pool || !dst_pool || !block_mapping) return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer", op);
+  if (src_block_stride_bytes < block_bytes || dst_block_stride_bytes < block_bytes) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: block stride smaller than block_bytes", op);
+  }
+  if (num_layers > 1 && (src_layer_stride_bytes <= 0 || dst_layer_stride_bytes <= 0)) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: layer strides must be positive with num_layers > 1", op);
+  }
+  if (num_layers > 65535) return fail(RG_ERR_INVALID_ARGUMENT, "%s: num_layers > 65535", op);
+  const int64_t all[5] = {block_bytes, src_block_stride_bytes, dst_block_stride_bytes,
+                          num_layers > 1 ? src_layer_stride_bytes : 0, num_layers > 1 ? dst_layer_stride_bytes : 0};
+  for (int64_t v : all) {
+    if (v % 16 != 0) return fail(RG_ERR_NOT_SUPPORTED, "%s: sizes and strides must be multiples of 16 bytes", op);
+  }
+  if (!aligned16(src_pool) || !aligned16(dst_pool)) {
+    return fail(RG_ERR_NOT_SUPPORTED, "%s: pool pointers must be 16-byte aligned", op);
+  }
+  // The kernel dereferences all three pointers: each must be memory HIP knows (device
+  // memory, or pinned host memory mapped into the device's address space), never pageable
+  // host memory.
+  const void* ptrs[3] = {src_pool, dst_pool, block_mapping};
+  const char* names[3] = {"src_pool", "dst_pool", "block_mapping"};
+  for (int i = 0; i < 3; ++i) {
+    hipPointerAttribute_t at;
+    if (hipPointerGetAttributes(&at, ptrs[i]) != hipSuccess || at.devicePointer == nullptr ||
+        (at.type != hipMemoryTypeDevice && at.type != hipMemoryTypeHost) || at.isManaged) {
+      (void)hipGetLastError();
+      return fail(RG_ERR_INVALID_ARGUMENT, "%s: %s is neither device memory nor pinned host memory", op, names[i]);
+    }
+  }
+  const int64_t vecs = block_bytes / 16;
+  // Slices of at least 16 KB per workgroup.
+  const int64_t slice = std::max<int64_t>(1024, ceil_div(vecs, 64));
+  const int64_t slices = ceil_div(vecs, slice);
+  const dim3 grid((unsigned)num_pairs, (unsigned)num_layers, (unsigned)slices);
+  hipLaunchKernelGGL(copy_blocks_kernel, grid, dim3(kCacheThreads), 0, as_stream(stream),
+                     static_cast<const uint4*>(src_pool), static_cast<uint4*>(dst_pool), block_mapping, vecs,
+                     src_block_stride_bytes / 16, dst_block_stride_bytes / 16, src_layer_stride_bytes / 16,
+                     dst_layer_stride_bytes / 16, slice);
+  return check_launch(op);
 }

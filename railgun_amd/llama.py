@@ -31,6 +31,7 @@ import torch
 import torch.nn.functional as F
 
 from .batch import StepBatch
+from .kv_pool import GpuBlockPool
 from .ops import PagedAttentionKernels, rms_norm, rope_cos_sin_table, silu_and_mul
 
 
@@ -126,31 +127,6 @@ class LlamaWeights:
         n = sum(w.numel() * w.element_size() for L in self.layers
                 for w in (L.input_norm, L.wqkv, L.wo, L.post_norm, L.w_gate_up, L.w_down))
         return n + self.norm.numel() * self.norm.element_size() + self.lm_head.numel() * self.lm_head.element_size()
-
-
-class GpuBlockPool:
-    """Paged KV storage of every layer: ``[layers, NB, 2, H_kv, bs, D]``; layer l's K and V
-    caches are the views ``[l, :, 0]`` and ``[l, :, 1]`` of Railgun's fused per-block layout
-    (block.rs:70,89-95), block stride ``2 H_kv bs D`` elements."""
-
-    def __init__(self, cfg: LlamaConfig, num_blocks: int, block_size: int, device, dtype=torch.bfloat16,
-                 fill: Optional[torch.Generator] = None):
-        shape = (cfg.num_hidden_layers, num_blocks, 2, cfg.num_key_value_heads, block_size, cfg.head_dim)
-        if fill is None:
-            self.storage = torch.zeros(shape, device=device, dtype=dtype)
-        else:  # N(0, 1) contents, for measurements over a pre-filled context
-            self.storage = torch.empty(shape, device=device, dtype=dtype)
-            for layer in range(shape[0]):
-                self.storage[layer].copy_(torch.randn(shape[1:], generator=fill, device=device,
-                                                      dtype=torch.float32).to(dtype))
-        self.num_blocks = num_blocks
-        self.block_size = block_size
-
-    def k_cache(self, layer: int) -> torch.Tensor:
-        return self.storage[layer, :, 0]
-
-    def v_cache(self, layer: int) -> torch.Tensor:
-        return self.storage[layer, :, 1]
 
 
 @dataclass
@@ -259,5 +235,5 @@ class RailgunLlama:
         return F.linear(h.index_select(0, st.last_rows), w.lm_head)
 
 
-__all__ = ["DeviceStep", "GpuBlockPool", "LLAMA_3_2_1B", "LayerWeights", "LlamaConfig", "LlamaWeights",
+__all__ = ["DeviceStep", "LLAMA_3_2_1B", "LayerWeights", "LlamaConfig", "LlamaWeights",
            "RailgunLlama"]

@@ -230,6 +230,42 @@ class PagedAttentionKernels:
             cos_sin.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(), num_heads, num_kv_heads, head_dim,
             block_size, num_tokens, dtype_code(qkv), k_cache.stride(0), _stream(qkv)))
 
+    def launch_copy_blocks(self, src_pool: torch.Tensor, dst_pool: torch.Tensor, block_mapping: torch.Tensor,
+                           layered: bool = False) -> None:
+        """Whole-block copies (rg_copy_blocks): block ``m[i, 1]`` of ``dst_pool`` becomes block
+        ``m[i, 0]`` of ``src_pool``, in every layer when ``layered``.
+
+        Pools are ``[NB, ...]`` (``layered=False``) or ``[layers, NB, ...]`` with contiguous
+        blocks and the same block shape and dtype on both sides; each may live on the device
+        or in pinned host memory.  ``block_mapping`` is int32 ``[pairs, 2]`` of (source,
+        destination) ids, on the device or pinned.  Asynchronous on the current stream of the
+        device side's device.
+        """
+        bdim = 1 if layered else 0
+        if src_pool.dtype != dst_pool.dtype or src_pool.dim() != dst_pool.dim() or src_pool.dim() < bdim + 1:
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "copy_blocks: pools must share dtype and rank")
+        if tuple(src_pool.shape[bdim + 1:]) != tuple(dst_pool.shape[bdim + 1:]) or \
+                (layered and src_pool.shape[0] != dst_pool.shape[0]):
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "copy_blocks: block shapes or layer counts differ")
+        for p in (src_pool, dst_pool):
+            if not p[(0,) * (bdim + 1)].is_contiguous():
+                raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "copy_blocks: blocks must be contiguous")
+            if not (p.is_cuda or p.is_pinned()):
+                raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "copy_blocks: pools must be on the GPU or pinned")
+        m = block_mapping
+        if m.dtype != torch.int32 or not m.is_contiguous() or m.dim() != 2 or m.shape[1] != 2 or \
+                not (m.is_cuda or m.is_pinned()):
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT,
+                               "copy_blocks: block_mapping must be contiguous int32 [pairs, 2], on the GPU or pinned")
+        es = src_pool.element_size()
+        block_bytes = src_pool[(0,) * (bdim + 1)].numel() * es
+        dev = src_pool.device if src_pool.is_cuda else dst_pool.device
+        stream = torch.cuda.current_stream(dev).cuda_stream if dev.type == "cuda" else 0
+        check(self.lib.rg_copy_blocks(
+            src_pool.data_ptr(), dst_pool.data_ptr(), m.data_ptr(), int(m.shape[0]), block_bytes,
+            src_pool.stride(bdim) * es, dst_pool.stride(bdim) * es, int(src_pool.shape[0]) if layered else 1,
+            src_pool.stride(0) * es if layered else 0, dst_pool.stride(0) * es if layered else 0, stream))
+
     def launch_prefill_packed(self, query, key_cache, value_cache, block_table, context_lens, cu_seqlens,
                               output, scale: float, num_heads: int, num_kv_heads: int, head_dim: int,
                               block_size: int, max_blocks_per_seq: int, num_seqs: int, num_tokens: int,

@@ -22,7 +22,8 @@ import torch
 
 from oracle import llama_ref
 from railgun_amd.batch import DecodeSlot, PrefillChunk, pack_step
-from railgun_amd.llama import DeviceStep, GpuBlockPool, LlamaConfig, LlamaWeights, RailgunLlama
+from railgun_amd.kv_pool import GpuBlockPool
+from railgun_amd.llama import DeviceStep, LlamaConfig, LlamaWeights, RailgunLlama
 from railgun_amd.ops import rms_norm, rope_cos_sin_table, silu_and_mul
 
 pytestmark = pytest.mark.gpu
@@ -146,7 +147,7 @@ def test_llama_prefill_decode_mixed(device, kernels, name):
     bs, nb = 16, 96
     sd = _hf_state(cfg, 11)
     w = LlamaWeights.from_state_dict(cfg, sd, device)
-    pool = GpuBlockPool(cfg, nb, bs, device)
+    pool = GpuBlockPool.for_model(cfg, nb, bs, device)
     model = RailgunLlama(cfg, w, pool, kernels, max_position=4096)
     ref32 = llama_ref.ReferenceLlama(cfg, sd, nb, bs)
     ref16 = llama_ref.ReferenceLlama(cfg, sd, nb, bs, act_dtype=torch.bfloat16)

@@ -96,6 +96,41 @@ def test_argument_checks_without_gpu():
     assert st == _lib.RG_ERR_INVALID_ARGUMENT and "without sequences" in msg
 
 
+def test_model_entry_argument_checks_without_gpu():
+    """rg_copy_blocks / rg_rms_norm / rg_silu_and_mul / rg_qkv_rope_reshape_and_cache reject bad
+    arguments before touching the GPU."""
+    st, msg = call("rg_copy_blocks", None, None, None, -1, 16, 16, 16, 1, 0, 0, None)
+    assert st == _lib.RG_ERR_INVALID_ARGUMENT
+    st, msg = call("rg_copy_blocks", None, None, None, 0, 16, 16, 16, 1, 0, 0, None)
+    assert st == _lib.RG_OK  # nothing to copy
+    st, msg = call("rg_copy_blocks", None, None, None, 3, 16, 16, 16, 1, 0, 0, None)
+    assert st == _lib.RG_ERR_INVALID_ARGUMENT and "null pointer" in msg
+    buf = np.zeros(64, np.float32)
+    p = buf.ctypes.data
+    st, msg = call("rg_copy_blocks", p, p, p, 1, 32, 16, 32, 1, 0, 0, None)
+    assert st == _lib.RG_ERR_INVALID_ARGUMENT and "stride smaller" in msg
+    st, msg = call("rg_copy_blocks", p, p, p, 1, 24, 32, 32, 1, 0, 0, None)
+    assert st == _lib.RG_ERR_NOT_SUPPORTED and "multiples of 16" in msg
+    st, msg = call("rg_copy_blocks", p, p, p, 1, 32, 32, 32, 2, 0, 64, None)
+    assert st == _lib.RG_ERR_INVALID_ARGUMENT and "layer strides" in msg
+    st, msg = call("rg_rms_norm", None, None, None, None, 1e-5, 4, 0, _lib.RG_DTYPE_BF16, None)
+    assert st == _lib.RG_ERR_INVALID_ARGUMENT
+    st, msg = call("rg_rms_norm", None, None, None, None, 1e-5, 4, 64, _lib.RG_DTYPE_BF16, None)
+    assert st == _lib.RG_ERR_INVALID_ARGUMENT and "null pointer" in msg
+    st, msg = call("rg_rms_norm", None, None, None, None, 1e-5, 0, 64, _lib.RG_DTYPE_BF16, None)
+    assert st == _lib.RG_OK
+    st, msg = call("rg_silu_and_mul", None, None, 70000, 64, _lib.RG_DTYPE_BF16, None)
+    assert st == _lib.RG_ERR_INVALID_ARGUMENT
+    st, msg = call("rg_silu_and_mul", None, None, 2, 64, 7, None)
+    assert st == _lib.RG_ERR_NOT_SUPPORTED
+    st, msg = call("rg_qkv_rope_reshape_and_cache", p, 100, p, p, p, p, p, p, 32, 8, 64, 16, 4, _lib.RG_DTYPE_BF16,
+                   0, None)
+    assert st == _lib.RG_ERR_INVALID_ARGUMENT and "qkv_token_stride" in msg
+    st, msg = call("rg_qkv_rope_reshape_and_cache", p, 3072, p, p, p, p, p, p, 30, 8, 64, 16, 4, _lib.RG_DTYPE_BF16,
+                   0, None)
+    assert st == _lib.RG_ERR_INVALID_ARGUMENT and "not a multiple" in msg
+
+
 def test_workspace_queries():
     lib = railgun_amd.load_library()
     assert lib.rg_v2_workspace_bytes(8, 32, 64, 128) == 8 * 32 * 64 * 128 * 4 + 2 * 8 * 32 * 64 * 4
