@@ -38,6 +38,7 @@ struct PrefillArgs {
   int32_t num_seqs;
   int32_t num_tokens;
   int32_t rank_tiles;  // ceil(max_query_len / 32): tile ranks launched per sequence (MFMA path)
+  int32_t sched_kbound;  // > 0: bound on the work keys of the sorted schedule (MFMA path)
   int64_t kv_stride;
 };
 
@@ -176,6 +177,11 @@ __device__ __forceinline__ void tile_barrier() {
   asm volatile("" ::: "memory");
 }
 constexpr int kPStages = RG_PF_STAGES;  // K/V tiles in flight (ring in LDS)
+// Sorted schedule tables (LDS): work keys up to kSchedKeys, sequences up to kSchedSeqs.
+constexpr int kSchedKeys = 1024;
+// Orders this wave's earlier LDS writes before its later LDS reads.
+__device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+constexpr int kSchedSeqs = 256;
 constexpr float kSlack = 8.f;           // log2 headroom of the lazy softmax rescale
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -224,29 +230,137 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_mfma_kernel(
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hkv = a.num_kv_heads;
   // Persistent workgroups: workgroup g serves kv-head g % hkv (so, with workgroups placed on
-  // the XCDs round-robin, each head's K/V stays in few L2s) and, among the Q = gridDim / hkv
-  // workgroups of that head, takes the work items (rank r, sequence s) = u = r * num_seqs + s
-  // of round i in snake order (u = i * Q + q, or i * Q + Q - 1 - q on odd rounds).  Rank r
-  // is the r-th query tile of s counted from its last one, so the longest tiles come first;
-  // the last rank also takes every tile further from the end (when max_query_len
-  // understates a sequence).
+  // the XCDs round-robin, each head's K/V stays in few L2s); the Q = gridDim / hkv workgroups
+  // of a head share its work items, one query tile (sequence s, tile t) each, taken in snake
+  // order (round i: position i * Q + q, or i * Q + Q - 1 - q on odd rounds) over a list sorted
+  // by work, longest first.  The work key of (s, t) is base_s + t, base_s = ceil(prior_s / 32)
+  // + 1 (key tiles of its first query tile, within one tile), so every key value occurs at most
+  // once per sequence: the list is "for k = kmax .. 1, for s ascending with base_s <= k <
+  // base_s + nt_s", and position -> (k, s) needs only the count B[k] of items with key >= k
+  // (built in LDS once per workgroup) and a scan of the sequences covering k.  Snake order over
+  // a work-sorted list keeps the workgroups within a few percent of each other where rank
+  // order (all sequences' last tiles first, then the next-to-last ...) left 30 % apart.
+  // Batches beyond the LDS tables (sched_kbound == 0) keep rank order: item (rank r, seq s) =
+  // r * num_seqs + s is the r-th tile of s from its end, the last rank taking every tile
+  // further from the end (when max_query_len understates a sequence).
   const int kvh = blockIdx.x % hkv;
   const int nq_wg = gridDim.x / hkv;
   const int qw = blockIdx.x / hkv;
-  const int n_items = a.rank_tiles * a.num_seqs;
+  const bool sorted = a.sched_kbound > 0;
+  __shared__ int sched_b[kSchedKeys + 2];
+  __shared__ int2 sched_seq[kSchedSeqs];
+  int n_items = a.rank_tiles * a.num_seqs;
+  if (sorted) {
+    const int kb = a.sched_kbound;  // keys live in [1, kb]
+    for (int k = tid; k < kb + 2; k += kPThreads) sched_b[k] = 0;
+    __syncthreads();
+    for (int q = tid; q < a.num_seqs; q += kPThreads) {
+      const int Lq = cu_seqlens[q + 1] - cu_seqlens[q];
+      const int ntq = Lq > 0 ? (Lq + kPT - 1) / kPT : 0;
+      const int pr = max(0, min(context_lens[q], a.max_blocks * a.block_size) - Lq);
+      const int bq = min((pr + kPT - 1) / kPT + 1, kb + 1);
+      const int nq_keys = min(ntq, kb + 1 - bq);  // keys past the bound do not occur (see host)
+      sched_seq[q] = make_int2(bq, nq_keys);
+      if (nq_keys > 0) {  // difference array of the per-key counts
+        atomicAdd(&sched_b[bq], 1);
+        atomicAdd(&sched_b[bq + nq_keys], -1);
+      }
+    }
+    __syncthreads();
+    if (w == 0) {
+      // counts: prefix sum over k = 1 .. kb; then B[k] = sum of counts over keys >= k.
+      int carry = 0;
+      for (int c0 = 1; c0 <= kb; c0 += 64) {
+        const int k = c0 + lane;
+        int v = k <= kb ? sched_b[k] : 0;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int t2 = __shfl_up(v, o, 64);
+          if (lane >= o) v += t2;
+        }
+        v += carry;
+        if (k <= kb) sched_b[k] = v;
+        carry = __shfl(v, 63, 64);
+      }
+      wave_lds_fence();
+      carry = 0;
+      for (int c1 = kb; c1 >= 1; c1 -= 64) {
+        const int k = c1 - lane;
+        int v = k >= 1 ? sched_b[k] : 0;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int t2 = __shfl_up(v, o, 64);
+          if (lane >= o) v += t2;
+        }
+        v += carry;
+        carry = __shfl(v, 63, 64);
+        if (k >= 1) sched_b[k] = v;
+      }
+      if (lane == 0) sched_b[kb + 1] = 0;
+    }
+    __syncthreads();
+    n_items = __builtin_amdgcn_readfirstlane(sched_b[1]);
+  }
+  // Element offset, inside a block, of the 16 bytes this lane copies for each of its tile
+  // loads (fast path of issue_tile): K rows key j (lane & 31), d chunk 16 ins + 8 (lane >> 5);
+  // V rows key kl of the instruction, physical chunk swizzled by the row.
+  int64_t lane_off[LOADS_PER_WAVE];
+#pragma unroll
+  for (int ld = 0; ld < LOADS_PER_WAVE; ++ld) {
+    const int ins = w + ld * kPWaves;
+    const int jj = lane & 31, half = lane >> 5;
+    if (ld * kPWaves < KI) {
+      lane_off[ld] = (int64_t)(jj & (kBlk - 1)) * D + 16 * ins + 8 * half;
+    } else {
+      const int vi = ins - KI;
+      const int kl = vi * (1024 / (D * 2)) + lane / TL::VCHUNKS;
+      lane_off[ld] = (int64_t)(kl & (kBlk - 1)) * D + 8 * TL::vchunk(kl, lane % TL::VCHUNKS);
+    }
+  }
   for (int round = 0; round * nq_wg < n_items; ++round) {
   const int u = round * nq_wg + ((round & 1) ? nq_wg - 1 - qw : qw);
   if (u >= n_items) continue;
-  const int s = u % a.num_seqs;
-  const int rank = u / a.num_seqs;
+  int s, t_first, t_stop;
+  if (sorted) {
+    // key k: the largest with B[k] > u (B is non-increasing); i: rank of the item among key k's.
+    int lo = 1, hi = a.sched_kbound;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (sched_b[mid] > u) lo = mid;
+      else hi = mid - 1;
+    }
+    const int k = __builtin_amdgcn_readfirstlane(lo);
+    int i = __builtin_amdgcn_readfirstlane(u - sched_b[k + 1]);
+    s = -1;
+    for (int c0 = 0; c0 < a.num_seqs && s < 0; c0 += 64) {
+      const int q = c0 + lane;
+      const int2 bn = q < a.num_seqs ? sched_seq[q] : make_int2(0, 0);
+      uint64_t m = __ballot(bn.x <= k && k < bn.x + bn.y);
+      const int cnt = __builtin_popcountll(m);
+      if (i < cnt) {
+        for (; i > 0; --i) m &= m - 1;
+        s = c0 + __ffsll((unsigned long long)m) - 1;
+      } else {
+        i -= cnt;
+      }
+    }
+    s = __builtin_amdgcn_readfirstlane(s);
+    t_first = k - sched_seq[s].x;
+    t_stop = t_first - 1;
+  } else {
+    s = u % a.num_seqs;
+    const int rank = u / a.num_seqs;
+    const int Ls = cu_seqlens[s + 1] - cu_seqlens[s];
+    const int nts = (Ls + kPT - 1) / kPT;
+    if (rank >= nts) continue;
+    t_first = nts - 1 - rank;
+    t_stop = rank == a.rank_tiles - 1 ? -1 : t_first - 1;
+  }
   const int row0 = cu_seqlens[s];
   const int L = cu_seqlens[s + 1] - row0;
-  const int ntile = (L + kPT - 1) / kPT;
-  if (rank >= ntile) continue;
-  const int t_stop = rank == a.rank_tiles - 1 ? -1 : ntile - 2 - rank;
   const int ctx = min(context_lens[s], a.max_blocks * a.block_size);
   const int prior = ctx - L;
-  for (int t = ntile - 1 - rank; t > t_stop; --t) {
+  for (int t = t_first; t > t_stop; --t) {
   const int q0 = t * kPT;                      // first query of the tile (within the sequence)
   const int nq = min(kPT, L - q0);
   const int pos_min = prior + q0;
@@ -288,18 +402,35 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_mfma_kernel(
 
   // Issues this wave's share of the global->LDS copies of key tile kt (wb <= kt < wb + 64)
   // into ring stage st.  Keys past the last position read the last valid key instead (they
-  // are masked).
+  // are masked).  A lane's element offset inside a block is the same for every tile of the
+  // workgroup (its kv-head is fixed): only the two block bases change per tile, and only the
+  // last tile of an item needs the clamp to pos_max (the slow path).
   auto issue_tile = [&](int kt, int st) {
     const int r = 2 * (kt - wb);  // even: both blocks sit in the same window register
     const int e0 = __builtin_amdgcn_readlane(r < 64 ? btw0 : btw1, r & 63);
     const int e1 = __builtin_amdgcn_readlane(r < 64 ? btw0 : btw1, (r & 63) + 1);
     const int64_t blk0 = (int64_t)e0 * a.kv_stride + head_off;
     const int64_t blk1 = (int64_t)e1 * a.kv_stride + head_off;
+    const uint32_t sbase = lds_base + st * TL::BYTES;
+    if (kt * kPT + kPT - 1 <= pos_max) {
+      const int64_t kb = j < kBlk ? blk0 : blk1;  // K rows: lane j reads key j of the tile
+#pragma unroll
+      for (int ld = 0; ld < LOADS_PER_WAVE; ++ld) {
+        const int ins = w + ld * kPWaves;
+        if (ld * kPWaves < KI) {  // K instructions (KI is a multiple of the wave count)
+          lds_dma16(kc + kb + lane_off[ld], __builtin_amdgcn_readfirstlane(sbase + ins * 1024));
+        } else {  // V instructions: each covers keys of one block
+          const int vi = ins - KI;
+          const int64_t vb = vi < VI / 2 ? blk0 : blk1;
+          lds_dma16(vc + vb + lane_off[ld], __builtin_amdgcn_readfirstlane(sbase + TL::KBYTES + vi * 1024));
+        }
+      }
+      return;
+    }
     auto row = [&](int kl) -> int64_t {  // kl: key within the tile
       const int key = min(kt * kPT + kl, pos_max) - kt * kPT;
       return (key < kBlk ? blk0 : blk1) + (int64_t)(key & (kBlk - 1)) * D;
     };
-    const uint32_t sbase = lds_base + st * TL::BYTES;
 #pragma unroll
     for (int ld = 0; ld < LOADS_PER_WAVE; ++ld) {
       const int ins = w + ld * kPWaves;
@@ -350,11 +481,13 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_mfma_kernel(
   // Masks keys past each query's position (tiles from kt_mask on, branch-free) and returns
   // the tile's maximum in the exp2 domain (both halves of the query's keys).
   auto mask_max = [&](f32x16_t& c, int kt) {
-    const int lim = kt >= kt_mask ? my_pos - kt * kPT : 1 << 30;
+    if (kt >= kt_mask) {  // wave-uniform: only the tiles around the diagonal hold such keys
+      const int lim = my_pos - kt * kPT;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int key = 8 * (v >> 2) + 4 * hh + (v & 3);
-      c[v] = key > lim ? -INFINITY : c[v];
+      for (int v = 0; v < 16; ++v) {
+        const int key = 8 * (v >> 2) + 4 * hh + (v & 3);
+        c[v] = key > lim ? -INFINITY : c[v];
+      }
     }
     float tmax = c[0];
 #pragma unroll
@@ -530,7 +663,7 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
   }
   PrefillArgs a{query, key_cache, value_cache, block_table, context_lens, cu_seqlens, output,
                 scale * kLog2e, num_heads, num_kv_heads, head_dim, block_size,
-                max_blocks_per_seq, num_seqs, num_tokens, 0, stride};
+                max_blocks_per_seq, num_seqs, num_tokens, 0, 0, stride};
   hipStream_t s = as_stream(stream);
   const int eb = dtype_bytes(dtype);
   if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && scale > 0.f && num_heads == 4 * num_kv_heads &&
@@ -542,6 +675,10 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
     // tiles beyond it; no query run is longer than num_tokens).
     const int64_t qmax = std::min<int64_t>(std::max<int32_t>(max_query_len, 1), num_tokens);
     a.rank_tiles = (int32_t)((qmax + kPT - 1) / kPT);
+    // Work keys are at most ceil(prior / 32) + ceil(L / 32) <= (max(table, L) + 62) / 32 with
+    // prior + L <= the table's tokens and L <= num_tokens.
+    const int64_t kbound = (std::max<int64_t>((int64_t)max_blocks_per_seq * block_size, num_tokens) + 62) / kPT + 1;
+    a.sched_kbound = (kbound <= kSchedKeys && num_seqs <= kSchedSeqs) ? (int32_t)kbound : 0;
     // Two resident workgroups per CU, split evenly over the kv-heads, at most one per item.
     const int64_t items = (int64_t)a.rank_tiles * num_seqs;
     const int64_t per_head = std::min<int64_t>(items, std::max<int64_t>(1, 2 * device_cu_count() / num_kv_heads));

@@ -80,3 +80,28 @@ def test_prefill_long_prior_context(device, kernels, max_query_len):
     bt = wl.assign_blocks(prior + lens, 16, 1000, 260, rng)
     w = wl.PrefillWorkload("long_prior", "bf16", 32, 8, 128, 16, 1000, lens, bt, 4, prior=prior)
     _run(device, kernels, w, seed=77, max_query_len=max_query_len)
+
+
+@pytest.mark.parametrize("nseq", [200, 300])
+def test_prefill_many_sequences(device, kernels, nseq):
+    """Many short sequences, bf16 D 64 GQA 4 (MFMA path): 200 use the work-sorted schedule
+    (its sequence scan crosses several 64-lane chunks), 300 exceed its LDS table and run in
+    rank order; both must match the oracle."""
+    rng = np.random.default_rng(nseq)
+    lens = rng.integers(1, 70, nseq).astype(np.int32)
+    prior = np.where(rng.random(nseq) < 0.3, rng.integers(1, 90, nseq), 0).astype(np.int32)
+    need = int(((prior + lens + 15) // 16).sum())
+    bt = wl.assign_blocks(prior + lens, 16, need + 8, 12, rng)
+    w = wl.PrefillWorkload(f"many{nseq}", "bf16", 8, 2, 64, 16, need + 8, lens, bt, 5, prior=prior)
+    _run(device, kernels, w, seed=nseq + 1, check_seqs=list(range(0, nseq, 7)))
+
+
+def test_prefill_wide_table_rank_order(device, kernels):
+    """A block table padded to 2200 entries (35,200 positions) puts the work-key bound past the
+    sorted schedule's LDS table: the rank-order path, with prior context, bf16 D 128."""
+    rng = np.random.default_rng(9)
+    lens = np.array([33, 170, 5, 96], np.int32)
+    prior = np.array([300, 2100, 0, 40], np.int32)
+    bt = wl.assign_blocks(prior + lens, 16, 400, 2200, rng)
+    w = wl.PrefillWorkload("wide_table", "bf16", 32, 8, 128, 16, 400, lens, bt, 4, prior=prior)
+    _run(device, kernels, w, seed=99)
