@@ -158,7 +158,18 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 #define RG_LDS __attribute__((address_space(3)))
 
 #ifndef RG_PF_STAGES
-#define RG_PF_STAGES 4
+#define RG_PF_STAGES 3
+#endif
+// 1: software-pipelined tile loop (scores of tile kt+1 under the softmax of tile kt);
+// 0: in-order tile loop.  In-order needs 16 fewer VGPRs, which lets three workgroups (three
+// waves per SIMD) share a CU; the extra resident waves hide more latency than the pipeline
+// did with two (measured at config 4: 209 us against 221 us).
+#ifndef RG_PF_PIPELINE
+#define RG_PF_PIPELINE 0
+#endif
+// Resident workgroups per CU the persistent grid is sized for (LDS: stages x tile bytes each).
+#ifndef RG_PF_WG_PER_CU
+#define RG_PF_WG_PER_CU 3
 #endif
 
 // 16 bytes per lane from global memory straight into LDS at lds_addr + 16 * lane (the
@@ -178,7 +189,10 @@ __device__ __forceinline__ void tile_barrier() {
 }
 constexpr int kPStages = RG_PF_STAGES;  // K/V tiles in flight (ring in LDS)
 // Sorted schedule tables (LDS): work keys up to kSchedKeys, sequences up to kSchedSeqs.
-constexpr int kSchedKeys = 1024;
+#ifndef RG_PF_SCHED_KEYS
+#define RG_PF_SCHED_KEYS 512
+#endif
+constexpr int kSchedKeys = RG_PF_SCHED_KEYS;
 // Orders this wave's earlier LDS writes before its later LDS reads.
 __device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 constexpr int kSchedSeqs = 256;
@@ -209,7 +223,7 @@ struct PTile {
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(kPThreads, 2) void prefill_mfma_kernel(
+__global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kernel(
     PrefillArgs a, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, const int32_t* __restrict__ cu_seqlens) {
@@ -304,17 +318,17 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_mfma_kernel(
   // Element offset, inside a block, of the 16 bytes this lane copies for each of its tile
   // loads (fast path of issue_tile): K rows key j (lane & 31), d chunk 16 ins + 8 (lane >> 5);
   // V rows key kl of the instruction, physical chunk swizzled by the row.
-  int64_t lane_off[LOADS_PER_WAVE];
+  int32_t lane_off[LOADS_PER_WAVE];
 #pragma unroll
   for (int ld = 0; ld < LOADS_PER_WAVE; ++ld) {
     const int ins = w + ld * kPWaves;
     const int jj = lane & 31, half = lane >> 5;
     if (ld * kPWaves < KI) {
-      lane_off[ld] = (int64_t)(jj & (kBlk - 1)) * D + 16 * ins + 8 * half;
+      lane_off[ld] = (jj & (kBlk - 1)) * D + 16 * ins + 8 * half;
     } else {
       const int vi = ins - KI;
       const int kl = vi * (1024 / (D * 2)) + lane / TL::VCHUNKS;
-      lane_off[ld] = (int64_t)(kl & (kBlk - 1)) * D + 8 * TL::vchunk(kl, lane % TL::VCHUNKS);
+      lane_off[ld] = (kl & (kBlk - 1)) * D + 8 * TL::vchunk(kl, lane % TL::VCHUNKS);
     }
   }
   for (int round = 0; round * nq_wg < n_items; ++round) {
@@ -549,12 +563,14 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_mfma_kernel(
   // This wave's copies of tile `need` have landed (all but the newest `pending` groups),
   // then the barrier shows every wave's copies and retires the stages read before it.
   auto wait_tiles = [&](auto pending) {
-    static_assert(LOADS_PER_WAVE * decltype(pending)::value < 16, "vmcnt immediate");
+    constexpr int n = LOADS_PER_WAVE * decltype(pending)::value;
+    static_assert(n < 64, "vmcnt immediate (6 bits: [3:0] and [15:14])");
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((LOADS_PER_WAVE * decltype(pending)::value) | 0x70 | 0xF00);
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00);
     tile_barrier();
   };
 
+#if RG_PF_PIPELINE
   // Prologue: tiles 0 .. kPStages-1 in flight (past the end: repeats of the last tile); with
   // tiles 0 and 1 in LDS, the scores and maximum of tile 0.
 #pragma unroll
@@ -586,6 +602,33 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_mfma_kernel(
   load_window();
   __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
   }
+
+#else
+  // In-order tile loop: tiles kt .. kt + kPStages - 2 are in flight when iteration kt starts;
+  // once tile kt has landed everywhere (wait + barrier, which also shows every wave is done
+  // with tile kt - 1), stage (kt - 1) % kPStages takes tile kt + kPStages - 1, then tile kt is
+  // computed: scores, maximum, probabilities, PV.
+#pragma unroll
+  for (int p = 0; p < kPStages - 1; ++p) issue_tile(min(p, nkt - 1), p);
+  int kt = 0;
+  for (;;) {
+  // Iterations whose refill tile kt + kPStages - 1 lies in the current block-table window.
+  const int kend = min(nkt, wb + 65 - kPStages);
+  for (; kt < kend; ++kt) {
+    wait_tiles(std::integral_constant<int, kPStages - 2>{});
+    issue_tile(min(kt + kPStages - 1, nkt - 1), (kt + kPStages - 1) % kPStages);
+    f32x16_t c = scores(kt % kPStages);
+    update_max(mask_max(c, kt));
+    uint32_t pk[8];
+    probs(c, pk);
+    accumulate(kt % kPStages, pk);
+  }
+  if (kt >= nkt) break;
+  wb += 64;
+  load_window();
+  __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
+  }
+#endif
 
   // Every copy issued (the ring's tail repeats the last tile) lands before the LDS is reused
   // or released.
@@ -679,9 +722,10 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
     // prior + L <= the table's tokens and L <= num_tokens.
     const int64_t kbound = (std::max<int64_t>((int64_t)max_blocks_per_seq * block_size, num_tokens) + 62) / kPT + 1;
     a.sched_kbound = (kbound <= kSchedKeys && num_seqs <= kSchedSeqs) ? (int32_t)kbound : 0;
-    // Two resident workgroups per CU, split evenly over the kv-heads, at most one per item.
+    // RG_PF_WG_PER_CU resident workgroups per CU, split evenly over the kv-heads, at most one
+    // per item.
     const int64_t items = (int64_t)a.rank_tiles * num_seqs;
-    const int64_t per_head = std::min<int64_t>(items, std::max<int64_t>(1, 2 * device_cu_count() / num_kv_heads));
+    const int64_t per_head = std::min<int64_t>(items, std::max<int64_t>(1, RG_PF_WG_PER_CU * device_cu_count() / num_kv_heads));
     const dim3 grid((unsigned)(per_head * num_kv_heads));
     auto go = [&](auto tag, auto dtag) {
       using T = decltype(tag);
