@@ -478,6 +478,7 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   const int e_row = (lane >> 2) & 3;
   const int qq = lane & 3;
   const int kt_mask = pos_min / kPT;  // tiles from here on may hold keys past a query
+  const int xor32_addr = (lane ^ 32) << 2;  // ds_bpermute address of the other half's lane
 
   // S^T = K Q^T of the tile in stage st: c[4jb + r] is key 8jb + 4hh + r for query j.
   auto scores = [&](int st) {
@@ -506,7 +507,8 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     float tmax = c[0];
 #pragma unroll
     for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, c[v]);
-    return fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * a.scale_log2;
+    const float other = __int_as_float(__builtin_amdgcn_ds_bpermute(xor32_addr, __float_as_int(tmax)));
+    return fmaxf(tmax, other) * a.scale_log2;
   };
   // Online softmax with a lazy maximum: m_run only moves when a tile's maximum exceeds it by
   // more than kSlack, so p = 2^(x - m_run) stays below 2^kSlack and the O^T rescale is rare.
@@ -570,7 +572,7 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     tile_barrier();
   };
 
-#if RG_PF_PIPELINE
+#if RG_PF_PIPELINE == 1
   // Prologue: tiles 0 .. kPStages-1 in flight (past the end: repeats of the last tile); with
   // tiles 0 and 1 in LDS, the scores and maximum of tile 0.
 #pragma unroll
