@@ -113,6 +113,41 @@ def test_mfma_path_shapes(device, kernels, dt, D, G):
     assert_close(gpu_v2(kernels, inp, 32), want, dt, "v2 P=32")
 
 
+def test_workspace_reused_across_calls(device, kernels):
+    """One workspace serves calls of different shapes (GQA 4 and 8, head_dim 128 and 64, empty
+    and long sequences) and a v2 call that falls back to partition + reduce on its front part:
+    every call matches the oracle whatever the previous calls left in it."""
+    shapes = [dict(ctx=CTX_RAGGED, G=4, D=128), dict(ctx=[2000, 37, 4096, 0, 900] * 6, G=4, D=128),
+              dict(ctx=CTX_RAGGED[::-1], G=8, D=64)]
+    inps = [make_inputs(device, sh["ctx"], "bf16", H=2 * sh["G"], Hkv=2, D=sh["D"], seed=40 + i)
+            for i, sh in enumerate(shapes)]
+    wants = [oracle_v1_plus(inp) for inp in inps]
+    nbytes = max(kernels.v1_workspace_bytes(len(inp["ctx"]), inp["H"], inp["Hkv"], inp["D"], inp["bs"], inp["mb"])
+                 for inp in inps)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    for i in (0, 1, 0, "v2", 2, 1, 2):
+        if i == "v2":
+            # v2 on the front of the same workspace, too small for the stream-K path: the
+            # partition + reduce fallback
+            inp, P = inps[0], 32
+            np_ = math.ceil(int(inp["ctx"].max()) / P)
+            need = kernels.v2_workspace_bytes(len(inp["ctx"]), inp["H"], np_, inp["D"])
+            assert need < nbytes
+            out = torch.full_like(inp["dq"], float("nan"))
+            kernels.launch_v2(inp["dq"], inp["dkc"], inp["dvc"], inp["dbt"], inp["dctx"], out, inp["scale"],
+                              inp["H"], inp["Hkv"], inp["D"], inp["bs"], inp["mb"], len(inp["ctx"]),
+                              int(inp["ctx"].max()), P, ws[:need])
+            torch.cuda.synchronize()
+            assert_close(dev_f32(out), wants[0], "bf16", "v2 fallback")
+            continue
+        inp = inps[i]
+        out = torch.full_like(inp["dq"], float("nan"))
+        kernels.launch_v1(inp["dq"], inp["dkc"], inp["dvc"], inp["dbt"], inp["dctx"], out, inp["scale"], inp["H"],
+                          inp["Hkv"], inp["D"], inp["bs"], inp["mb"], len(inp["ctx"]), workspace=ws)
+        torch.cuda.synchronize()
+        assert_close(dev_f32(out), wants[i], "bf16", f"shape {i}")
+
+
 @pytest.mark.parametrize("dt,D,bs,G", [("f32", 128, 16, 4), ("bf16", 96, 16, 4), ("bf16", 256, 16, 2),
                                        ("f16", 32, 8, 3), ("bf16", 128, 32, 4), ("f32", 256, 8, 1)])
 def test_generic_path_shapes(device, kernels, dt, D, bs, G):
