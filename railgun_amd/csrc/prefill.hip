@@ -40,6 +40,7 @@ struct PrefillArgs {
   int32_t rank_tiles;  // ceil(max_query_len / 32): tile ranks launched per sequence (MFMA path)
   int32_t sched_kbound;  // > 0: bound on the work keys of the sorted schedule (MFMA path)
   int64_t kv_stride;
+  uint32_t kv_stride_bytes;  // MFMA path: block stride in bytes (below 2^32)
 };
 
 // Sequence owning packed row `row`: the last s with cu_seqlens[s] <= row.
@@ -179,6 +180,11 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
 }
+// The same copy from a wave-uniform base plus a 32-bit per-lane byte offset.
+__device__ __forceinline__ void lds_dma16_s(const char* base, uint32_t lane_bytes, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(lane_bytes), "s"(base), "s"(lds_addr)
+               : "memory", "m0");
+}
 // Workgroup barrier without the memory fence of __syncthreads (which would also wait for
 // every prefetch in flight); the asm statements keep the compiler from moving memory
 // accesses across it.
@@ -188,6 +194,15 @@ __device__ __forceinline__ void tile_barrier() {
   asm volatile("" ::: "memory");
 }
 constexpr int kPStages = RG_PF_STAGES;  // K/V tiles in flight (ring in LDS)
+// LDS operand reads in flight ahead of the MFMA that uses them: K (QK^T) and V (PV).
+#ifndef RG_PF_KAHEAD
+#define RG_PF_KAHEAD 4
+#endif
+#ifndef RG_PF_VAHEAD
+#define RG_PF_VAHEAD 3
+#endif
+constexpr int kKAhead = RG_PF_KAHEAD;
+constexpr int kVAhead = RG_PF_VAHEAD;
 // Sorted schedule tables (LDS): work keys up to kSchedKeys, sequences up to kSchedSeqs.
 #ifndef RG_PF_SCHED_KEYS
 #define RG_PF_SCHED_KEYS 512
@@ -209,8 +224,11 @@ template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi)
   return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)lo, (_Float16)hi});
 }
 
-// LDS image of one key tile: K as the MFMA A-operand image (chunk i of lane l at
-// i*1024 + l*16), V row-major [key][D] with the 16-byte chunks of row `key` XOR-swizzled by
+// LDS image of one key tile (two KV blocks of 16 keys).  K: the 16-byte chunk c of key k of
+// block b at b * KBYTES / 2 + c * 256 + k * 16, so that one copy instruction (1 KB: chunks
+// 4n .. 4n+3 of the block's 16 keys) reads from one block only, and the MFMA A-operand read
+// of d chunk i (chunk 2i + half of key j) is one 256-byte run per 16 lanes at a constant
+// offset 512 i.  V: row-major [key][D] with the 16-byte chunks of row `key` XOR-swizzled by
 // 2*(key & 3) so that the transposing reads of four consecutive rows hit distinct banks.
 template <int D>
 struct PTile {
@@ -219,6 +237,7 @@ struct PTile {
   static constexpr int VBYTES = kPT * D * 2;
   static constexpr int BYTES = KBYTES + VBYTES;
   static constexpr int VCHUNKS = D / 8;  // 16-byte chunks per V row
+  static constexpr int BLK_INS = D / 32;  // 1 KB copy instructions per block, for K and for V
   __device__ static __forceinline__ int vchunk(int key, int c) { return c ^ (2 * (key & 3)); }
 };
 
@@ -233,10 +252,11 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   constexpr int G = kPWaves;
   constexpr int NKC = TL::NKC;     // 16-element d chunks = QK MFMAs per key tile
   constexpr int NDB = D / 32;      // 32-row d blocks of O^T
-  constexpr int KI = NKC;          // global->LDS instructions for K (1 KB each)
-  constexpr int VI = TL::VBYTES / 1024;  // ... and for V
-  static_assert(KI % kPWaves == 0 && VI % kPWaves == 0, "tile loads split evenly over the waves");
-  constexpr int LOADS_PER_WAVE = (KI + VI) / kPWaves;
+  // Tile copies: waves 2b and 2b+1 copy block b of the tile, each half of its K and half of
+  // its V instructions (BLK_INS / 2 of each).
+  constexpr int HALF_INS = TL::BLK_INS / 2;
+  static_assert(HALF_INS >= 1 && TL::BLK_INS % 2 == 0, "block copies split over two waves");
+  constexpr int LOADS_PER_WAVE = 2 * HALF_INS;
   __shared__ __attribute__((aligned(16))) char lds[kPStages * TL::BYTES];
 
   const int tid = threadIdx.x;
@@ -315,20 +335,31 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     __syncthreads();
     n_items = __builtin_amdgcn_readfirstlane(sched_b[1]);
   }
-  // Element offset, inside a block, of the 16 bytes this lane copies for each of its tile
-  // loads (fast path of issue_tile): K rows key j (lane & 31), d chunk 16 ins + 8 (lane >> 5);
-  // V rows key kl of the instruction, physical chunk swizzled by the row.
+  // This wave's tile copies: block cb of the tile, K instructions n = cp * HALF_INS + t and V
+  // instructions cb * BLK_INS + cp * HALF_INS + t (t < HALF_INS).  For each: the key within
+  // the tile (copy_key) and the element offset inside its block of the 16 bytes this lane
+  // copies (K: key lane & 15, chunk 4n + lane / 16; V: key kl of the instruction, physical
+  // chunk swizzled by the row), and the LDS offset of the instruction inside a ring stage.
+  const int cb = w >> 1, cp = w & 1;
+  auto copy_key = [&](int ld) {
+    if (ld < HALF_INS) return kBlk * cb + (lane & (kBlk - 1));
+    const int vi = cb * TL::BLK_INS + cp * HALF_INS + ld % HALF_INS;
+    return vi * (1024 / (D * 2)) + lane / TL::VCHUNKS;
+  };
   int32_t lane_off[LOADS_PER_WAVE];
+  uint32_t ins_lds[LOADS_PER_WAVE];
 #pragma unroll
   for (int ld = 0; ld < LOADS_PER_WAVE; ++ld) {
-    const int ins = w + ld * kPWaves;
-    const int jj = lane & 31, half = lane >> 5;
-    if (ld * kPWaves < KI) {
-      lane_off[ld] = (jj & (kBlk - 1)) * D + 16 * ins + 8 * half;
+    const int t = ld % HALF_INS;
+    const int kl = copy_key(ld);
+    if (ld < HALF_INS) {
+      const int n = cp * HALF_INS + t;
+      lane_off[ld] = (kl & (kBlk - 1)) * D + 8 * (4 * n + (lane >> 4));
+      ins_lds[ld] = cb * (TL::KBYTES / 2) + n * 1024;
     } else {
-      const int vi = ins - KI;
-      const int kl = vi * (1024 / (D * 2)) + lane / TL::VCHUNKS;
+      const int vi = cb * TL::BLK_INS + cp * HALF_INS + t;
       lane_off[ld] = (kl & (kBlk - 1)) * D + 8 * TL::vchunk(kl, lane % TL::VCHUNKS);
+      ins_lds[ld] = TL::KBYTES + vi * 1024;
     }
   }
   for (int round = 0; round * nq_wg < n_items; ++round) {
@@ -411,52 +442,42 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   // iteration.
   __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
   const int64_t head_off = (int64_t)kvh * kBlk * D;
+  const uint32_t head_off_bytes = (uint32_t)head_off * 2u;
   const int nkt = pos_max / kPT + 1;
   const uint32_t lds_base = (uint32_t)(uintptr_t)((RG_LDS char*)lds);
 
   // Issues this wave's share of the global->LDS copies of key tile kt (wb <= kt < wb + 64)
   // into ring stage st.  Keys past the last position read the last valid key instead (they
-  // are masked).  A lane's element offset inside a block is the same for every tile of the
-  // workgroup (its kv-head is fixed): only the two block bases change per tile, and only the
-  // last tile of an item needs the clamp to pos_max (the slow path).
+  // are masked).  Every instruction reads from one block (this wave's block cb of the tile),
+  // so the fast path is a scalar block base (block number x block stride, 32 x 32 -> 64-bit)
+  // plus the lane's fixed 32-bit offset; only the last tile of an item needs the clamp to
+  // pos_max, with per-lane addresses (the slow path).
   auto issue_tile = [&](int kt, int st) {
     const int r = 2 * (kt - wb);  // even: both blocks sit in the same window register
+    const uint32_t sbase = lds_base + st * TL::BYTES;
+    if (kt * kPT + kPT - 1 <= pos_max) {
+      const uint32_t e = (uint32_t)__builtin_amdgcn_readlane(r < 64 ? btw0 : btw1, (r & 63) + cb);
+      const uint64_t boff = (uint64_t)e * a.kv_stride_bytes + head_off_bytes;
+      const char* kbase = reinterpret_cast<const char*>(kc) + boff;
+      const char* vbase = reinterpret_cast<const char*>(vc) + boff;
+#pragma unroll
+      for (int ld = 0; ld < LOADS_PER_WAVE; ++ld) {
+        lds_dma16_s(ld < HALF_INS ? kbase : vbase, (uint32_t)lane_off[ld] * 2u, sbase + ins_lds[ld]);
+      }
+      return;
+    }
     const int e0 = __builtin_amdgcn_readlane(r < 64 ? btw0 : btw1, r & 63);
     const int e1 = __builtin_amdgcn_readlane(r < 64 ? btw0 : btw1, (r & 63) + 1);
     const int64_t blk0 = (int64_t)e0 * a.kv_stride + head_off;
     const int64_t blk1 = (int64_t)e1 * a.kv_stride + head_off;
-    const uint32_t sbase = lds_base + st * TL::BYTES;
-    if (kt * kPT + kPT - 1 <= pos_max) {
-      const int64_t kb = j < kBlk ? blk0 : blk1;  // K rows: lane j reads key j of the tile
-#pragma unroll
-      for (int ld = 0; ld < LOADS_PER_WAVE; ++ld) {
-        const int ins = w + ld * kPWaves;
-        if (ld * kPWaves < KI) {  // K instructions (KI is a multiple of the wave count)
-          lds_dma16(kc + kb + lane_off[ld], __builtin_amdgcn_readfirstlane(sbase + ins * 1024));
-        } else {  // V instructions: each covers keys of one block
-          const int vi = ins - KI;
-          const int64_t vb = vi < VI / 2 ? blk0 : blk1;
-          lds_dma16(vc + vb + lane_off[ld], __builtin_amdgcn_readfirstlane(sbase + TL::KBYTES + vi * 1024));
-        }
-      }
-      return;
-    }
-    auto row = [&](int kl) -> int64_t {  // kl: key within the tile
-      const int key = min(kt * kPT + kl, pos_max) - kt * kPT;
-      return (key < kBlk ? blk0 : blk1) + (int64_t)(key & (kBlk - 1)) * D;
-    };
 #pragma unroll
     for (int ld = 0; ld < LOADS_PER_WAVE; ++ld) {
-      const int ins = w + ld * kPWaves;
-      if (ins < KI) {
-        lds_dma16(kc + row(j) + 16 * ins + 8 * hh, __builtin_amdgcn_readfirstlane(sbase + ins * 1024));
-      } else {
-        const int vi = ins - KI;
-        const int kl = vi * (1024 / (D * 2)) + lane / TL::VCHUNKS;  // key within the tile
-        const int pch = lane % TL::VCHUNKS;                          // physical chunk position
-        lds_dma16(vc + row(kl) + 8 * TL::vchunk(kl, pch),
-                  __builtin_amdgcn_readfirstlane(sbase + TL::KBYTES + vi * 1024));
-      }
+      // The copy of key lane_key (within the tile) with the clamped key's row instead.
+      const int kl = copy_key(ld);
+      const int key = min(kt * kPT + kl, pos_max) - kt * kPT;
+      const int64_t src = (key < kBlk ? blk0 : blk1) + (int64_t)((key & (kBlk - 1)) - (kl & (kBlk - 1))) * D +
+                          lane_off[ld];
+      lds_dma16((ld < HALF_INS ? kc : vc) + src, sbase + ins_lds[ld]);
     }
   };
 
@@ -480,29 +501,38 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   const int kt_mask = pos_min / kPT;  // tiles from here on may hold keys past a query
   const int xor32_addr = (lane ^ 32) << 2;  // ds_bpermute address of the other half's lane
 
-  // S^T = K Q^T of the tile in stage st: c[4jb + r] is key 8jb + 4hh + r for query j.
+  // S^T = K Q^T of the tile in stage st: c[4jb + r] is key 8jb + 4hh + r for query j.  The K
+  // operands are read kKAhead MFMAs ahead of their use (a rolling set of registers); the
+  // scheduling barriers keep that order, which the compiler would otherwise trade for fewer
+  // registers by waiting for each read right before its MFMA.
+  const int k_lane = (j >> 4) * (TL::KBYTES / 2) + hh * 256 + (j & (kBlk - 1)) * 16;
   auto scores = [&](int st) {
-    const char* base = lds + st * TL::BYTES;
-    uint4 ka[NKC];
+    const char* base = lds + st * TL::BYTES + k_lane;
+    constexpr int A = kKAhead < NKC ? kKAhead : NKC;
+    uint4 ka[A];
 #pragma unroll
-    for (int i = 0; i < NKC; ++i) ka[i] = *reinterpret_cast<const uint4*>(base + i * 1024 + lane * 16);
+    for (int i = 0; i < A; ++i) ka[i] = *reinterpret_cast<const uint4*>(base + i * 512);
     f32x16_t c;
 #pragma unroll
     for (int v = 0; v < 16; ++v) c[v] = 0.f;
 #pragma unroll
-    for (int i = 0; i < NKC; ++i) c = MF::run(ka[i], qb[i], c);
+    for (int i = 0; i < NKC; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      c = MF::run(ka[i % A], qb[i], c);
+      if (i + A < NKC) ka[i % A] = *reinterpret_cast<const uint4*>(base + (i + A) * 512);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     return c;
   };
   // Masks keys past each query's position (tiles from kt_mask on, branch-free) and returns
   // the tile's maximum in the exp2 domain (both halves of the query's keys).
   auto mask_max = [&](f32x16_t& c, int kt) {
     if (kt >= kt_mask) {  // wave-uniform: only the tiles around the diagonal hold such keys
-      const int lim = my_pos - kt * kPT;
+      // key 8 (v >> 2) + 4 hh + (v & 3) > my_pos - 32 kt, with the lane's part on the right
+      // so that the left side is an inline constant.
+      const int lim = my_pos - kt * kPT - 4 * hh;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = 8 * (v >> 2) + 4 * hh + (v & 3);
-        c[v] = key > lim ? -INFINITY : c[v];
-      }
+      for (int v = 0; v < 16; ++v) c[v] = 8 * (v >> 2) + (v & 3) > lim ? -INFINITY : c[v];
     }
     float tmax = c[0];
 #pragma unroll
@@ -541,26 +571,40 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   // O^T += V^T P^T for the tile in stage st, in two 16-key MFMA steps.  The A operand comes
   // from the transposing LDS read: in each 16-lane group, lane 4e+q points at
   // V[key0 + e][d0 + 4q .. +4] and lane i receives V[key0 .. key0+3][d0 + i].
-  auto accumulate = [&](int st, const uint32_t (&pk)[8]) {
+  // A operand m = n * NDB + db of the PV product (keys 16n .. 16n+15, d block db).
+  auto v_operand = [&](int st, int m) {
     const char* vbase = vlds + st * TL::BYTES;
+    const int n = m / NDB, db = m % NDB;
+    const int d = 32 * db + 16 * (grp & 1) + 4 * qq;  // this lane's address column
+    v4i16_t part[2];
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const uint4 pb = make_uint4(pk[4 * n], pk[4 * n + 1], pk[4 * n + 2], pk[4 * n + 3]);
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const int d = 32 * db + 16 * (grp & 1) + 4 * qq;  // this lane's address column
-        v4i16_t part[2];
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int key = 16 * n + 8 * half + 4 * (grp >> 1) + e_row;
-          const int off = key * (D * 2) + TL::vchunk(key, d >> 3) * 16 + (d & 7) * 2;
-          part[half] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((RG_LDS v4i16_t*)(vbase + off));
-        }
-        const uint2 lo = __builtin_bit_cast(uint2, part[0]);
-        const uint2 hi = __builtin_bit_cast(uint2, part[1]);
-        o[db] = MF::run(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[db]);
-      }
+    for (int half = 0; half < 2; ++half) {
+      const int key = 16 * n + 8 * half + 4 * (grp >> 1) + e_row;
+      const int off = key * (D * 2) + TL::vchunk(key, d >> 3) * 16 + (d & 7) * 2;
+      part[half] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((RG_LDS v4i16_t*)(vbase + off));
     }
+    const uint2 lo = __builtin_bit_cast(uint2, part[0]);
+    const uint2 hi = __builtin_bit_cast(uint2, part[1]);
+    return make_uint4(lo.x, lo.y, hi.x, hi.y);
+  };
+  // The first kVAhead V operands are read before the softmax (their latency hides under it),
+  // the rest kVAhead MFMAs ahead of use, in a rolling set of registers.
+  constexpr int kVA = kVAhead < 2 * NDB ? kVAhead : 2 * NDB;
+  auto v_prefetch = [&](int st, uint4 (&va)[kVA]) {
+#pragma unroll
+    for (int m = 0; m < kVA; ++m) va[m] = v_operand(st, m);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto accumulate = [&](int st, const uint32_t (&pk)[8], uint4 (&va)[kVA]) {
+#pragma unroll
+    for (int m = 0; m < 2 * NDB; ++m) {
+      const int n = m / NDB;
+      const uint4 pb = make_uint4(pk[4 * n], pk[4 * n + 1], pk[4 * n + 2], pk[4 * n + 3]);
+      __builtin_amdgcn_sched_barrier(0);
+      o[m % NDB] = MF::run(va[m % kVA], pb, o[m % NDB]);
+      if (m + kVA < 2 * NDB) va[m % kVA] = v_operand(st, m + kVA);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   };
   // This wave's copies of tile `need` have landed (all but the newest `pending` groups),
   // then the barrier shows every wave's copies and retires the stages read before it.
@@ -588,9 +632,11 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   for (; kt < kend; ++kt) {
     const int kn = min(kt + 1, nkt - 1);  // past the end: tile nkt-1 again (no new maximum)
     f32x16_t cn = scores(kn % kPStages);
+    uint4 va[kVA];
+    v_prefetch(kt % kPStages, va);
     uint32_t pk[8];
     probs(c, pk);
-    accumulate(kt % kPStages, pk);
+    accumulate(kt % kPStages, pk, va);
     const float tmax = mask_max(cn, kn);
     update_max(tmax);
     c = cn;
@@ -613,17 +659,21 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
 #pragma unroll
   for (int p = 0; p < kPStages - 1; ++p) issue_tile(min(p, nkt - 1), p);
   int kt = 0;
+  int st = 0;  // ring stage of tile kt (kt % kPStages, kept as a rotating counter)
   for (;;) {
   // Iterations whose refill tile kt + kPStages - 1 lies in the current block-table window.
   const int kend = min(nkt, wb + 65 - kPStages);
   for (; kt < kend; ++kt) {
     wait_tiles(std::integral_constant<int, kPStages - 2>{});
-    issue_tile(min(kt + kPStages - 1, nkt - 1), (kt + kPStages - 1) % kPStages);
-    f32x16_t c = scores(kt % kPStages);
+    issue_tile(min(kt + kPStages - 1, nkt - 1), st == 0 ? kPStages - 1 : st - 1);
+    f32x16_t c = scores(st);
+    uint4 va[kVA];
+    v_prefetch(st, va);
     update_max(mask_max(c, kt));
     uint32_t pk[8];
     probs(c, pk);
-    accumulate(kt % kPStages, pk);
+    accumulate(st, pk, va);
+    st = st == kPStages - 1 ? 0 : st + 1;
   }
   if (kt >= nkt) break;
   wb += 64;
@@ -708,14 +758,15 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
   }
   PrefillArgs a{query, key_cache, value_cache, block_table, context_lens, cu_seqlens, output,
                 scale * kLog2e, num_heads, num_kv_heads, head_dim, block_size,
-                max_blocks_per_seq, num_seqs, num_tokens, 0, 0, stride};
+                max_blocks_per_seq, num_seqs, num_tokens, 0, 0, stride, 0};
   hipStream_t s = as_stream(stream);
   const int eb = dtype_bytes(dtype);
   if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && scale > 0.f && num_heads == 4 * num_kv_heads &&
       block_size == kBlk &&
       (head_dim == 64 || head_dim == 128) && max_blocks_per_seq > 0 && aligned16(query) &&
       aligned16(key_cache) && aligned16(value_cache) && (stride * eb) % 16 == 0 &&
-      (reinterpret_cast<uintptr_t>(output) & 7u) == 0) {
+      stride * eb <= (int64_t)UINT32_MAX && (reinterpret_cast<uintptr_t>(output) & 7u) == 0) {
+    a.kv_stride_bytes = (uint32_t)(stride * eb);
     // Tile ranks per sequence from max_query_len (a hint: the kernel's last rank covers any
     // tiles beyond it; no query run is longer than num_tokens).
     const int64_t qmax = std::min<int64_t>(std::max<int32_t>(max_query_len, 1), num_tokens);
