@@ -12,6 +12,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "rg_common.hpp"
@@ -39,6 +40,7 @@ struct PrefillArgs {
   int32_t num_tokens;
   int32_t rank_tiles;  // ceil(max_query_len / 32): tile ranks launched per sequence (MFMA path)
   int32_t sched_kbound;  // > 0: bound on the work keys of the sorted schedule (MFMA path)
+  int32_t queue_slot;    // >= 0: work items come from the counters of this slot (MFMA path)
   int64_t kv_stride;
   uint32_t kv_stride_bytes;  // MFMA path: block stride in bytes (below 2^32)
 };
@@ -211,6 +213,16 @@ constexpr int kSchedKeys = RG_PF_SCHED_KEYS;
 // Orders this wave's earlier LDS writes before its later LDS reads.
 __device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 constexpr int kSchedSeqs = 256;
+// Work queues of the MFMA kernel: per launch slot, one item counter per kv-head and a count of
+// finished workgroups; the last workgroup of a launch puts them back to zero.  Launches take
+// the slots in turn, so launches in flight at the same time (other streams) use different
+// counters unless kQueueSlots of them overlap.
+#ifndef RG_PF_QUEUE
+#define RG_PF_QUEUE 1
+#endif
+constexpr int kQueueSlots = 64;
+constexpr int kQueueHeads = 63;
+__device__ int g_prefill_queue[kQueueSlots][kQueueHeads + 1];
 constexpr float kSlack = 8.f;           // log2 headroom of the lazy softmax rescale
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -222,6 +234,16 @@ template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float lo, float hi
 }
 template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)lo, (_Float16)hi});
+}
+// acc + lo + hi of a packed pair (v_dot2 with (1, 1), fp32 accumulation).
+template <typename T> __device__ __forceinline__ float pair_sum(uint32_t pair, float acc);
+template <> __device__ __forceinline__ float pair_sum<bf16_t>(uint32_t pair, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair),
+                                         __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
+}
+template <> __device__ __forceinline__ float pair_sum<f16_t>(uint32_t pair, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pair), __builtin_bit_cast(f16x2_t, 0x3C003C00u),
+                                acc, false);
 }
 
 // LDS image of one key tile (two KV blocks of 16 keys).  K: the 16-byte chunk c of key k of
@@ -362,9 +384,23 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
       ins_lds[ld] = TL::KBYTES + vi * 1024;
     }
   }
-  for (int round = 0; round * nq_wg < n_items; ++round) {
-  const int u = round * nq_wg + ((round & 1) ? nq_wg - 1 - qw : qw);
-  if (u >= n_items) continue;
+  // Work items: from the kv-head's queue counter (dynamic: a workgroup that runs ahead of the
+  // others on its CU takes more items), or else statically in snake order.
+  int* const queue = a.queue_slot >= 0 ? &g_prefill_queue[a.queue_slot][0] : nullptr;
+  __shared__ int s_item;
+  for (int round = 0;; ++round) {
+  int u;
+  if (queue) {
+    if (tid == 0) s_item = atomicAdd(&queue[kvh], 1);
+    __syncthreads();
+    u = __builtin_amdgcn_readfirstlane(s_item);
+    __syncthreads();
+    if (u >= n_items) break;
+  } else {
+    if (round * nq_wg >= n_items) break;
+    u = round * nq_wg + ((round & 1) ? nq_wg - 1 - qw : qw);
+    if (u >= n_items) continue;
+  }
   int s, t_first, t_stop;
   if (sorted) {
     // key k: the largest with B[k] > u (B is non-increasing); i: rank of the item among key k's.
@@ -537,14 +573,18 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     float tmax = c[0];
 #pragma unroll
     for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, c[v]);
-    const float other = __int_as_float(__builtin_amdgcn_ds_bpermute(xor32_addr, __float_as_int(tmax)));
-    return fmaxf(tmax, other) * a.scale_log2;
+    return tmax * a.scale_log2;
   };
   // Online softmax with a lazy maximum: m_run only moves when a tile's maximum exceeds it by
   // more than kSlack, so p = 2^(x - m_run) stays below 2^kSlack and the O^T rescale is rare.
-  auto update_max = [&](float tmax) {
-    const bool grow = tmax > m_run + kSlack;
-    if (__ballot(grow)) {
+  // Each lane checks its own half of the query's keys; only when some lane's half exceeds the
+  // slack do the two halves (lanes l and l ^ 32, which must keep the same m_run because the
+  // PV product sums over both) exchange their maxima.
+  auto update_max = [&](float tmax_half) {
+    if (__ballot(tmax_half > m_run + kSlack)) {
+      const float other = __int_as_float(__builtin_amdgcn_ds_bpermute(xor32_addr, __float_as_int(tmax_half)));
+      const float tmax = fmaxf(tmax_half, other);
+      const bool grow = tmax > m_run + kSlack;
       const float m_new = grow ? tmax : m_run;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
@@ -557,16 +597,22 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   };
   // Probabilities of tile scores c as the packed B operand of the PV product (keys 16n+4hh+r
   // and 16n+8+4hh+r in k-slots 8hh..8hh+7 for n = 0, 1).
+  // The row sum adds the rounded pairs (two dot products with (1, 1)), so the normaliser
+  // weighs exactly the probabilities that enter the PV product.
   auto probs = [&](const f32x16_t& c, uint32_t (&pk)[8]) {
-    float psum = 0.f;
 #pragma unroll
     for (int v = 0; v < 16; v += 2) {
       const float p0 = __builtin_amdgcn_exp2f(fmaf(c[v], a.scale_log2, -m_run));
       const float p1 = __builtin_amdgcn_exp2f(fmaf(c[v + 1], a.scale_log2, -m_run));
-      psum += p0 + p1;
       pk[v / 2] = pack2<T>(p0, p1);
     }
-    l_run += psum;
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      s0 = pair_sum<T>(pk[i], s0);
+      s1 = pair_sum<T>(pk[i + 1], s1);
+    }
+    l_run += s0 + s1;
   };
   // O^T += V^T P^T for the tile in stage st, in two 16-key MFMA steps.  The A operand comes
   // from the transposing LDS read: in each 16-lane group, lane 4e+q points at
@@ -665,8 +711,9 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   const int kend = min(nkt, wb + 65 - kPStages);
   for (; kt < kend; ++kt) {
     wait_tiles(std::integral_constant<int, kPStages - 2>{});
-    issue_tile(min(kt + kPStages - 1, nkt - 1), st == 0 ? kPStages - 1 : st - 1);
     f32x16_t c = scores(st);
+    // The copies of tile kt + kPStages - 1 go out while the QK MFMAs run.
+    issue_tile(min(kt + kPStages - 1, nkt - 1), st == 0 ? kPStages - 1 : st - 1);
     uint4 va[kVA];
     v_prefetch(st, va);
     update_max(mask_max(c, kt));
@@ -703,6 +750,14 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   }
   }  // tiles of this work item
   }  // work items of this workgroup
+  if (queue) {
+    // Every workgroup has taken its last item; the last one to get here clears the slot.
+    __syncthreads();
+    if (tid == 0 && atomicAdd(&queue[kQueueHeads], 1) == (int)gridDim.x - 1) {
+      for (int h = 0; h < hkv; ++h) atomicExch(&queue[h], 0);
+      atomicExch(&queue[kQueueHeads], 0);
+    }
+  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -758,7 +813,7 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
   }
   PrefillArgs a{query, key_cache, value_cache, block_table, context_lens, cu_seqlens, output,
                 scale * kLog2e, num_heads, num_kv_heads, head_dim, block_size,
-                max_blocks_per_seq, num_seqs, num_tokens, 0, 0, stride, 0};
+                max_blocks_per_seq, num_seqs, num_tokens, 0, 0, -1, stride, 0};
   hipStream_t s = as_stream(stream);
   const int eb = dtype_bytes(dtype);
   if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && scale > 0.f && num_heads == 4 * num_kv_heads &&
@@ -775,6 +830,9 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
     // prior + L <= the table's tokens and L <= num_tokens.
     const int64_t kbound = (std::max<int64_t>((int64_t)max_blocks_per_seq * block_size, num_tokens) + 62) / kPT + 1;
     a.sched_kbound = (kbound <= kSchedKeys && num_seqs <= kSchedSeqs) ? (int32_t)kbound : 0;
+    static std::atomic<uint32_t> launches{0};
+    a.queue_slot = (RG_PF_QUEUE && num_kv_heads <= kQueueHeads)
+                       ? (int32_t)(launches.fetch_add(1, std::memory_order_relaxed) % kQueueSlots) : -1;
     // RG_PF_WG_PER_CU resident workgroups per CU, split evenly over the kv-heads, at most one
     // per item.
     const int64_t items = (int64_t)a.rank_tiles * num_seqs;

@@ -105,3 +105,52 @@ def test_prefill_wide_table_rank_order(device, kernels):
     bt = wl.assign_blocks(prior + lens, 16, 400, 2200, rng)
     w = wl.PrefillWorkload("wide_table", "bf16", 32, 8, 128, 16, 400, lens, bt, 4, prior=prior)
     _run(device, kernels, w, seed=99)
+
+
+def test_prefill_repeated_launches_and_streams(device, kernels):
+    """The MFMA kernel takes its work items from per-launch counters that the last workgroup
+    clears: 140 launches (every counter slot reused twice), then launches alternating between
+    two streams without waits between them, all bit-equal to the first launch, which matches
+    the oracle (bf16 D 128, with prior context)."""
+    rng = np.random.default_rng(21)
+    lens = np.array([300, 45, 129, 800, 7], np.int32)
+    prior = np.array([0, 500, 64, 0, 1000], np.int32)
+    bt = wl.assign_blocks(prior + lens, 16, 300, 120, rng)
+    w = wl.PrefillWorkload("queue", "bf16", 32, 8, 128, 16, 300, lens, bt, 4, prior=prior)
+    first = _run(device, kernels, w, seed=23)
+    # the same device inputs again (same generator, same draw order as _run)
+    drng = np.random.default_rng(23)
+    T, H, hkv, D, bs = w.num_tokens, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
+    q = normal(drng, (T, H, D), "bf16")
+    k, v = normal(drng, (T, hkv, D), "bf16"), normal(drng, (T, hkv, D), "bf16")
+    kc, vc = normal(drng, (w.num_blocks, hkv, bs, D), "bf16"), normal(drng, (w.num_blocks, hkv, bs, D), "bf16")
+    table = rope_cos_sin_table(int(w.context_lens.max()), D, w.rope_theta)
+    dq, dkc, dvc = to_dev(q, "bf16", device), to_dev(kc, "bf16", device), to_dev(vc, "bf16", device)
+    kernels.launch_rope_reshape_and_cache(dq, to_dev(k, "bf16", device), to_dev(v, "bf16", device), dkc, dvc,
+                                          table.to(device), i32(w.positions, device), i32(w.slot_mapping, device),
+                                          H, hkv, D, bs, T)
+    bt_d, ctx_d, cu_d = i32(w.block_table, device), i32(w.context_lens, device), i32(w.cu_seqlens, device)
+    maxq = int(w.seq_lens.max())
+
+    def launch(out):
+        kernels.launch_prefill_packed(dq, dkc, dvc, bt_d, ctx_d, cu_d, out, w.scale, H, hkv, D, bs, w.max_blocks,
+                                      w.num_seqs, T, maxq)
+
+    outs = [torch.full_like(dq, float("nan")) for _ in range(4)]
+    for i in range(140):
+        launch(outs[i % 4])
+        if i % 4 == 3:
+            torch.cuda.synchronize()
+            for o in outs:
+                assert np.array_equal(dev_f32(o), first), f"launch {i}"
+    streams = [torch.cuda.Stream(device=device), torch.cuda.Stream(device=device)]
+    sides = [[torch.full_like(dq, float("nan")) for _ in range(3)] for _ in streams]
+    torch.cuda.synchronize()
+    for i in range(3):
+        for st, side in zip(streams, sides):
+            with torch.cuda.stream(st):
+                launch(side[i])
+    torch.cuda.synchronize()
+    for side in sides:
+        for o in side:
+            assert np.array_equal(dev_f32(o), first)
