@@ -12,7 +12,6 @@
 #include <math.h>
 
 #include <algorithm>
-#include <atomic>
 #include <type_traits>
 
 #include "rg_common.hpp"
@@ -40,7 +39,6 @@ struct PrefillArgs {
   int32_t num_tokens;
   int32_t rank_tiles;  // ceil(max_query_len / 32): tile ranks launched per sequence (MFMA path)
   int32_t sched_kbound;  // > 0: bound on the work keys of the sorted schedule (MFMA path)
-  int32_t queue_slot;    // >= 0: work items come from the counters of this slot (MFMA path)
   int64_t kv_stride;
   uint32_t kv_stride_bytes;  // MFMA path: block stride in bytes (below 2^32)
 };
@@ -163,13 +161,6 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 #ifndef RG_PF_STAGES
 #define RG_PF_STAGES 3
 #endif
-// 1: software-pipelined tile loop (scores of tile kt+1 under the softmax of tile kt);
-// 0: in-order tile loop.  In-order needs 16 fewer VGPRs, which lets three workgroups (three
-// waves per SIMD) share a CU; the extra resident waves hide more latency than the pipeline
-// did with two (measured at config 4: 209 us against 221 us).
-#ifndef RG_PF_PIPELINE
-#define RG_PF_PIPELINE 0
-#endif
 // Resident workgroups per CU the persistent grid is sized for (LDS: stages x tile bytes each).
 #ifndef RG_PF_WG_PER_CU
 #define RG_PF_WG_PER_CU 3
@@ -213,16 +204,7 @@ constexpr int kSchedKeys = RG_PF_SCHED_KEYS;
 // Orders this wave's earlier LDS writes before its later LDS reads.
 __device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 constexpr int kSchedSeqs = 256;
-// Work queues of the MFMA kernel: per launch slot, one item counter per kv-head and a count of
-// finished workgroups; the last workgroup of a launch puts them back to zero.  Launches take
-// the slots in turn, so launches in flight at the same time (other streams) use different
-// counters unless kQueueSlots of them overlap.
-#ifndef RG_PF_QUEUE
-#define RG_PF_QUEUE 1
-#endif
-constexpr int kQueueSlots = 64;
-constexpr int kQueueHeads = 63;
-__device__ int g_prefill_queue[kQueueSlots][kQueueHeads + 1];
+
 constexpr float kSlack = 8.f;           // log2 headroom of the lazy softmax rescale
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -303,23 +285,41 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   const int nq_wg = gridDim.x / hkv;
   const int qw = blockIdx.x / hkv;
   const bool sorted = a.sched_kbound > 0;
+  const int kb = a.sched_kbound;  // sorted schedule: keys live in [1, kb]
+  const int table_tokens = a.max_blocks * a.block_size;
+  const int H = a.num_heads;
+  const int head = kvh * G + w;
+  const int j = lane & 31;   // query column owned by this lane
+  const int hh = lane >> 5;  // which half of the k-slots
   __shared__ int sched_b[kSchedKeys + 2];
-  __shared__ int2 sched_seq[kSchedSeqs];
+  // Sorted schedule, per sequence: its first packed row and the positions cached before its
+  // rows (context - rows, negative for an inconsistent context); entry num_seqs holds the end
+  // of the packed stream.
+  __shared__ int2 sched_seq[kSchedSeqs + 1];
+  // Work keys of a sequence of L rows after `prior` cached positions: base ceil(prior / 32) + 1
+  // (capped at kb + 1) and the number of its query tiles whose key is within the bound.
+  auto seq_keys = [&](int L, int prior) {
+    const int nt = L > 0 ? (L + kPT - 1) / kPT : 0;
+    const int bq = min((max(prior, 0) + kPT - 1) / kPT + 1, kb + 1);
+    return make_int2(bq, min(nt, kb + 1 - bq));
+  };
   int n_items = a.rank_tiles * a.num_seqs;
   if (sorted) {
-    const int kb = a.sched_kbound;  // keys live in [1, kb]
     for (int k = tid; k < kb + 2; k += kPThreads) sched_b[k] = 0;
     __syncthreads();
-    for (int q = tid; q < a.num_seqs; q += kPThreads) {
-      const int Lq = cu_seqlens[q + 1] - cu_seqlens[q];
-      const int ntq = Lq > 0 ? (Lq + kPT - 1) / kPT : 0;
-      const int pr = max(0, min(context_lens[q], a.max_blocks * a.block_size) - Lq);
-      const int bq = min((pr + kPT - 1) / kPT + 1, kb + 1);
-      const int nq_keys = min(ntq, kb + 1 - bq);  // keys past the bound do not occur (see host)
-      sched_seq[q] = make_int2(bq, nq_keys);
-      if (nq_keys > 0) {  // difference array of the per-key counts
-        atomicAdd(&sched_b[bq], 1);
-        atomicAdd(&sched_b[bq + nq_keys], -1);
+    for (int q = tid; q <= a.num_seqs; q += kPThreads) {
+      const int r0 = cu_seqlens[q];
+      if (q == a.num_seqs) {
+        sched_seq[q] = make_int2(r0, 0);
+        continue;
+      }
+      const int Lq = cu_seqlens[q + 1] - r0;
+      const int pr = min(context_lens[q], table_tokens) - Lq;
+      sched_seq[q] = make_int2(r0, pr);
+      const int2 kn = seq_keys(Lq, pr);  // keys past the bound do not occur (see host)
+      if (kn.y > 0) {  // difference array of the per-key counts
+        atomicAdd(&sched_b[kn.x], 1);
+        atomicAdd(&sched_b[kn.x + kn.y], -1);
       }
     }
     __syncthreads();
@@ -384,102 +384,119 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
       ins_lds[ld] = TL::KBYTES + vi * 1024;
     }
   }
-  // Work items: from the kv-head's queue counter (dynamic: a workgroup that runs ahead of the
-  // others on its CU takes more items), or else statically in snake order.
-  int* const queue = a.queue_slot >= 0 ? &g_prefill_queue[a.queue_slot][0] : nullptr;
-  __shared__ int s_item;
-  for (int round = 0;; ++round) {
-  int u;
-  if (queue) {
-    if (tid == 0) s_item = atomicAdd(&queue[kvh], 1);
-    __syncthreads();
-    u = __builtin_amdgcn_readfirstlane(s_item);
-    __syncthreads();
-    if (u >= n_items) break;
-  } else {
-    if (round * nq_wg >= n_items) break;
-    u = round * nq_wg + ((round & 1) ? nq_wg - 1 - qw : qw);
-    if (u >= n_items) continue;
-  }
-  int s, t_first, t_stop;
-  if (sorted) {
-    // key k: the largest with B[k] > u (B is non-increasing); i: rank of the item among key k's.
-    int lo = 1, hi = a.sched_kbound;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (sched_b[mid] > u) lo = mid;
-      else hi = mid - 1;
-    }
-    const int k = __builtin_amdgcn_readfirstlane(lo);
-    int i = __builtin_amdgcn_readfirstlane(u - sched_b[k + 1]);
-    s = -1;
-    for (int c0 = 0; c0 < a.num_seqs && s < 0; c0 += 64) {
-      const int q = c0 + lane;
-      const int2 bn = q < a.num_seqs ? sched_seq[q] : make_int2(0, 0);
-      uint64_t m = __ballot(bn.x <= k && k < bn.x + bn.y);
-      const int cnt = __builtin_popcountll(m);
-      if (i < cnt) {
-        for (; i > 0; --i) m &= m - 1;
-        s = c0 + __ffsll((unsigned long long)m) - 1;
-      } else {
-        i -= cnt;
-      }
-    }
-    s = __builtin_amdgcn_readfirstlane(s);
-    t_first = k - sched_seq[s].x;
-    t_stop = t_first - 1;
-  } else {
-    s = u % a.num_seqs;
-    const int rank = u / a.num_seqs;
-    const int Ls = cu_seqlens[s + 1] - cu_seqlens[s];
-    const int nts = (Ls + kPT - 1) / kPT;
-    if (rank >= nts) continue;
-    t_first = nts - 1 - rank;
-    t_stop = rank == a.rank_tiles - 1 ? -1 : t_first - 1;
-  }
-  const int row0 = cu_seqlens[s];
-  const int L = cu_seqlens[s + 1] - row0;
-  const int ctx = min(context_lens[s], a.max_blocks * a.block_size);
-  const int prior = ctx - L;
-  for (int t = t_first; t > t_stop; --t) {
-  const int q0 = t * kPT;                      // first query of the tile (within the sequence)
-  const int nq = min(kPT, L - q0);
-  const int pos_min = prior + q0;
-  const int pos_max = prior + q0 + nq - 1;
-  const int head = kvh * G + w;
-  const int H = a.num_heads;
-  const int j = lane & 31;                     // query column owned by this lane
-  const int hh = lane >> 5;                    // which half of the k-slots
-  const bool q_valid = j < nq && pos_min >= 0;
-  const int my_pos = pos_min + j;
-
-  const int32_t* bt = block_table + (int64_t)s * a.max_blocks;
-  const int last_blk = pos_max / kBlk;
-  // Block-table window in registers: lane i holds the numbers of blocks 2 * wb + i and
-  // 2 * wb + 64 + i (clamped to the sequence's last block), i.e. of key tiles wb .. wb + 63;
-  // a tile's two block numbers are then v_readlane's, with no memory wait in the tile loop.
-  int wb = 0;
-  int btw0, btw1;
-  auto load_window = [&]() {
-    btw0 = bt[min(2 * wb + lane, last_blk)];
-    btw1 = bt[min(2 * wb + 64 + lane, last_blk)];
+  // A unit of work: query tile t of sequence s (rows row0 + 32 t ..), whose rows follow
+  // `prior` cached positions.  An item of the sorted schedule is one unit; an item of the rank
+  // order may hold several (tiles t down to t_stop + 1).
+  struct Unit {
+    int s, t, t_stop, row0, L, prior;
   };
-  load_window();
+  // Item u -> its first unit; false for an item without a tile (rank order).
+  auto resolve = [&](int u, Unit& un) -> bool {
+    if (sorted) {
+      // key k: the largest with B[k] > u (B is non-increasing); i: rank of the item among key k's.
+      int lo = 1, hi = kb;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (sched_b[mid] > u) lo = mid;
+        else hi = mid - 1;
+      }
+      const int k = __builtin_amdgcn_readfirstlane(lo);
+      int i = __builtin_amdgcn_readfirstlane(u - sched_b[k + 1]);
+      int sq = -1;
+      for (int c0 = 0; c0 < a.num_seqs && sq < 0; c0 += 64) {
+        const int q = c0 + lane;
+        int2 kn = make_int2(0, 0);
+        if (q < a.num_seqs) {
+          const int2 m0 = sched_seq[q];
+          kn = seq_keys(sched_seq[q + 1].x - m0.x, m0.y);
+        }
+        uint64_t m = __ballot(kn.x <= k && k < kn.x + kn.y);
+        const int cnt = __builtin_popcountll(m);
+        if (i < cnt) {
+          for (; i > 0; --i) m &= m - 1;
+          sq = c0 + __ffsll((unsigned long long)m) - 1;
+        } else {
+          i -= cnt;
+        }
+      }
+      un.s = __builtin_amdgcn_readfirstlane(sq);
+      const int2 m0 = sched_seq[un.s];
+      un.row0 = __builtin_amdgcn_readfirstlane(m0.x);
+      un.L = __builtin_amdgcn_readfirstlane(sched_seq[un.s + 1].x) - un.row0;
+      un.prior = __builtin_amdgcn_readfirstlane(m0.y);
+      un.t = k - seq_keys(un.L, un.prior).x;
+      un.t_stop = un.t - 1;
+      return true;
+    }
+    un.s = u % a.num_seqs;
+    const int rank = u / a.num_seqs;
+    un.row0 = cu_seqlens[un.s];
+    un.L = cu_seqlens[un.s + 1] - un.row0;
+    const int nts = (un.L + kPT - 1) / kPT;
+    if (rank >= nts) return false;
+    un.prior = min(context_lens[un.s], table_tokens) - un.L;
+    un.t = nts - 1 - rank;
+    un.t_stop = rank == a.rank_tiles - 1 ? -1 : un.t - 1;
+    return true;
+  };
+  // Work items of this workgroup, in snake order (round r: position r * Q + q, or
+  // r * Q + Q - 1 - q on odd rounds, for the Q workgroups of the kv-head); n_items once done.
+  // (A shared work counter was measured: it evens out the workgroups of a CU but not the
+  // CU's finish time, and its round trips cost more than it saved.)
+  int round = 0;
+  auto take_item = [&]() -> int {
+    const int r = round++;
+    const int u = r * nq_wg + ((r & 1) ? nq_wg - 1 - qw : qw);
+    return u < n_items ? u : n_items;
+  };
 
-  // Q^T operand (B): lane holds q[query j][16i + 8hh .. +8] for every d chunk i.
+  // Per-unit registers, loaded ahead of the unit: the block-table window (lane i holds the
+  // numbers of blocks 2 wb + i and 2 wb + 64 + i, clamped to the unit's last block, i.e. of key
+  // tiles wb .. wb + 63; a tile's two block numbers are then v_readlane's) and the Q^T operand
+  // (lane holds q[query j][16i + 8hh .. +8] for every d chunk i; zero for rows without a
+  // position).
+  int btw0 = 0, btw1 = 0;
   uint4 qb[NKC];
-  {
-    const uint4* qr = reinterpret_cast<const uint4*>(q + ((int64_t)(row0 + q0 + (q_valid ? j : 0)) * H + head) * D);
+  auto load_window = [&](const Unit& un, int wbase, int last_blk) {
+    const int32_t* bt = block_table + (int64_t)un.s * a.max_blocks;
+    btw0 = bt[min(2 * wbase + lane, last_blk)];
+    btw1 = bt[min(2 * wbase + 64 + lane, last_blk)];
+  };
+  auto load_unit = [&](const Unit& un) {
+    const int q0 = un.t * kPT;
+    const int nq = min(kPT, un.L - q0);
+    const int pos_max = un.prior + q0 + nq - 1;
+    const bool row_ok = j < nq && un.prior + q0 + j >= 0;
+    if (pos_max >= 0) load_window(un, 0, pos_max / kBlk);
+    const uint4* qr = reinterpret_cast<const uint4*>(q + ((int64_t)(un.row0 + q0 + (row_ok ? j : 0)) * H + head) * D);
 #pragma unroll
-    for (int i = 0; i < NKC; ++i) qb[i] = q_valid ? qr[2 * i + hh] : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < NKC; ++i) qb[i] = row_ok ? qr[2 * i + hh] : make_uint4(0, 0, 0, 0);
+  };
+
+  Unit cur{};
+  bool have = false;
+  for (int u = take_item(); u < n_items; u = take_item()) {
+    if (resolve(u, cur)) {
+      have = true;
+      break;
+    }
   }
-  // Settle Q and the window here, once: otherwise the first use inside the tile loop would
-  // wait for every vector-memory operation in flight (the tile prefetches included) on every
-  // iteration.
+  if (have) load_unit(cur);
+  while (have) {
+  const int row0 = cur.row0;
+  const int q0 = cur.t * kPT;                  // first query of the tile (within the sequence)
+  const int nq = min(kPT, cur.L - q0);
+  const int pos_min = cur.prior + q0;
+  const int pos_max = pos_min + nq - 1;
+  const bool row_ok = j < nq && pos_min + j >= 0;
+  // Rows without a position attend like the tile's last row (finite scores; written as zeros).
+  const int my_pos = row_ok ? pos_min + j : pos_max;
+  int wb = 0;
+  // Q and the window have landed; nothing else is in flight.
   __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
   const int64_t head_off = (int64_t)kvh * kBlk * D;
   const uint32_t head_off_bytes = (uint32_t)head_off * 2u;
-  const int nkt = pos_max / kPT + 1;
+  const int nkt = pos_max >= 0 ? pos_max / kPT + 1 : 0;
   const uint32_t lds_base = (uint32_t)(uintptr_t)((RG_LDS char*)lds);
 
   // Issues this wave's share of the global->LDS copies of key tile kt (wb <= kt < wb + 64)
@@ -662,58 +679,31 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     tile_barrier();
   };
 
-#if RG_PF_PIPELINE == 1
-  // Prologue: tiles 0 .. kPStages-1 in flight (past the end: repeats of the last tile); with
-  // tiles 0 and 1 in LDS, the scores and maximum of tile 0.
+  // In-order tile loop: the copies of tiles kt .. min(kt + kPStages - 2, nkt - 1) are in flight
+  // when iteration kt starts; once tile kt has landed everywhere (wait + barrier, which also
+  // shows every wave is done with tile kt - 1), stage (kt - 1) % kPStages takes tile
+  // kt + kPStages - 1 (if there is one), then tile kt is computed: scores, maximum,
+  // probabilities, PV.
+  static_assert(kPStages == 3 || kPStages == 4, "ring depth");
+  auto wait_for = [&](int kt) {  // tile kt landed; min(kPStages - 2, nkt - 1 - kt) newer tiles may not have
+    const int newer = nkt - 1 - kt;
+    if (newer >= kPStages - 2) wait_tiles(std::integral_constant<int, kPStages - 2>{});
+    else if (kPStages == 4 && newer == 1) wait_tiles(std::integral_constant<int, 1>{});
+    else wait_tiles(std::integral_constant<int, 0>{});
+  };
 #pragma unroll
-  for (int p = 0; p < kPStages; ++p) issue_tile(min(p, nkt - 1), p);
-  wait_tiles(std::integral_constant<int, kPStages - 2>{});
-  f32x16_t c = scores(0);
-  update_max(mask_max(c, 0));
-
-  int kt = 0;
-  for (;;) {
-  // Iterations whose refill tile kt + kPStages lies in the current block-table window.
-  const int kend = min(nkt, wb + 64 - kPStages);
-  for (; kt < kend; ++kt) {
-    const int kn = min(kt + 1, nkt - 1);  // past the end: tile nkt-1 again (no new maximum)
-    f32x16_t cn = scores(kn % kPStages);
-    uint4 va[kVA];
-    v_prefetch(kt % kPStages, va);
-    uint32_t pk[8];
-    probs(c, pk);
-    accumulate(kt % kPStages, pk, va);
-    const float tmax = mask_max(cn, kn);
-    update_max(tmax);
-    c = cn;
-    // Tile kt+2 in LDS; every wave is done with stage kt, which takes tile kt + kPStages.
-    wait_tiles(std::integral_constant<int, kPStages - 3>{});
-    issue_tile(min(kt + kPStages, nkt - 1), kt % kPStages);
-  }
-  if (kt >= nkt) break;
-  // Next 64 tiles (sequences past 2048 positions): the wait drains the copies in flight once.
-  wb += 64;
-  load_window();
-  __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
-  }
-
-#else
-  // In-order tile loop: tiles kt .. kt + kPStages - 2 are in flight when iteration kt starts;
-  // once tile kt has landed everywhere (wait + barrier, which also shows every wave is done
-  // with tile kt - 1), stage (kt - 1) % kPStages takes tile kt + kPStages - 1, then tile kt is
-  // computed: scores, maximum, probabilities, PV.
-#pragma unroll
-  for (int p = 0; p < kPStages - 1; ++p) issue_tile(min(p, nkt - 1), p);
+  for (int p = 0; p < kPStages - 1; ++p)
+    if (p < nkt) issue_tile(p, p);
   int kt = 0;
   int st = 0;  // ring stage of tile kt (kt % kPStages, kept as a rotating counter)
-  for (;;) {
+  while (kt < nkt) {
   // Iterations whose refill tile kt + kPStages - 1 lies in the current block-table window.
   const int kend = min(nkt, wb + 65 - kPStages);
   for (; kt < kend; ++kt) {
-    wait_tiles(std::integral_constant<int, kPStages - 2>{});
+    wait_for(kt);
     f32x16_t c = scores(st);
     // The copies of tile kt + kPStages - 1 go out while the QK MFMAs run.
-    issue_tile(min(kt + kPStages - 1, nkt - 1), st == 0 ? kPStages - 1 : st - 1);
+    if (kt + kPStages - 1 < nkt) issue_tile(kt + kPStages - 1, st == 0 ? kPStages - 1 : st - 1);
     uint4 va[kVA];
     v_prefetch(st, va);
     update_max(mask_max(c, kt));
@@ -724,40 +714,77 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   }
   if (kt >= nkt) break;
   wb += 64;
-  load_window();
+  load_window(cur, wb, pos_max / kBlk);
   __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
   }
-#endif
 
-  // Every copy issued (the ring's tail repeats the last tile) lands before the LDS is reused
-  // or released.
-  __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
+  // Next unit: the next tile of this item or the first unit of the next item.  Every wave is
+  // done with the LDS stages after the barrier; the next unit's Q and window loads go out
+  // before this unit's epilogue.
   tile_barrier();
-  // Normalise (the two halves of a query's keys live in lanes l and l ^ 32) and write.
+  Unit nxt{};
+  bool nhave = false;
+  if (cur.t - 1 > cur.t_stop) {
+    nxt = cur;
+    nxt.t = cur.t - 1;
+    nhave = true;
+  } else {
+    for (int u = take_item(); u < n_items; u = take_item()) {
+      if (resolve(u, nxt)) {
+        nhave = true;
+        break;
+      }
+    }
+  }
+  // Normalise (the two halves of a query's keys live in lanes l and l ^ 32) and write; rows
+  // without a position get zeros.  The tile goes out through LDS, DP columns at a time: each
+  // wave writes its rows into its quarter of ring stage kPStages - 1 (16-byte chunks XOR-
+  // swizzled by the row), then reads whole row pieces back, so that every store writes
+  // 16 bytes per lane over full runs of a row.  That stage is free here: after the barrier
+  // above nobody reads the ring, the next unit's prologue fills stages 0 and 1, and stage
+  // kPStages - 1 is refilled only after the next unit's first barrier.
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if (q_valid) {
-  const float inv = 1.f / l_tot;
-  S* orow = static_cast<S*>(a.out) + ((int64_t)(row0 + q0 + j) * H + head) * D;
+  const float inv = row_ok ? 1.f / l_tot : 0.f;
+  if (nhave) load_unit(nxt);
+  {
+    constexpr int DP = TL::BYTES / kPWaves / (kPT * 2);  // columns per pass
+    constexpr int CH = DP / 8;                            // 16-byte chunks per row piece
+    constexpr int RPR = 64 / CH;                          // rows per read
+    static_assert(D % DP == 0 && DP % 32 == 0 && 64 % CH == 0, "epilogue passes");
+    char* ebuf = lds + (kPStages - 1) * TL::BYTES + w * (TL::BYTES / kPWaves);
+    // (The lane's rows are formed here, not hoisted out of the unit loop, where they would
+    // take registers for the whole loop.)
+    int lr = lane;
+    asm volatile("" : "+v"(lr));
+    const int wr = lr & 31;  // row written by this lane (its query column j)
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
+    for (int pass = 0; pass < D / DP; ++pass) {
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      const int d0 = 32 * db + 8 * jb + 4 * hh;
-      const uint32_t w0 = pack2<T>(o[db][4 * jb] * inv, o[db][4 * jb + 1] * inv);
-      const uint32_t w1 = pack2<T>(o[db][4 * jb + 2] * inv, o[db][4 * jb + 3] * inv);
-      *reinterpret_cast<uint2*>(orow + d0) = make_uint2(w0, w1);
+      for (int db = pass * DP / 32; db < (pass + 1) * DP / 32; ++db)
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          const int dl = 32 * db + 8 * jb - pass * DP;  // + 4 hh
+          const uint32_t w0 = pack2<T>(o[db][4 * jb] * inv, o[db][4 * jb + 1] * inv);
+          const uint32_t w1 = pack2<T>(o[db][4 * jb + 2] * inv, o[db][4 * jb + 3] * inv);
+          const int off = wr * (DP * 2) + (((dl >> 3) ^ (wr & (CH - 1))) << 4) + 8 * hh;
+          *reinterpret_cast<uint2*>(ebuf + off) = make_uint2(w0, w1);
+        }
+      wave_lds_fence();
+#pragma unroll
+      for (int i = 0; i < kPT / RPR; ++i) {
+        const int r = i * RPR + lr / CH, c = lr % CH;
+        const uint4 v = *reinterpret_cast<const uint4*>(ebuf + r * (DP * 2) + ((c ^ (r & (CH - 1))) << 4));
+        if (r < nq) {
+          S* orow = static_cast<S*>(a.out) + ((int64_t)(row0 + q0 + r) * H + head) * D;
+          *reinterpret_cast<uint4*>(orow + pass * DP + 8 * c) = v;
+        }
+      }
+      wave_lds_fence();  // the reads have returned before the next pass overwrites the buffer
     }
   }
-  }  // tiles of this work item
-  }  // work items of this workgroup
-  if (queue) {
-    // Every workgroup has taken its last item; the last one to get here clears the slot.
-    __syncthreads();
-    if (tid == 0 && atomicAdd(&queue[kQueueHeads], 1) == (int)gridDim.x - 1) {
-      for (int h = 0; h < hkv; ++h) atomicExch(&queue[h], 0);
-      atomicExch(&queue[kQueueHeads], 0);
-    }
-  }
+  cur = nxt;
+  have = nhave;
+  }  // units of this workgroup
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -813,14 +840,14 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
   }
   PrefillArgs a{query, key_cache, value_cache, block_table, context_lens, cu_seqlens, output,
                 scale * kLog2e, num_heads, num_kv_heads, head_dim, block_size,
-                max_blocks_per_seq, num_seqs, num_tokens, 0, 0, -1, stride, 0};
+                max_blocks_per_seq, num_seqs, num_tokens, 0, 0, stride, 0};
   hipStream_t s = as_stream(stream);
   const int eb = dtype_bytes(dtype);
   if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && scale > 0.f && num_heads == 4 * num_kv_heads &&
       block_size == kBlk &&
       (head_dim == 64 || head_dim == 128) && max_blocks_per_seq > 0 && aligned16(query) &&
       aligned16(key_cache) && aligned16(value_cache) && (stride * eb) % 16 == 0 &&
-      stride * eb <= (int64_t)UINT32_MAX && (reinterpret_cast<uintptr_t>(output) & 7u) == 0) {
+      stride * eb <= (int64_t)UINT32_MAX && aligned16(output)) {
     a.kv_stride_bytes = (uint32_t)(stride * eb);
     // Tile ranks per sequence from max_query_len (a hint: the kernel's last rank covers any
     // tiles beyond it; no query run is longer than num_tokens).
@@ -830,9 +857,6 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
     // prior + L <= the table's tokens and L <= num_tokens.
     const int64_t kbound = (std::max<int64_t>((int64_t)max_blocks_per_seq * block_size, num_tokens) + 62) / kPT + 1;
     a.sched_kbound = (kbound <= kSchedKeys && num_seqs <= kSchedSeqs) ? (int32_t)kbound : 0;
-    static std::atomic<uint32_t> launches{0};
-    a.queue_slot = (RG_PF_QUEUE && num_kv_heads <= kQueueHeads)
-                       ? (int32_t)(launches.fetch_add(1, std::memory_order_relaxed) % kQueueSlots) : -1;
     // RG_PF_WG_PER_CU resident workgroups per CU, split evenly over the kv-heads, at most one
     // per item.
     const int64_t items = (int64_t)a.rank_tiles * num_seqs;

@@ -154,3 +154,30 @@ def test_prefill_repeated_launches_and_streams(device, kernels):
     for side in sides:
         for o in side:
             assert np.array_equal(dev_f32(o), first)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_rows_without_position(device, kernels, D):
+    """Context lengths shorter than the chunk (row j of s has position ctx_s - L_s + j): rows
+    with a negative position are zeros and the others attend to positions 0..pos, as in the
+    oracle; a sequence with no cached position at all is zeros throughout (MFMA path, bf16)."""
+    rng = np.random.default_rng(31 + D)
+    lens = np.array([40, 100, 70, 33, 5], np.int32)
+    ctx = np.array([25, 10, 0, 33, 64], np.int32)
+    hkv, H, bs, nb, mb = 2, 8, 16, 64, 8
+    bt = np.stack([rng.permutation(nb)[:mb] for _ in lens]).astype(np.int32)
+    T = int(lens.sum())
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q = normal(rng, (T, H, D), "bf16")
+    kc, vc = normal(rng, (nb, hkv, bs, D), "bf16"), normal(rng, (nb, hkv, bs, D), "bf16")
+    out = torch.full((T, H, D), float("nan"), dtype=torch.bfloat16, device=device)
+    scale = 1.0 / math.sqrt(D)
+    kernels.launch_prefill_packed(to_dev(q, "bf16", device), to_dev(kc, "bf16", device), to_dev(vc, "bf16", device),
+                                  i32(bt, device), i32(ctx, device), i32(cu, device), out, scale, H, hkv, D, bs, mb,
+                                  len(lens), T, int(lens.max()))
+    torch.cuda.synchronize()
+    want = orc.prefill_packed(q, kc, vc, bt, ctx, cu, scale, "bf16")
+    got = dev_f32(out)
+    assert not np.isnan(got).any()
+    assert_close(got, want, "bf16", "rows without a position")
+    assert np.all(got[cu[2]:cu[3]] == 0)
