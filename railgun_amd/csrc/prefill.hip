@@ -201,6 +201,18 @@ constexpr int kVAhead = RG_PF_VAHEAD;
 #define RG_PF_SCHED_KEYS 512
 #endif
 constexpr int kSchedKeys = RG_PF_SCHED_KEYS;
+// Inclusive prefix sum over the 64 lanes with DPP (no LDS round trips): sums within each row
+// of 16 lanes by shifts of 1, 2, 4 and 8, then lane 15 of rows 0 and 2 into rows 1 and 3,
+// then lane 31 into rows 2 and 3.  Lanes whose source falls outside the row receive 0.
+__device__ __forceinline__ int wave_prefix_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
 // Orders this wave's earlier LDS writes before its later LDS reads.
 __device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 constexpr int kSchedSeqs = 256;
@@ -328,28 +340,16 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
       int carry = 0;
       for (int c0 = 1; c0 <= kb; c0 += 64) {
         const int k = c0 + lane;
-        int v = k <= kb ? sched_b[k] : 0;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const int t2 = __shfl_up(v, o, 64);
-          if (lane >= o) v += t2;
-        }
-        v += carry;
+        const int v = wave_prefix_sum(k <= kb ? sched_b[k] : 0) + carry;
         if (k <= kb) sched_b[k] = v;
-        carry = __shfl(v, 63, 64);
+        carry = __builtin_amdgcn_readlane(v, 63);
       }
       wave_lds_fence();
       carry = 0;
       for (int c1 = kb; c1 >= 1; c1 -= 64) {
         const int k = c1 - lane;
-        int v = k >= 1 ? sched_b[k] : 0;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const int t2 = __shfl_up(v, o, 64);
-          if (lane >= o) v += t2;
-        }
-        v += carry;
-        carry = __shfl(v, 63, 64);
+        const int v = wave_prefix_sum(k >= 1 ? sched_b[k] : 0) + carry;
+        carry = __builtin_amdgcn_readlane(v, 63);
         if (k >= 1) sched_b[k] = v;
       }
       if (lane == 0) sched_b[kb + 1] = 0;
@@ -420,6 +420,7 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
         }
       }
       un.s = __builtin_amdgcn_readfirstlane(sq);
+      if (un.s < 0) return false;  // (not reached with consistent tables)
       const int2 m0 = sched_seq[un.s];
       un.row0 = __builtin_amdgcn_readfirstlane(m0.x);
       un.L = __builtin_amdgcn_readfirstlane(sched_seq[un.s + 1].x) - un.row0;
@@ -694,6 +695,22 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
 #pragma unroll
   for (int p = 0; p < kPStages - 1; ++p)
     if (p < nkt) issue_tile(p, p);
+  // Next unit (the next tile of this item, or the first unit of the next item), found while
+  // the first copies are in flight: it needs only the LDS tables and the static item order.
+  Unit nxt{};
+  bool nhave = false;
+  if (cur.t - 1 > cur.t_stop) {
+    nxt = cur;
+    nxt.t = cur.t - 1;
+    nhave = true;
+  } else {
+    for (int u = take_item(); u < n_items; u = take_item()) {
+      if (resolve(u, nxt)) {
+        nhave = true;
+        break;
+      }
+    }
+  }
   int kt = 0;
   int st = 0;  // ring stage of tile kt (kt % kPStages, kept as a rotating counter)
   while (kt < nkt) {
@@ -718,24 +735,9 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
   }
 
-  // Next unit: the next tile of this item or the first unit of the next item.  Every wave is
-  // done with the LDS stages after the barrier; the next unit's Q and window loads go out
-  // before this unit's epilogue.
+  // Every wave is done with the LDS stages after the barrier; the next unit's Q and window
+  // loads go out before this unit's epilogue.
   tile_barrier();
-  Unit nxt{};
-  bool nhave = false;
-  if (cur.t - 1 > cur.t_stop) {
-    nxt = cur;
-    nxt.t = cur.t - 1;
-    nhave = true;
-  } else {
-    for (int u = take_item(); u < n_items; u = take_item()) {
-      if (resolve(u, nxt)) {
-        nhave = true;
-        break;
-      }
-    }
-  }
   // Normalise (the two halves of a query's keys live in lanes l and l ^ 32) and write; rows
   // without a position get zeros.  The tile goes out through LDS, DP columns at a time: each
   // wave writes its rows into its quarter of ring stage kPStages - 1 (16-byte chunks XOR-
