@@ -7,6 +7,8 @@
 // decode step's few tokens still spread over thousands of waves.
 #include <algorithm>
 
+#include <initializer_list>
+
 #include "rg_common.hpp"
 
 namespace rg {
@@ -136,6 +138,37 @@ __device__ __forceinline__ void rope_row(const typename elem<T>::storage* __rest
 
 constexpr int kRowsPerGroup = kCacheThreads / 64;
 
+// 16-byte form of rope_row for 2-byte elements: this thread rotates the pairs (i, i + D/2) for
+// i in [8c, 8c + 8) with one 16-byte load and store per half and four of cos / sin.  Same
+// arithmetic as rope_row (bit-identical results).
+template <typename T>
+__device__ __forceinline__ void rope_chunk16(const uint16_t* __restrict__ src, uint16_t* dst,
+                                             const float* __restrict__ cs, int half, int c) {
+  using E = elem<T>;
+  const uint4 lo = *reinterpret_cast<const uint4*>(src + 8 * c);
+  const uint4 hi = *reinterpret_cast<const uint4*>(src + half + 8 * c);
+  const float4 c0 = *reinterpret_cast<const float4*>(cs + 8 * c);
+  const float4 c1 = *reinterpret_cast<const float4*>(cs + 8 * c + 4);
+  const float4 s0 = *reinterpret_cast<const float4*>(cs + half + 8 * c);
+  const float4 s1 = *reinterpret_cast<const float4*>(cs + half + 8 * c + 4);
+  const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w}, hw[4] = {hi.x, hi.y, hi.z, hi.w};
+  const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  uint32_t ol[4], oh[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float a0, b0, a1, b1;
+    rotate_pair(E::to_f32((uint16_t)(lw[k] & 0xffffu)), E::to_f32((uint16_t)(hw[k] & 0xffffu)), cv[2 * k],
+                sv[2 * k], a0, b0);
+    rotate_pair(E::to_f32((uint16_t)(lw[k] >> 16)), E::to_f32((uint16_t)(hw[k] >> 16)), cv[2 * k + 1],
+                sv[2 * k + 1], a1, b1);
+    ol[k] = (uint32_t)E::from_f32(a0) | ((uint32_t)E::from_f32(a1) << 16);
+    oh[k] = (uint32_t)E::from_f32(b0) | ((uint32_t)E::from_f32(b1) << 16);
+  }
+  *reinterpret_cast<uint4*>(dst + 8 * c) = make_uint4(ol[0], ol[1], ol[2], ol[3]);
+  *reinterpret_cast<uint4*>(dst + half + 8 * c) = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+}
+
 // In-place RoPE (rope.cu:11-42 semantics); grid (tokens, ceil(heads / 4)), wave = one row.
 template <typename T>
 __global__ __launch_bounds__(kCacheThreads) void rope_inplace_kernel(
@@ -201,6 +234,78 @@ __global__ __launch_bounds__(kCacheThreads) void rope_cache_kernel(
   }
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// 16-byte form of rope_cache_kernel for 2-byte elements with head_dim D a multiple of 16
+// (D / 16 divides the workgroup): D / 16 threads per row (8 pairs each), so a workgroup covers
+// kCacheThreads * 16 / D rows of one token; grid (tokens, row groups).  Rows, strides, the
+// cache block stride and cos_sin are 16-byte aligned (checked on the host).
+template <typename T>
+__global__ __launch_bounds__(kCacheThreads) void rope_cache_vec_kernel(RopeRows<uint16_t> io,
+                                                                       uint16_t* __restrict__ k_cache,
+                                                                       uint16_t* __restrict__ v_cache,
+                                                                       const float* __restrict__ cos_sin,
+                                                                       const int32_t* __restrict__ positions,
+                                                                       const int32_t* __restrict__ slot_mapping,
+                                                                       int num_heads, CacheGeom g) {
+  const int D = g.head_dim;
+  const int per_row = D / 16;
+  const int t = blockIdx.x;
+  const int r = blockIdx.y * (kCacheThreads / per_row) + threadIdx.x / per_row;
+  const int c = threadIdx.x % per_row;
+  const int hkv = g.num_kv_heads;
+  const int half = D / 2;
+  if (r >= num_heads + 2 * hkv) return;
+  if (r < num_heads) {
+    const int64_t pos = positions[t];
+    rope_chunk16<T>(io.q_src + t * io.q_src_stride + (int64_t)r * D, io.q_dst + t * io.q_dst_stride + (int64_t)r * D,
+                    cos_sin + pos * D, half, c);
+    return;
+  }
+  const int32_t slot = slot_mapping[t];
+  if (slot < 0) return;  // padding token (paged_attention.cu:127-128)
+  const int64_t blk = slot / g.block_size;
+  const int off = slot % g.block_size;
+  if (r < num_heads + hkv) {
+    const int h = r - num_heads;
+    const int64_t pos = positions[t];
+    rope_chunk16<T>(io.k_src + t * io.k_src_stride + (int64_t)h * D, k_cache + cache_row(g, blk, h, off),
+                    cos_sin + pos * D, half, c);
+  } else {
+    const int h = r - num_heads - hkv;
+    const uint16_t* src = io.v_src + t * io.v_src_stride + (int64_t)h * D;
+    uint16_t* dst = v_cache + cache_row(g, blk, h, off);
+    *reinterpret_cast<uint4*>(dst + 8 * c) = *reinterpret_cast<const uint4*>(src + 8 * c);
+    *reinterpret_cast<uint4*>(dst + half + 8 * c) = *reinterpret_cast<const uint4*>(src + half + 8 * c);
+  }
+}
+
+// 16-byte form of rope_inplace_kernel (same conditions); grid (tokens, row groups).
+template <typename T>
+__global__ __launch_bounds__(kCacheThreads) void rope_inplace_vec_kernel(uint16_t* __restrict__ x,
+                                                                         const float* __restrict__ cos_sin,
+                                                                         const int32_t* __restrict__ positions,
+                                                                         int num_heads, int head_dim) {
+  const int per_row = head_dim / 16;
+  const int t = blockIdx.x;
+  const int h = blockIdx.y * (kCacheThreads / per_row) + threadIdx.x / per_row;
+  if (h >= num_heads) return;
+  const int64_t pos = positions[t];
+  uint16_t* row = x + ((int64_t)t * num_heads + h) * head_dim;
+  rope_chunk16<T>(row, row, cos_sin + pos * head_dim, head_dim / 2, threadIdx.x % per_row);
+}
+
+// Whether the 16-byte RoPE kernels apply (2-byte elements): head_dim a multiple of 16 whose
+// 16-element chunks divide the workgroup, 16-byte aligned pointers and strides.
+bool rope_vec_ok(int d, std::initializer_list<const void*> ptrs, std::initializer_list<int64_t> strides) {
+  if (d % 16 != 0 || kCacheThreads % (d / 16) != 0) return false;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return false;
+  for (int64_t st : strides)
+    if (st % 8 != 0) return false;
+  return true;
+}
+
 // ---------------------------------------------------------------- block copy ----
 
 // Whole-block copies between two pools: grid (pairs, layers, slices).  Pair i copies block
@@ -224,8 +329,6 @@ __global__ __launch_bounds__(kCacheThreads) void copy_blocks_kernel(const uint4*
 }
 
 // ------------------------------------------------------------ host side ----
-
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int check_cache_args(const char* op, const void* k, const void* v, const void* kc,
                      const void* vc, const int32_t* slots, int32_t hkv, int32_t d, int32_t bs,
@@ -284,6 +387,14 @@ int launch_scatter(const char* op, const void* k, const void* v, void* k_cache, 
 template <typename T>
 int launch_rope_inplace(void* x, const float* cs, const int32_t* pos, int h, int d, int n, hipStream_t s) {
   using S = typename elem<T>::storage;
+  if constexpr (sizeof(S) == 2) {
+    if (rope_vec_ok(d, {x, cs}, {(int64_t)d})) {
+      const int rows = kCacheThreads / (d / 16);
+      hipLaunchKernelGGL(rope_inplace_vec_kernel<T>, dim3(n, (h + rows - 1) / rows), dim3(kCacheThreads), 0, s,
+                         static_cast<uint16_t*>(x), cs, pos, h, d);
+      return check_launch("rope");
+    }
+  }
   const dim3 grid(n, (h + kRowsPerGroup - 1) / kRowsPerGroup);
   hipLaunchKernelGGL(rope_inplace_kernel<T>, grid, dim3(kCacheThreads), 0, s, static_cast<S*>(x), cs, pos, h,
                      d);
@@ -296,6 +407,15 @@ int launch_rope_cache(const RopeRows<typename elem<T>::storage>& io, void* kc, v
                       const char* op) {
   using S = typename elem<T>::storage;
   const int rows = h + 2 * g.num_kv_heads;
+  if constexpr (sizeof(S) == 2) {
+    if (rope_vec_ok(g.head_dim, {io.q_src, io.q_dst, io.k_src, io.v_src, kc, vc, cs},
+                    {io.q_src_stride, io.q_dst_stride, io.k_src_stride, io.v_src_stride, g.kv_block_stride})) {
+      const int per_wg = kCacheThreads / (g.head_dim / 16);
+      hipLaunchKernelGGL(rope_cache_vec_kernel<T>, dim3(n, (rows + per_wg - 1) / per_wg), dim3(kCacheThreads), 0, s,
+                         io, static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), cs, pos, slots, h, g);
+      return check_launch(op);
+    }
+  }
   const dim3 grid(n, (rows + kRowsPerGroup - 1) / kRowsPerGroup);
   hipLaunchKernelGGL(rope_cache_kernel<T>, grid, dim3(kCacheThreads), 0, s, io, static_cast<S*>(kc),
                      static_cast<S*>(vc), cs, pos, slots, h, g);

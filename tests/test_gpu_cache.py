@@ -83,7 +83,7 @@ def test_rope_bit_exact(device, kernels, dt, D):
     np.testing.assert_array_equal(from_dev(dx, dt).view(np.uint8), x.view(np.uint8))
 
 
-@pytest.mark.parametrize("which", ["config2", "config4", "small"])
+@pytest.mark.parametrize("which", ["config2", "config4", "small", "small_f16"])
 def test_rope_reshape_and_cache_bit_exact(device, kernels, which):
     """Fused pass == rope(q), rope(k) + scatter, at the decode (T=64) and prefill (T~13k) sizes."""
     if which == "config2":
@@ -96,6 +96,12 @@ def test_rope_reshape_and_cache_bit_exact(device, kernels, which):
         T, H, hkv, D, bs, nb, dt = w.num_tokens, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size, \
             w.num_blocks, "bf16"
         pos, slots = w.positions, w.slot_mapping
+    elif which == "small_f16":  # the 16-byte kernel with D 64, f16, some padding slots
+        T, H, hkv, D, bs, nb, dt = 37, 8, 2, 64, 16, 9, "f16"
+        rng0 = np.random.default_rng(2)
+        pos = rng0.integers(0, 300, size=T).astype(np.int32)
+        slots = _slots(rng0, T, nb, bs)
+        slots[[3, 17]] = -1
     else:
         T, H, hkv, D, bs, nb, dt = 9, 4, 2, 6, 4, 5, "f32"
         rng0 = np.random.default_rng(1)
@@ -103,7 +109,7 @@ def test_rope_reshape_and_cache_bit_exact(device, kernels, which):
         slots = _slots(rng0, T, nb, bs)
     rng = np.random.default_rng(T)
     q, k, v = normal(rng, (T, H, D), dt), normal(rng, (T, hkv, D), dt), normal(rng, (T, hkv, D), dt)
-    if which == "small":
+    if which.startswith("small"):
         kc, vc = normal(rng, (nb, hkv, bs, D), dt), normal(rng, (nb, hkv, bs, D), dt)
     else:  # large pools: zero-filled, so untouched rows are checked against zeros
         kc = np.zeros((nb, hkv, bs, D), orc.NP_STORAGE[dt])
