@@ -661,7 +661,9 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
     cur.kvh = __builtin_amdgcn_readfirstlane(r / cur.nblk);
     cur.b = __builtin_amdgcn_readfirstlane(r - cur.kvh * cur.nblk);
   }
-  auto advance = [&](Cursor& c) {
+  // Every lambda of the kernel is forced inline: one left out of line is called with its
+  // captures in scratch memory (G = 16, and D = 64 with G = 8, spilled that way).
+  auto advance = [&](Cursor& c) __attribute__((always_inline)) {
     if (++c.b == c.nblk) {
       c.b = 0;
       if (++c.kvh == hkv) {
@@ -679,7 +681,7 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   // per-unit address needs a v_readlane instead of a scalar load waited on in the loop.
   int64_t wbase = 0;
   int btw = 0;
-  auto fill_window = [&](const Cursor& c0, int64_t base) {
+  auto fill_window = [&](const Cursor& c0, int64_t base) __attribute__((always_inline)) {
     int ss = c0.s, kh = c0.kvh, b = c0.b + lane, nb = c0.nblk;
     while (b >= nb && ss < a.batch) {
       b -= nb;
@@ -695,7 +697,8 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   };
   // ldi: index of the unit cursor c points at.  A window refill (every 64 units) waits for
   // everything in flight once.
-  auto load_unit = [&](const Cursor& c, int64_t ldi, uint4 (&kk)[NK], uint4 (&vv)[NV], const Tile& t) {
+  auto load_unit = [&](const Cursor& c, int64_t ldi, uint4 (&kk)[NK], uint4 (&vv)[NV], const Tile& t)
+      __attribute__((always_inline)) {
     if (ldi - wbase >= 64) {
       wbase = ldi;
       fill_window(c, ldi);
@@ -709,11 +712,11 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   Tile tile;
   tile.init(lane);
   const int H = a.num_heads;
-  auto begin_segment = [&](const Cursor& c) {
+  auto begin_segment = [&](const Cursor& c) __attribute__((always_inline)) {
     tile.load_q(q_ptr + ((int64_t)c.s * H + (int64_t)c.kvh * G) * D);
     tile.reset();
   };
-  auto end_segment = [&](const Cursor& c) {
+  auto end_segment = [&](const Cursor& c) __attribute__((always_inline)) {
     float lsum[4];
     tile.reduce(lsum);
     const int64_t g = (int64_t)c.s * hkv + c.kvh;
