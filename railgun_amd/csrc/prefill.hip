@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "rg_common.hpp"
 
@@ -541,6 +542,9 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
+  // m_run + kSlack in raw score units (this path runs with scale > 0 only), so that a tile's
+  // test needs no multiply: raw maximum > m_thr  <=>  scaled maximum > m_run + kSlack.
+  float m_thr = -INFINITY;
 
   // The tile loop is software-pipelined: iteration kt turns the scores of tile kt into
   // probabilities while the MFMA unit computes the scores of tile kt+1, then accumulates
@@ -579,7 +583,7 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     return c;
   };
   // Masks keys past each query's position (tiles from kt_mask on, branch-free) and returns
-  // the tile's maximum in the exp2 domain (both halves of the query's keys).
+  // the raw maximum of this lane's half of the query's keys.
   auto mask_max = [&](f32x16_t& c, int kt) {
     if (kt >= kt_mask) {  // wave-uniform: only the tiles around the diagonal hold such keys
       // key 8 (v >> 2) + 4 hh + (v & 3) > my_pos - 32 kt, with the lane's part on the right
@@ -591,21 +595,22 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     float tmax = c[0];
 #pragma unroll
     for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, c[v]);
-    return tmax * a.scale_log2;
+    return tmax;
   };
   // Online softmax with a lazy maximum: m_run only moves when a tile's maximum exceeds it by
   // more than kSlack, so p = 2^(x - m_run) stays below 2^kSlack and the O^T rescale is rare.
   // Each lane checks its own half of the query's keys; only when some lane's half exceeds the
   // slack do the two halves (lanes l and l ^ 32, which must keep the same m_run because the
   // PV product sums over both) exchange their maxima.
-  auto update_max = [&](float tmax_half) {
-    if (__ballot(tmax_half > m_run + kSlack)) {
-      const float other = __int_as_float(__builtin_amdgcn_ds_bpermute(xor32_addr, __float_as_int(tmax_half)));
-      const float tmax = fmaxf(tmax_half, other);
+  auto update_max = [&](float raw_half) {
+    if (__ballot(raw_half > m_thr)) {
+      const float other = __int_as_float(__builtin_amdgcn_ds_bpermute(xor32_addr, __float_as_int(raw_half)));
+      const float tmax = fmaxf(raw_half, other) * a.scale_log2;
       const bool grow = tmax > m_run + kSlack;
       const float m_new = grow ? tmax : m_run;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
+      m_thr = (m_run + kSlack) / a.scale_log2;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -624,13 +629,14 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
       const float p1 = __builtin_amdgcn_exp2f(fmaf(c[v + 1], a.scale_log2, -m_run));
       pk[v / 2] = pack2<T>(p0, p1);
     }
-    float s0 = 0.f, s1 = 0.f;
+    // Two chains, the first one starting from l_run itself.
+    float s0 = pair_sum<T>(pk[0], l_run), s1 = pair_sum<T>(pk[1], 0.f);
 #pragma unroll
-    for (int i = 0; i < 8; i += 2) {
+    for (int i = 2; i < 8; i += 2) {
       s0 = pair_sum<T>(pk[i], s0);
       s1 = pair_sum<T>(pk[i + 1], s1);
     }
-    l_run += s0 + s1;
+    l_run = s0 + s1;
   };
   // O^T += V^T P^T for the tile in stage st, in two 16-key MFMA steps.  The A operand comes
   // from the transposing LDS read: in each 16-lane group, lane 4e+q points at
@@ -711,22 +717,30 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
       }
     }
   }
+  // Tile kt in ring stage SC (a compile-time stage).
+  auto tile_step = [&](int kt, auto sc) __attribute__((always_inline)) {
+    constexpr int S = decltype(sc)::value;
+    wait_for(kt);
+    f32x16_t c = scores(S);
+    // The copies of tile kt + kPStages - 1 go out while the QK MFMAs run.
+    if (kt + kPStages - 1 < nkt) issue_tile(kt + kPStages - 1, S == 0 ? kPStages - 1 : S - 1);
+    uint4 va[kVA];
+    v_prefetch(S, va);
+    update_max(mask_max(c, kt));
+    uint32_t pk[8];
+    probs(c, pk);
+    accumulate(S, pk, va);
+  };
   int kt = 0;
   int st = 0;  // ring stage of tile kt (kt % kPStages, kept as a rotating counter)
   while (kt < nkt) {
   // Iterations whose refill tile kt + kPStages - 1 lies in the current block-table window.
   const int kend = min(nkt, wb + 65 - kPStages);
   for (; kt < kend; ++kt) {
-    wait_for(kt);
-    f32x16_t c = scores(st);
-    // The copies of tile kt + kPStages - 1 go out while the QK MFMAs run.
-    if (kt + kPStages - 1 < nkt) issue_tile(kt + kPStages - 1, st == 0 ? kPStages - 1 : st - 1);
-    uint4 va[kVA];
-    v_prefetch(st, va);
-    update_max(mask_max(c, kt));
-    uint32_t pk[8];
-    probs(c, pk);
-    accumulate(st, pk, va);
+    // One copy of the tile per ring stage, so that each stage's LDS offsets are immediates.
+    [&]<int... S>(std::integer_sequence<int, S...>) {
+      ((st == S ? tile_step(kt, std::integral_constant<int, S>{}) : void()), ...);
+    }(std::make_integer_sequence<int, kPStages>{});
     st = st == kPStages - 1 ? 0 : st + 1;
   }
   if (kt >= nkt) break;
