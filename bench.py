@@ -297,7 +297,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(the decode path shards by sequence or kv-head with no exchange, see DESIGN.md)"}))
+                                   "(across GPUs the decode path would shard by sequence or kv-head with no exchange)"}))
         return 2
     import torch
 
