@@ -536,6 +536,7 @@ struct StreamArgs {
   void* out;
   float* part_acc;   // [num_partials, G, D]
   float* part_ml;    // [num_partials, G, 2]: (m in log2 units, l)
+  int2* seg_desc;    // [batch * H_kv]: (first worker, number of workers) of each segment with units
   float scale_log2;
   int32_t num_heads;
   int32_t num_kv_heads;
@@ -712,9 +713,15 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   Tile tile;
   tile.init(lane);
   const int H = a.num_heads;
-  auto begin_segment = [&](const Cursor& c) __attribute__((always_inline)) {
+  // Segment start at global unit ubeg + c.b.  The worker holding a segment's first block
+  // (b == 0) is the first of the segment's workers: it records them for the merge kernel.
+  auto begin_segment = [&](const Cursor& c, int64_t ubeg) __attribute__((always_inline)) {
     tile.load_q(q_ptr + ((int64_t)c.s * H + (int64_t)c.kvh * G) * D);
     tile.reset();
+    if (c.b == 0 && lane == 0) {
+      const int64_t last = worker_of(ubeg + c.nblk - 1, U, W);
+      a.seg_desc[(int64_t)c.s * hkv + c.kvh] = make_int2((int)k, (int)(last - k + 1));
+    }
   };
   auto end_segment = [&](const Cursor& c) __attribute__((always_inline)) {
     float lsum[4];
@@ -759,7 +766,7 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
     }
   }
   int64_t loaded = min<int64_t>(kSkPrefetch, n);  // units whose loads have been issued
-  begin_segment(cur);
+  begin_segment(cur, u0);
   // Unit j computes from ring slot j % NBUF while the loads of unit j + kSkPrefetch go to
   // slot (j + kSkPrefetch) % NBUF.  Whole rounds of NBUF units run without a bounds test, so the
   // loop has no path that skips a round's loads (such a path makes the compiler drain every
@@ -780,7 +787,7 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
       end_segment(cur);
       if (j + 1 < n) {
         advance(cur);
-        begin_segment(cur);
+        begin_segment(cur, u0 + j + 1);
         ctx_cur = min(context_lens[cur.s], a.max_blocks * kBS);
       }
     } else {
@@ -822,21 +829,10 @@ __global__ __launch_bounds__(64 * G) void decode_stream_merge_kernel(StreamArgs 
     for (int e = 0; e < PER; ++e) out[e] = 0;
     return;
   }
-  // Total units and the segment's first unit (one pass over the context lengths).
-  int64_t U = 0, before = 0;
-  for (int c0 = 0; c0 < a.batch; c0 += 64) {
-    const int ss = c0 + lane;
-    const int64_t n = ss < a.batch ? (int64_t)seq_blocks(context_lens, ss, a.max_blocks) * hkv : 0;
-    const int64_t incl = wave_incl_scan(n, lane);
-    if (c0 <= s && s < c0 + 64) before = U + __shfl(incl - n, s - c0, 64);
-    U += __shfl(incl, 63, 64);
-  }
-  const int64_t ubeg = before + (int64_t)kvh * nblk;
-  const int64_t W = min<int64_t>(a.num_workers, U);
-  const int64_t first = worker_of(ubeg, U, W);
-  const int64_t last = worker_of(ubeg + nblk - 1, U, W);
-  const int64_t pbase = first + (int64_t)s * hkv + kvh;  // partial index of worker `first`
-  const int np = (int)(last - first + 1);
+  // The segment's workers, as the first of them recorded (their partials: first + g .. ).
+  const int2 dsc = a.seg_desc[(int64_t)s * hkv + kvh];
+  const int64_t pbase = (int64_t)dsc.x + (int64_t)s * hkv + kvh;  // partial index of the first worker
+  const int np = dsc.y;
 
   float m = -INFINITY, l = 0.f;
   float acc[PER];
@@ -1119,18 +1115,22 @@ int32_t stream_workers(const Shape& sh) {
 struct StreamScratch {
   float* acc;
   float* ml;
+  int2* desc;
 };
 
 size_t stream_bytes(const Shape& sh, int32_t workers, StreamScratch* carve, void* base) {
   const int64_t G = sh.H / sh.Hkv;
-  const int64_t partials = (int64_t)workers + (int64_t)sh.B * sh.Hkv;
+  const int64_t segments = (int64_t)sh.B * sh.Hkv;
+  const int64_t partials = (int64_t)workers + segments;
   const size_t acc = align_up((size_t)(partials * G * sh.D) * 4, 256);
   const size_t ml = align_up((size_t)(partials * G * 2) * 4, 256);
+  const size_t desc = align_up((size_t)segments * sizeof(int2), 256);
   if (carve) {
     carve->acc = static_cast<float*>(base);
     carve->ml = reinterpret_cast<float*>(static_cast<char*>(base) + acc);
+    carve->desc = reinterpret_cast<int2*>(static_cast<char*>(base) + acc + ml);
   }
-  return acc + ml;
+  return acc + ml + desc;
 }
 
 template <typename T, int D, int G>
@@ -1164,6 +1164,7 @@ int run_stream(const char* op, const DecodeArgs& a, int32_t dtype, const Shape& 
   sa.out = a.out;
   sa.part_acc = sc.acc;
   sa.part_ml = sc.ml;
+  sa.seg_desc = sc.desc;
   sa.scale_log2 = a.scale_log2;
   sa.num_heads = sh.H;
   sa.num_kv_heads = sh.Hkv;
