@@ -285,36 +285,64 @@ struct DecodeTile {
   // kb / vb: the [16, D] rows of one kv-head in one block.
   // Load i of K reads dims 32i .. 32i + 32 of all 16 rows: 64 contiguous bytes per row.
   __device__ __forceinline__ void load(const S* kb, const S* vb, uint4 (&kk)[NK], uint4 (&vv)[NV]) const {
+    load_part<1, 0>(kb, vb, kk, vv);
+  }
+  // The same into entries [B*NK, (B+1)*NK) and [B*NV, (B+1)*NV) of an NB-block ring slot.
+  template <int NB, int B>
+  __device__ __forceinline__ void load_part(const S* kb, const S* vb, uint4 (&kk)[NB * NK], uint4 (&vv)[NB * NV]) const {
     const uint4* kp = reinterpret_cast<const uint4*>(kb + col * D + seg * 8);
 #pragma unroll
-    for (int i = 0; i < NK; ++i) kk[i] = kp[4 * i];
+    for (int i = 0; i < NK; ++i) kk[B * NK + i] = kp[4 * i];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) vv[i] = *reinterpret_cast<const uint4*>(vb + (i * TPI + vrow) * D + vd0);
+    for (int i = 0; i < NV; ++i) vv[B * NV + i] = *reinterpret_cast<const uint4*>(vb + (i * TPI + vrow) * D + vd0);
   }
-  // One block whose first token has context index tok0 (tokens >= ctx are masked).
-  __device__ __forceinline__ void step(const uint4 (&kr)[NK], const uint4 (&vr)[NV], int tok0, int ctx,
+  // NB consecutive blocks of one kv-head (kr / vr: block b in entries [b*NK, (b+1)*NK) and
+  // [b*NV, (b+1)*NV)) whose first token has context index tok0; tokens >= ctx are masked.  One
+  // running-max update, rescale decision and LDS exchange serve all NB * 16 tokens.
+  // p_lds holds NB * 16 rows of GP probabilities.
+  template <int NB = 1>
+  __device__ __forceinline__ void step(const uint4 (&kr)[NB * NK], const uint4 (&vr)[NB * NV], int tok0, int ctx,
                                        float scale_log2, float* p_lds, float* alpha_lds) {
-    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t c[NB];
 #pragma unroll
-    for (int i = 0; i < NK; ++i) c = MF::run(qa[i], kr[i], c);
-    const bool tail = tok0 + kBS > ctx;
-    const bool valid = tok0 + col < ctx;
-    float pr[4], al[4];
+    for (int b = 0; b < NB; ++b) {
+      c[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < NK; ++i) c[b] = MF::run(qa[i], kr[b * NK + i], c[b]);
+    }
+    const bool tail = tok0 + NB * kBS > ctx;
+    float x[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const bool valid = tok0 + b * kBS + col < ctx;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[b][r] = valid ? c[b][r] * scale_log2 : -INFINITY;
+    }
+    float pr[NB][4], al[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float x = valid ? c[r] * scale_log2 : -INFINITY;
-      const float bm = row16_max(x);
+      float mx = x[0][r];
+#pragma unroll
+      for (int b = 1; b < NB; ++b) mx = fmaxf(mx, x[b][r]);
+      const float bm = row16_max(mx);
       const float m_new = fmaxf(m_run[r], bm);
       al[r] = fast_exp2(m_run[r] - m_new);
-      pr[r] = fast_exp2(x - m_new);
-      l_run[r] = l_run[r] * al[r] + pr[r];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) pr[b][r] = fast_exp2(x[b][r] - m_new);
+      float ps = pr[0][r];
+#pragma unroll
+      for (int b = 1; b < NB; ++b) ps += pr[b][r];
+      l_run[r] = l_run[r] * al[r] + ps;
       m_run[r] = m_new;
     }
     // The running max of a head moves on few blocks only: skip the rescale of acc when it
     // moved for no head (a wave-uniform decision).
     const bool rescale = __ballot(al[0] != 1.f || al[1] != 1.f || al[2] != 1.f || al[3] != 1.f) != 0;
     if (seg < HG) {
-      *reinterpret_cast<float4*>(&p_lds[col * GP + 4 * seg]) = make_float4(pr[0], pr[1], pr[2], pr[3]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+        *reinterpret_cast<float4*>(&p_lds[(b * kBS + col) * GP + 4 * seg]) =
+            make_float4(pr[b][0], pr[b][1], pr[b][2], pr[b][3]);
       if (col == 0) *reinterpret_cast<float4*>(&alpha_lds[4 * seg]) = make_float4(al[0], al[1], al[2], al[3]);
     }
     wave_lds_sync();
@@ -327,13 +355,14 @@ struct DecodeTile {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] *= alh[h];
     }
-    float vf[NV][8];
+    // V load i covers tokens i * TPI .. + TPI of the NB * 16 (NV * TPI = 16 per block).
+    float vf[NB * NV][8];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) MF::unpack8(vr[i], vf[i]);
+    for (int i = 0; i < NB * NV; ++i) MF::unpack8(vr[i], vf[i]);
     if (tail) {
       // Rows past the context may hold any bit pattern; keep them out of 0*x.
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
+      for (int i = 0; i < NB * NV; ++i) {
         if (tok0 + i * TPI + vrow >= ctx) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) vf[i][e] = 0.f;
@@ -341,7 +370,7 @@ struct DecodeTile {
       }
     }
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
+    for (int i = 0; i < NB * NV; ++i) {
       const int t = i * TPI + vrow;
       float ph[G];
 #pragma unroll
@@ -522,8 +551,17 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 #ifndef RG_SK_PREFETCH_D64
 #define RG_SK_PREFETCH_D64 4
 #endif
+// Blocks per stream-K unit.  At head_dim 64 a block of one kv-head is 2 KB of K + 2 KB of V;
+// two of them per unit give the same 8 KB per unit as head_dim 128, so the per-unit fixed
+// work (running-max reductions, rescale decision, LDS exchange, cursor) is spread over the
+// same bytes.
+#ifndef RG_SK_BPU_D64
+#define RG_SK_BPU_D64 2
+#endif
 template <int D>
-constexpr int sk_prefetch() { return D <= 64 ? RG_SK_PREFETCH_D64 : RG_SK_PREFETCH; }
+constexpr int sk_bpu() { return D <= 64 ? RG_SK_BPU_D64 : 1; }
+template <int D>
+constexpr int sk_prefetch() { return D <= 64 && sk_bpu<D>() == 1 ? RG_SK_PREFETCH_D64 : RG_SK_PREFETCH; }
 
 // Optional occupancy floor of the stream-K kernel (waves per SIMD).
 #if defined(RG_SK_OCC) && RG_SK_OCC > 0
@@ -550,10 +588,15 @@ __device__ __forceinline__ int64_t worker_start(int64_t k, int64_t U, int64_t W)
 // The worker whose range contains unit u (the last k with worker_start(k) <= u).
 __device__ __forceinline__ int64_t worker_of(int64_t u, int64_t U, int64_t W) { return ((u + 1) * W - 1) / U; }
 
-// Units of sequence s: ceil(ctx/16) blocks per kv-head (context clamped to the table row).
+// Blocks of sequence s: ceil(ctx/16) per kv-head (context clamped to the table row).
 __device__ __forceinline__ int seq_blocks(const int32_t* ctxl, int s, int max_blocks) {
   const int c = max(0, min(ctxl[s], max_blocks * kBS));
   return (c + kBS - 1) / kBS;
+}
+// Stream-K units of sequence s per kv-head: its blocks in runs of BPU (the last run may be short).
+template <int BPU>
+__device__ __forceinline__ int seq_units(const int32_t* ctxl, int s, int max_blocks) {
+  return (seq_blocks(ctxl, s, max_blocks) + BPU - 1) / BPU;
 }
 
 // A wave-uniform 64-bit value made visibly uniform to the compiler.
@@ -575,6 +618,7 @@ __device__ __forceinline__ int64_t wave_incl_scan(int64_t v, int lane) {
 
 // Total units U and, if `target` >= 0, the sequence containing unit `target` and the first
 // unit of that sequence.  Every lane returns the same values.
+template <int BPU>
 __device__ __forceinline__ int64_t scan_units(const int32_t* ctxl, int batch, int max_blocks, int hkv,
                                               int lane, int64_t target, int& seq_out, int64_t& seq_start) {
   int64_t base = 0;
@@ -582,7 +626,7 @@ __device__ __forceinline__ int64_t scan_units(const int32_t* ctxl, int batch, in
   seq_start = 0;
   for (int c0 = 0; c0 < batch; c0 += 64) {
     const int s = c0 + lane;
-    const int64_t n = s < batch ? (int64_t)seq_blocks(ctxl, s, max_blocks) * hkv : 0;
+    const int64_t n = s < batch ? (int64_t)seq_units<BPU>(ctxl, s, max_blocks) * hkv : 0;
     const int64_t incl = wave_incl_scan(n, lane) + base;
     const int64_t excl = incl - n;
     if (target >= 0 && seq_out < 0) {
@@ -610,7 +654,8 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   constexpr int NV = Tile::NV;
   constexpr int kSkPrefetch = sk_prefetch<D>();
   constexpr int NBUF = kSkPrefetch + 1;
-  __shared__ float p_lds[2][kBS * GP];
+  constexpr int BPU = sk_bpu<D>();
+  __shared__ float p_lds[2][BPU * kBS * GP];
   __shared__ float alpha_lds[2][GP];
 
   const int lane = threadIdx.x;
@@ -621,7 +666,7 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   int64_t U, W, u0, u1, seq_start;
   int s;
   if (a.batch <= 64) {
-    const int64_t n = lane < a.batch ? (int64_t)seq_blocks(context_lens, lane, a.max_blocks) * hkv : 0;
+    const int64_t n = lane < a.batch ? (int64_t)seq_units<BPU>(context_lens, lane, a.max_blocks) * hkv : 0;
     const int64_t incl = wave_incl_scan(n, lane);
     const int64_t excl = incl - n;
     U = uniform64(__shfl(incl, 63, 64));
@@ -637,17 +682,18 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   } else {
     int s_dummy;
     int64_t st_dummy;
-    U = uniform64(scan_units(context_lens, a.batch, a.max_blocks, hkv, lane, -1, s_dummy, st_dummy));
+    U = uniform64(scan_units<BPU>(context_lens, a.batch, a.max_blocks, hkv, lane, -1, s_dummy, st_dummy));
     W = min<int64_t>(a.num_workers, U);
     if (k >= W) return;
     u0 = worker_start(k, U, W);
     u1 = worker_start(k + 1, U, W);
-    scan_units(context_lens, a.batch, a.max_blocks, hkv, lane, u0, s, seq_start);
+    scan_units<BPU>(context_lens, a.batch, a.max_blocks, hkv, lane, u0, s, seq_start);
     s = __builtin_amdgcn_readfirstlane(s);
     seq_start = uniform64(seq_start);
   }
 
-  // Cursor of the unit being computed (cs, ckvh, cb) and of the unit being loaded.
+  // Cursor of the unit being computed and of the unit being loaded: sequence, kv-head, unit b
+  // of the segment's nblk units (blocks b * BPU .. b * BPU + BPU - 1).
   struct Cursor {
     int s, kvh, b, nblk;
   };
@@ -656,7 +702,7 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   // load instead of a vector load whose wait would also drain the K/V prefetches.
   Cursor cur;
   cur.s = s;
-  cur.nblk = __builtin_amdgcn_readfirstlane(seq_blocks(context_lens, s, a.max_blocks));
+  cur.nblk = __builtin_amdgcn_readfirstlane(seq_units<BPU>(context_lens, s, a.max_blocks));
   {
     const int r = __builtin_amdgcn_readfirstlane((int)(u0 - seq_start));
     cur.kvh = __builtin_amdgcn_readfirstlane(r / cur.nblk);
@@ -671,17 +717,19 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
         c.kvh = 0;
         do {
           ++c.s;
-          c.nblk = c.s < a.batch ? seq_blocks(context_lens, c.s, a.max_blocks) : 1;
+          c.nblk = c.s < a.batch ? seq_units<BPU>(context_lens, c.s, a.max_blocks) : 1;
         } while (c.nblk == 0);
       }
     }
   };
-  // Block numbers of the worker's units in a register window: lane i holds the block of
-  // unit wbase + i (units counted from u0).  Filling it walks each lane's cursor i units on
-  // (a few steps: ranges cross few segments) and reads all 64 entries with one load, so the
-  // per-unit address needs a v_readlane instead of a scalar load waited on in the loop.
+  // Block numbers of the worker's units in a register window: lane i holds the blocks of
+  // unit wbase + i (units counted from u0; btw[r] is block r of the unit, and a short last
+  // unit repeats its first block, which the step masks).  Filling it walks each lane's cursor
+  // i units on (a few steps: ranges cross few segments) and reads all 64 units' entries with
+  // BPU loads, so the per-unit address needs a v_readlane instead of a scalar load waited on
+  // in the loop.
   int64_t wbase = 0;
-  int btw = 0;
+  int btw[BPU];
   auto fill_window = [&](const Cursor& c0, int64_t base) __attribute__((always_inline)) {
     int ss = c0.s, kh = c0.kvh, b = c0.b + lane, nb = c0.nblk;
     while (b >= nb && ss < a.batch) {
@@ -690,24 +738,34 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
         kh = 0;
         do {
           ++ss;
-          nb = ss < a.batch ? seq_blocks(context_lens, ss, a.max_blocks) : 1;
+          nb = ss < a.batch ? seq_units<BPU>(context_lens, ss, a.max_blocks) : 1;
         } while (nb == 0);
       }
     }
-    btw = base + lane < u1 - u0 && ss < a.batch ? block_table[(int64_t)ss * a.max_blocks + b] : 0;
+    const bool live = base + lane < u1 - u0 && ss < a.batch;
+    const int32_t* row = block_table + (int64_t)(live ? ss : 0) * a.max_blocks;
+    const int nbk = live ? seq_blocks(context_lens, ss, a.max_blocks) : 0;
+#pragma unroll
+    for (int r = 0; r < BPU; ++r) {
+      const int bk = b * BPU + r < nbk ? b * BPU + r : b * BPU;
+      btw[r] = live ? row[bk] : 0;
+    }
   };
   // ldi: index of the unit cursor c points at.  A window refill (every 64 units) waits for
   // everything in flight once.
-  auto load_unit = [&](const Cursor& c, int64_t ldi, uint4 (&kk)[NK], uint4 (&vv)[NV], const Tile& t)
+  auto load_unit = [&](const Cursor& c, int64_t ldi, uint4 (&kk)[BPU * NK], uint4 (&vv)[BPU * NV], const Tile& t)
       __attribute__((always_inline)) {
     if (ldi - wbase >= 64) {
       wbase = ldi;
       fill_window(c, ldi);
       __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
     }
-    const int e = __builtin_amdgcn_readlane(btw, (int)(ldi - wbase));
-    const int64_t off = (int64_t)e * a.kv_stride + (int64_t)c.kvh * kBS * D;
-    t.load(kc + off, vc + off, kk, vv);
+    const int64_t head = (int64_t)c.kvh * kBS * D;
+    [&]<int... R>(std::integer_sequence<int, R...>) __attribute__((always_inline)) {
+      ((t.template load_part<BPU, R>(kc + (int64_t)__builtin_amdgcn_readlane(btw[R], (int)(ldi - wbase)) * a.kv_stride + head,
+                                     vc + (int64_t)__builtin_amdgcn_readlane(btw[R], (int)(ldi - wbase)) * a.kv_stride + head,
+                                     kk, vv)), ...);
+    }(std::make_integer_sequence<int, BPU>{});
   };
 
   Tile tile;
@@ -755,7 +813,7 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   int64_t ldi = 0;
   int ctx_cur = min(context_lens[cur.s], a.max_blocks * kBS);
   fill_window(cur, 0);
-  uint4 kbuf[NBUF][NK], vbuf[NBUF][NV];
+  uint4 kbuf[NBUF][BPU * NK], vbuf[NBUF][BPU * NV];
   // Prologue: the first kSkPrefetch units (the last one repeated past the end of the range).
 #pragma unroll
   for (int q = 0; q < kSkPrefetch; ++q) {
@@ -781,7 +839,8 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
         ++ldi;
       }
     }
-    tile.step(kbuf[q], vbuf[q], cur.b * kBS, ctx_cur, a.scale_log2, p_lds[j & 1], alpha_lds[j & 1]);
+    tile.template step<BPU>(kbuf[q], vbuf[q], cur.b * BPU * kBS, ctx_cur, a.scale_log2, p_lds[j & 1],
+                            alpha_lds[j & 1]);
     const bool last_of_segment = cur.b + 1 == cur.nblk || j + 1 == n;
     if (last_of_segment) {
       end_segment(cur);

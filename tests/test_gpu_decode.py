@@ -113,6 +113,18 @@ def test_mfma_path_shapes(device, kernels, dt, D, G):
     assert_close(gpu_v2(kernels, inp, 32), want, dt, "v2 P=32")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_stream_odd_blocks_full_row(device, kernels, D):
+    """Stream-K units of two blocks (head_dim 64): sequences whose odd block count fills the
+    whole block-table row (19 blocks, max_blocks 19), so a segment's last unit has one block
+    and no table entry after it; fused pool layout, 132 sequences (the two-pass unit scan)
+    and more units than workers."""
+    ctx = [300, 289, 33, 300, 17, 300] * 22
+    inp = make_inputs(device, ctx, "bf16", H=8, Hkv=2, D=D, seed=70 + D, fused=True, mb=19)
+    assert inp["mb"] == 19 and max((c + 15) // 16 for c in ctx) == 19
+    assert_close(gpu_v1(kernels, inp, True), oracle_v1_plus(inp), "bf16", "ws=True")
+
+
 def test_workspace_reused_across_calls(device, kernels):
     """One workspace serves calls of different shapes (GQA 4 and 8, head_dim 128 and 64, empty
     and long sequences) and a v2 call that falls back to partition + reduce on its front part:
