@@ -546,22 +546,25 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 #ifndef RG_SK_PREFETCH
 #define RG_SK_PREFETCH 3
 #endif
-// head_dim 64 halves a unit's bytes (2 KB of K + 2 KB of V), so twice as many units stay in
-// flight for the same bytes per wave.
-#ifndef RG_SK_PREFETCH_D64
-#define RG_SK_PREFETCH_D64 4
+#ifndef RG_SK_BPU_D128
+#define RG_SK_BPU_D128 1
 #endif
-// Blocks per stream-K unit.  At head_dim 64 a block of one kv-head is 2 KB of K + 2 KB of V;
-// two of them per unit give the same 8 KB per unit as head_dim 128, so the per-unit fixed
-// work (running-max reductions, rescale decision, LDS exchange, cursor) is spread over the
-// same bytes.
+// Blocks per stream-K unit and prefetch depth at head_dim 64.  A block of one kv-head is
+// 2 KB of K + 2 KB of V there, while the per-unit fixed work (running-max reductions,
+// rescale decision, LDS exchange, cursor) is the same as at head_dim 128.  Units of four
+// blocks (16 KB) with two of them in flight measured fastest: 206.6 us per layer at the
+// Llama-3.2-1B step against 216.6 us for two-block units three deep and 236.5 us for
+// one-block units four deep (2 x 4, 2 x 5 and 3 x 3 were in between).
 #ifndef RG_SK_BPU_D64
-#define RG_SK_BPU_D64 2
+#define RG_SK_BPU_D64 4
+#endif
+#ifndef RG_SK_PREFETCH_D64
+#define RG_SK_PREFETCH_D64 2
 #endif
 template <int D>
-constexpr int sk_bpu() { return D <= 64 ? RG_SK_BPU_D64 : 1; }
+constexpr int sk_bpu() { return D <= 64 ? RG_SK_BPU_D64 : RG_SK_BPU_D128; }
 template <int D>
-constexpr int sk_prefetch() { return D <= 64 && sk_bpu<D>() == 1 ? RG_SK_PREFETCH_D64 : RG_SK_PREFETCH; }
+constexpr int sk_prefetch() { return D <= 64 ? RG_SK_PREFETCH_D64 : RG_SK_PREFETCH; }
 
 // Optional occupancy floor of the stream-K kernel (waves per SIMD).
 #if defined(RG_SK_OCC) && RG_SK_OCC > 0

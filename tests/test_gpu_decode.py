@@ -115,10 +115,10 @@ def test_mfma_path_shapes(device, kernels, dt, D, G):
 
 @pytest.mark.parametrize("D", [64, 128])
 def test_stream_odd_blocks_full_row(device, kernels, D):
-    """Stream-K units of two blocks (head_dim 64): sequences whose odd block count fills the
-    whole block-table row (19 blocks, max_blocks 19), so a segment's last unit has one block
-    and no table entry after it; fused pool layout, 132 sequences (the two-pass unit scan)
-    and more units than workers."""
+    """Stream-K units of several blocks (head_dim 64): sequences whose block count is no
+    multiple of the unit fill the whole block-table row (19 blocks, max_blocks 19), so a
+    segment's last unit is short and has no table entry after it; fused pool layout, 132
+    sequences (the two-pass unit scan) and more units than workers."""
     ctx = [300, 289, 33, 300, 17, 300] * 22
     inp = make_inputs(device, ctx, "bf16", H=8, Hkv=2, D=D, seed=70 + D, fused=True, mb=19)
     assert inp["mb"] == 19 and max((c + 15) // 16 for c in ctx) == 19
