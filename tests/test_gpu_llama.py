@@ -34,7 +34,7 @@ def _bf16_round(x: torch.Tensor) -> torch.Tensor:
     return x.to(torch.bfloat16).float()
 
 
-@pytest.mark.parametrize("hidden", [2048, 120, 100])
+@pytest.mark.parametrize("hidden", [2048, 6144, 8200, 120, 100])  # 16-byte rows of 1-5 vectors per thread, a short row, scalar form
 def test_rms_norm_residual(device, hidden):
     g = torch.Generator().manual_seed(hidden)
     rows = 37
@@ -57,7 +57,7 @@ def test_rms_norm_residual(device, hidden):
     torch.testing.assert_close(out2.cpu().float(), want2, atol=0, rtol=2 ** -7)
 
 
-@pytest.mark.parametrize("inter", [8192, 300])
+@pytest.mark.parametrize("inter", [8192, 200, 300])  # full and partial workgroups per row
 def test_silu_and_mul(device, inter):
     g = torch.Generator().manual_seed(inter)
     gu = (3 * torch.randn(9, 2 * inter, generator=g)).to(torch.bfloat16)
