@@ -529,10 +529,11 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 
 // ------------------------------------------------------------- stream-K -----
 //
-// The decode work is the list of units (sequence s, kv-head, block b) ordered with b
-// fastest; segment g = s * num_kv_heads + kvh is the run of units of one (s, kv-head).
+// The decode work is the list of units (sequence s, kv-head, b) ordered with b fastest,
+// unit b covering blocks [b * BPU, b * BPU + BPU) of the sequence (sk_bpu: 1 at head_dim 128,
+// 4 at head_dim 64); segment g = s * num_kv_heads + kvh is the run of units of one (s, kv-head).
 // Worker k (one wave) takes units [k*U/W, (k+1)*U/W) of the U units, so every wave streams
-// the same number of KV blocks whatever the context lengths are.  A worker emits one partial
+// the same number of units whatever the context lengths are.  A worker emits one partial
 // (m, l, acc) for every segment it touches, at partial index k + g (distinct for all
 // (worker, segment) pairs because each worker's segments and each segment's workers are
 // consecutive).  decode_stream_merge_kernel combines the partials of each segment.  When
@@ -868,8 +869,8 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
 }
 
 // One workgroup per segment (sequence, kv-head), one wave per head of the group: merges the
-// partials of workers worker_of(first unit) .. worker_of(last unit) of the segment and writes
-// the G output rows.  Lane l of wave h holds dims [l*D/64, (l+1)*D/64) of head h, so each
+// partials of the segment's workers (the range its first worker recorded in seg_desc) and
+// writes the G output rows.  Lane l of wave h holds dims [l*D/64, (l+1)*D/64) of head h, so each
 // partial's [G, D] accumulator is read as one contiguous row by the whole workgroup; every
 // lane folds the partials in order with an online rescale (loads of consecutive partials
 // are independent, so they are issued ahead of the folds).
