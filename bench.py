@@ -9,7 +9,7 @@ kernels), timed with HIP events on the stream it is launched on.  Side figures: 
 (v2 split-K, 8 x 32k) and config 4 (packed causal prefill, bf16 MFMA roofline).
 
 ``cpu_baseline`` times the restated reference CPU path (gather -> q.K^T*scale -> softmax -> .V,
-oracle/oracle.c) on host cores over a bounded sample of the same workload.
+oracle/oracle.c) on every host core this process may use, over the whole config-2 batch.
 """
 from __future__ import annotations
 
@@ -116,44 +116,69 @@ def rope_cache_call(w, st):
                                     st["slots"])
 
 
+def host_cores() -> tuple[int, str]:
+    """Cores this process may run on: its CPU affinity, bounded by a cgroup CPU quota when one
+    is set (cpu.max); and a description of both."""
+    n = len(os.sched_getaffinity(0))
+    note = f"{n} in the CPU affinity"
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            q = max(1, math.ceil(int(quota) / int(period)))
+            note += f", cgroup quota {q}"
+            n = min(n, q)
+    except (OSError, ValueError):
+        pass
+    return n, note
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(w, seconds_target: float = 10.0) -> dict:
-    """The restated reference CPU path on a bounded sample of config 2 (first n sequences)."""
+    """The restated reference CPU path (gather -> q.K^T*scale -> softmax -> .V, fp32, threaded
+    over (sequence, kv-head)) on the whole config-2 batch: its 64 sequences, context lengths and
+    block tables, over a pool of the same size (N(0, 1), bf16)."""
     import numpy as np
 
     from oracle import oracle as orc
 
-    import dataclasses
-
-    from railgun_amd import workloads as wl
-
-    cores = min(os.cpu_count() or 1, 16)
+    cores, core_note = host_cores()
     rng = np.random.default_rng(7)
-    n = 8
-    sub_ctx = w.context_lens[:n]
-    need = int(((sub_ctx.astype(np.int64) + w.block_size - 1) // w.block_size).sum())
-    bt = wl.assign_blocks(sub_ctx, w.block_size, need, w.max_blocks, rng)
-    shape = (need, w.num_kv_heads, w.block_size, w.head_dim)
+    shape = (w.num_blocks, w.num_kv_heads, w.block_size, w.head_dim)
     kc = orc.bf16_round(rng.standard_normal(size=shape, dtype=np.float32))
     vc = orc.bf16_round(rng.standard_normal(size=shape, dtype=np.float32))
-    q = orc.bf16_round(rng.standard_normal(size=(n, w.num_heads, w.head_dim), dtype=np.float32))
-    sub = dataclasses.replace(w, num_blocks=need, context_lens=sub_ctx, block_table=bt)
-    t0 = time.perf_counter()
-    orc.cpu_attention_gathered(q, kc, vc, bt, sub_ctx, w.scale, "bf16", nthreads=cores)
-    one = time.perf_counter() - t0
-    reps = max(1, min(20, int(seconds_target / max(one, 1e-3))))
-    times = []
-    for _ in range(reps):
+    q = orc.bf16_round(rng.standard_normal(size=(w.batch, w.num_heads, w.head_dim), dtype=np.float32))
+
+    def run() -> float:
         t0 = time.perf_counter()
-        orc.cpu_attention_gathered(q, kc, vc, bt, sub_ctx, w.scale, "bf16", nthreads=cores)
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
-    return {"value": round(sub.decode_bytes() / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"first {n} of the 64 config-2 sequences ({int(sub_ctx.sum())} context tokens, 32/8 heads, "
-                      f"D 128, bf16 upcast to fp32), median of {reps} runs after a warm-up, "
-                      f"{sub.decode_bytes() / 1e6:.1f} MB algorithmic bytes per run"}
+        orc.cpu_attention_gathered(q, kc, vc, w.block_table, w.context_lens, w.scale, "bf16", nthreads=cores)
+        return time.perf_counter() - t0
+
+    one = run()  # warm-up
+    reps = max(10, min(100, int(seconds_target / max(one, 1e-3))))
+    times = sorted(run() for _ in range(reps))
+    med = times[len(times) // 2]
+    return {"value": round(w.decode_bytes() / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "cpu": cpu_model(),
+            "sample": f"the whole config-2 batch ({w.batch} sequences, {int(w.context_lens.sum())} context tokens, "
+                      f"32/8 heads, D 128, bf16 upcast to fp32), {w.decode_bytes() / 1e6:.1f} MB algorithmic bytes "
+                      f"per run, median of {reps} runs after a warm-up, {cores} threads ({core_note})",
+            "ms_per_run": round(med * 1e3, 2)}
 
 
 def side_v2(device, gen, steps: int) -> dict:
+    """Config 3 (8 x 32768, P = 512): the combined v2 entry with its full scratch, which runs the
+    stream-K form (balanced split-K over all waves), and the reference's own launcher pair,
+    rg_paged_attention_v2_partition over NP = 64 partitions + rg_paged_attention_v2_reduce
+    (paged_attn_op.rs:108-158), timed on the same inputs."""
     import torch
 
     from railgun_amd import workloads as wl
@@ -170,13 +195,29 @@ def side_v2(device, gen, steps: int) -> dict:
                                 w.num_kv_heads, w.head_dim, w.block_size, w.max_blocks, w.batch,
                                 int(w.context_lens.max()), P, ws)
 
+    tmp = torch.empty((w.batch, w.num_heads, np_, w.head_dim), dtype=torch.float32, device=device)
+    es = torch.empty((w.batch, w.num_heads, np_), dtype=torch.float32, device=device)
+    ml = torch.empty_like(es)
+
+    def pair():
+        k = st["kernels"]
+        k.launch_v2_partition(st["q"], st["kc"], st["vc"], st["bt"], st["ctx"], tmp, es, ml, None, w.scale,
+                              w.num_heads, w.num_kv_heads, w.head_dim, w.block_size, w.max_blocks, np_, w.batch, P)
+        k.launch_v2_reduce(st["out"], es, ml, tmp, st["ctx"], None, w.num_heads, w.head_dim, np_, w.batch, P)
+
     ms = time_events(call, steps, 3)
+    ms_pair = time_events(pair, steps, 3)
     gbs = w.decode_bytes() / (ms * 1e-3) / 1e9
-    del st, ws
+    gbs_pair = w.decode_bytes() / (ms_pair * 1e-3) / 1e9
+    del st, ws, tmp, es, ml
     torch.cuda.empty_cache()
-    return {"workload": w.name, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": w.decode_bytes(),
-            "traffic": measured_traffic("paged_attention_v2_config3")}
+    return {"workload": w.name, "kernel": "rg_paged_attention_v2 (stream-K split over all waves + merge)",
+            "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes": w.decode_bytes(), "traffic": measured_traffic("paged_attention_v2_config3"),
+            "reference_pair": {"kernel": f"rg_paged_attention_v2_partition (P {P}, NP {np_}) + "
+                                         "rg_paged_attention_v2_reduce",
+                               "us": round(ms_pair * 1e3, 2), "GB/s": round(gbs_pair, 1),
+                               "frac_hbm_peak": round(gbs_pair / HBM_PEAK_GBS, 4)}}
 
 
 def side_prefill(device, gen, steps: int) -> dict:

@@ -370,53 +370,115 @@ void or_paged_attention_v2_reduce(float* out, const float* exp_sums, const float
  * kernel; crates/vllm-models/src/llama/attention.rs:128-132 routes prefill
  * through the decode op).  Row j of sequence s (rows cu[s]..cu[s+1]) sits at
  * position ctx[s] - L_s + j and attends to cache positions 0..pos with
- * softmax(scale * q.K) V, computed in double.  GQA kvh = h / (H/H_kv). */
+ * softmax(scale * q.K) V, computed in double.  GQA kvh = h / (H/H_kv).
+ *
+ * prefill_row computes every head of one packed row; sc holds pos + 1 doubles
+ * and acc D doubles. */
+static void prefill_row(const dec_args* a, const int32_t* cu, float* out, int s, int row,
+                        double* sc, double* acc) {
+  const int L = cu[s + 1] - cu[s];
+  const int pos = a->ctx[s] - L + (row - cu[s]);
+  const int H = a->H, D = a->D;
+  for (int h = 0; h < H; ++h) {
+    float* o = out + ((int64_t)row * H + h) * D;
+    if (pos < 0) {
+      memset(o, 0, sizeof(float) * D);
+      continue;
+    }
+    const int kvh = h / (H / a->Hkv);
+    double mx = -INFINITY;
+    for (int t = 0; t <= pos; ++t) {
+      const int64_t r = token_row(a, s, kvh, t);
+      double dot = 0.0;
+      for (int d = 0; d < D; ++d)
+        dot += (double)ld(a->q, ((int64_t)row * H + h) * D + d, a->dt) * (double)ld(a->kc, r + d, a->dt);
+      sc[t] = dot * (double)a->scale;
+      if (sc[t] > mx) mx = sc[t];
+    }
+    double sum = 0.0;
+    for (int d = 0; d < D; ++d) acc[d] = 0.0;
+    for (int t = 0; t <= pos; ++t) {
+      const double e = exp(sc[t] - mx);
+      sum += e;
+      const int64_t r = token_row(a, s, kvh, t);
+      for (int d = 0; d < D; ++d) acc[d] += e * (double)ld(a->vc, r + d, a->dt);
+    }
+    for (int d = 0; d < D; ++d) o[d] = (float)(acc[d] / sum);
+  }
+}
+
+static int max_ctx_of(const int32_t* ctx, int S) {
+  int m = 1;
+  for (int s = 0; s < S; ++s)
+    if (ctx[s] > m) m = ctx[s];
+  return m;
+}
+
 void or_prefill_packed(const void* q, const void* kc, const void* vc, const int32_t* bt,
                        const int32_t* ctx, const int32_t* cu, float* out, float scale, int S,
                        int H, int Hkv, int D, int bs, int MB, int dt, int64_t stride) {
   dec_args a = {q, kc, vc, bt, ctx, scale, S, H, Hkv, D, bs, MB, dt, stride};
-  double* sc = NULL;
+  double* sc = (double*)malloc(sizeof(double) * (size_t)max_ctx_of(ctx, S));
   double* acc = (double*)malloc(sizeof(double) * D);
-  int sc_cap = 0;
-  for (int s = 0; s < S; ++s) {
-    const int L = cu[s + 1] - cu[s];
-    for (int j = 0; j < L; ++j) {
-      const int row = cu[s] + j;
-      const int pos = ctx[s] - L + j;
-      for (int h = 0; h < H; ++h) {
-        float* o = out + ((int64_t)row * H + h) * D;
-        if (pos < 0) {
-          memset(o, 0, sizeof(float) * D);
-          continue;
-        }
-        const int kvh = h / (H / Hkv);
-        if (pos + 1 > sc_cap) {
-          sc_cap = pos + 1;
-          sc = (double*)realloc(sc, sizeof(double) * sc_cap);
-        }
-        double mx = -INFINITY;
-        for (int t = 0; t <= pos; ++t) {
-          const int64_t r = token_row(&a, s, kvh, t);
-          double dot = 0.0;
-          for (int d = 0; d < D; ++d)
-            dot += (double)ld(q, ((int64_t)row * H + h) * D + d, dt) * (double)ld(kc, r + d, dt);
-          sc[t] = dot * (double)scale;
-          if (sc[t] > mx) mx = sc[t];
-        }
-        double sum = 0.0;
-        for (int d = 0; d < D; ++d) acc[d] = 0.0;
-        for (int t = 0; t <= pos; ++t) {
-          const double e = exp(sc[t] - mx);
-          sum += e;
-          const int64_t r = token_row(&a, s, kvh, t);
-          for (int d = 0; d < D; ++d) acc[d] += e * (double)ld(vc, r + d, dt);
-        }
-        for (int d = 0; d < D; ++d) o[d] = (float)(acc[d] / sum);
-      }
-    }
+  for (int s = 0; s < S; ++s)
+    for (int row = cu[s]; row < cu[s + 1]; ++row) prefill_row(&a, cu, out, s, row, sc, acc);
+  free(sc);
+  free(acc);
+}
+
+/* The same rows as or_prefill_packed, for a list of packed row indices only
+ * (rows[i] in [0, cu[S])), spread over `nthreads` POSIX threads: every listed
+ * row of `out` is written exactly as or_prefill_packed writes it, the others
+ * are left untouched.  For long streams where every row would take minutes. */
+typedef struct {
+  const dec_args* a;
+  const int32_t* cu;
+  const int32_t* rows;
+  float* out;
+  int nrows;
+  int next;
+  pthread_mutex_t mu;
+} prefill_job;
+
+static void* prefill_worker(void* arg) {
+  prefill_job* job = (prefill_job*)arg;
+  const dec_args* a = job->a;
+  double* sc = (double*)malloc(sizeof(double) * (size_t)max_ctx_of(a->ctx, a->B));
+  double* acc = (double*)malloc(sizeof(double) * a->D);
+  for (;;) {
+    pthread_mutex_lock(&job->mu);
+    const int i = job->next++;
+    pthread_mutex_unlock(&job->mu);
+    if (i >= job->nrows) break;
+    const int row = job->rows[i];
+    int s = 0;
+    while (s + 1 < a->B && job->cu[s + 1] <= row) ++s;
+    prefill_row(a, job->cu, job->out, s, row, sc, acc);
   }
   free(sc);
   free(acc);
+  return NULL;
+}
+
+void or_prefill_packed_rows(const void* q, const void* kc, const void* vc, const int32_t* bt,
+                            const int32_t* ctx, const int32_t* cu, const int32_t* rows, int nrows,
+                            float* out, float scale, int S, int H, int Hkv, int D, int bs, int MB,
+                            int dt, int64_t stride, int nthreads) {
+  dec_args a = {q, kc, vc, bt, ctx, scale, S, H, Hkv, D, bs, MB, dt, stride};
+  prefill_job job;
+  job.a = &a;
+  job.cu = cu;
+  job.rows = rows;
+  job.out = out;
+  job.nrows = nrows;
+  job.next = 0;
+  pthread_mutex_init(&job.mu, NULL);
+  if (nthreads < 1) nthreads = 1;
+  pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * nthreads);
+  for (int i = 0; i < nthreads; ++i) pthread_create(&th[i], NULL, prefill_worker, &job);
+  for (int i = 0; i < nthreads; ++i) pthread_join(th[i], NULL);
+  free(th);
+  pthread_mutex_destroy(&job.mu);
 }
 
 /* ------------------------------------------- reference CPU attention path --- */
@@ -424,10 +486,19 @@ void or_prefill_packed(const void* q, const void* kc, const void* vc, const int3
 /* The reference's CPU counterpart of the decode op, "candle-core CPU attention
  * over the gathered blocks" (the rank-3 path of attention.rs:144-154 fed with
  * gathered cache rows): per (s, kv-head) gather the ctx rows of K and V into
- * contiguous fp32 [ctx, D]; per q-head scores = q.K^T * scale
- * (attention.rs:150), softmax over the last dim (max-subtract, exp, sum,
- * divide; attention.rs:151), out = probs.V (attention.rs:152).  Work items
- * (s, kv-head) are spread over `nthreads` POSIX threads. */
+ * contiguous fp32 [ctx, D] (candle's to_dtype(F32) of the gathered tensor); per
+ * q-head scores = q.K^T * scale (attention.rs:150), softmax over the last dim
+ * (max-subtract, exp, sum, divide; attention.rs:151), out = probs.V
+ * (attention.rs:152).  Work items (s, kv-head) are spread over `nthreads` POSIX
+ * threads.
+ *
+ * The two products are written the way a blocked CPU gemm (candle's `gemm`
+ * crate) computes them: q.K^T with eight-lane partial sums over d, all G q-heads
+ * of the kv-head from one load of each K row, and probs.V as rank-1 updates over
+ * t.  The dot products are therefore summed in a different order than a
+ * sequential loop (a float32 rounding difference, covered by the tolerance of
+ * every comparison).  The hot loops are compiled for AVX2 and for generic
+ * x86-64, picked at load time. */
 typedef struct {
   const dec_args* a;
   float* out;
@@ -436,46 +507,138 @@ typedef struct {
   pthread_mutex_t mu;
 } cpu_job;
 
+#if defined(__x86_64__) && defined(__GNUC__) && !defined(__clang__)
+#define OR_CLONES __attribute__((target_clones("avx2", "default")))
+#else
+#define OR_CLONES
+#endif
+
+typedef float v8f __attribute__((vector_size(32)));
+
+static inline v8f ld8(const float* p) {
+  v8f v;
+  memcpy(&v, p, sizeof(v));
+  return v;
+}
+
+/* sc[j][t] = (q_j . K[t]) * scale for the g q-heads q [g, D] and rows K [n, D]
+ * (D a multiple of 8). */
+OR_CLONES static void scores_group(const float* restrict q, const float* restrict kg, float* restrict sc, int n,
+                                   int D, int g, float scale) {
+  for (int t = 0; t < n; ++t) {
+    const float* restrict kr = kg + (int64_t)t * D;
+    for (int j0 = 0; j0 < g; j0 += 4) {
+      const int nj = g - j0 < 4 ? g - j0 : 4;
+      v8f acc[4] = {{0}, {0}, {0}, {0}};
+      for (int d = 0; d < D; d += 8) {
+        const v8f k8 = ld8(kr + d);
+        for (int j = 0; j < nj; ++j) acc[j] += ld8(q + (int64_t)(j0 + j) * D + d) * k8;
+      }
+      for (int j = 0; j < nj; ++j) {
+        const v8f a = acc[j];
+        const float sum = ((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7]));
+        sc[(int64_t)(j0 + j) * n + t] = sum * scale;
+      }
+    }
+  }
+}
+
+/* o[j][d] = sum_t p[j][t] * V[t][d] for the g heads, accumulated in t order; 16-column
+ * slices of four heads are held in registers over the whole t loop (D a multiple of 16). */
+OR_CLONES static void probs_v_group(const float* restrict p, const float* restrict vg, float* restrict o, int n,
+                                    int D, int g) {
+  for (int d0 = 0; d0 < D; d0 += 16) {
+    for (int j0 = 0; j0 < g; j0 += 4) {
+      const int nj = g - j0 < 4 ? g - j0 : 4;
+      v8f acc[4][2] = {{{0}, {0}}, {{0}, {0}}, {{0}, {0}}, {{0}, {0}}};
+      for (int t = 0; t < n; ++t) {
+        const float* restrict vr = vg + (int64_t)t * D + d0;
+        const v8f v0 = ld8(vr), v1 = ld8(vr + 8);
+        for (int j = 0; j < nj; ++j) {
+          const float pt = p[(int64_t)(j0 + j) * n + t];
+          acc[j][0] += pt * v0;
+          acc[j][1] += pt * v1;
+        }
+      }
+      for (int j = 0; j < nj; ++j) {
+        memcpy(o + (int64_t)(j0 + j) * D + d0, &acc[j][0], sizeof(v8f));
+        memcpy(o + (int64_t)(j0 + j) * D + d0 + 8, &acc[j][1], sizeof(v8f));
+      }
+    }
+  }
+}
+
+/* The same for any D (a multiple of 4): rank-1 updates of o over t. */
+static void probs_v_any(const float* restrict p, const float* restrict vg, float* restrict o, int n, int D, int g) {
+  for (int i = 0; i < g * D; ++i) o[i] = 0.f;
+  for (int t = 0; t < n; ++t)
+    for (int j = 0; j < g; ++j) {
+      const float pt = p[(int64_t)j * n + t];
+      for (int d = 0; d < D; ++d) o[(int64_t)j * D + d] += pt * vg[(int64_t)t * D + d];
+    }
+}
+
+/* One gathered row of K and of V as fp32. */
+OR_CLONES static void gather_row(const void* kc, const void* vc, int64_t row, int D, int dt, float* restrict kr,
+                                 float* restrict vr) {
+  if (dt == OR_BF16) {
+    const uint16_t* kp = (const uint16_t*)kc + row;
+    const uint16_t* vp = (const uint16_t*)vc + row;
+    for (int d = 0; d < D; ++d) {
+      kr[d] = bits_to_f32((uint32_t)kp[d] << 16);
+      vr[d] = bits_to_f32((uint32_t)vp[d] << 16);
+    }
+  } else {
+    for (int d = 0; d < D; ++d) {
+      kr[d] = ld(kc, row + d, dt);
+      vr[d] = ld(vc, row + d, dt);
+    }
+  }
+}
+
+/* Scratch per thread: kg/vg [n, D], probs [g, n], qv and ov [g, D]. */
 static void cpu_item(const dec_args* a, float* out, int item, float* kg, float* vg, float* probs,
-                     float* qv) {
+                     float* qv, float* ov) {
   const int s = item / a->Hkv;
   const int kvh = item % a->Hkv;
-  const int n = a->ctx[s];
+  const int n = a->ctx[s] > 0 ? a->ctx[s] : 0;
   const int g = a->H / a->Hkv;
   const int D = a->D;
-  for (int t = 0; t < n; ++t) {
-    const int64_t row = token_row(a, s, kvh, t);
-    for (int d = 0; d < D; ++d) {
-      kg[(int64_t)t * D + d] = ld(a->kc, row + d, a->dt);
-      vg[(int64_t)t * D + d] = ld(a->vc, row + d, a->dt);
-    }
+  float* o = out + ((int64_t)s * a->H + (int64_t)kvh * g) * D;  /* the group's g rows, contiguous */
+  if (n == 0) {
+    memset(o, 0, sizeof(float) * (size_t)g * D);
+    return;
+  }
+  for (int t = 0; t < n; ++t)
+    gather_row(a->kc, a->vc, token_row(a, s, kvh, t), D, a->dt, kg + (int64_t)t * D, vg + (int64_t)t * D);
+  for (int j = 0; j < g; ++j) load_q(a, s, kvh * g + j, qv + (int64_t)j * D);
+  if (D % 8 == 0) {
+    scores_group(qv, kg, probs, n, D, g, a->scale);
+  } else {
+    for (int j = 0; j < g; ++j)
+      for (int t = 0; t < n; ++t) {
+        float dot = 0.f;
+        for (int d = 0; d < D; ++d) dot += qv[(int64_t)j * D + d] * kg[(int64_t)t * D + d];
+        probs[(int64_t)j * n + t] = dot * a->scale;
+      }
   }
   for (int j = 0; j < g; ++j) {
-    const int h = kvh * g + j;
-    float* o = out + ((int64_t)s * a->H + h) * D;
-    for (int d = 0; d < D; ++d) o[d] = 0.f;
-    if (n <= 0) continue;
-    load_q(a, s, h, qv);
+    float* pj = probs + (int64_t)j * n;
     float mx = -INFINITY;
-    for (int t = 0; t < n; ++t) {
-      float dot = 0.f;
-      const float* kr = kg + (int64_t)t * D;
-      for (int d = 0; d < D; ++d) dot += qv[d] * kr[d];
-      probs[t] = dot * a->scale;
-      if (probs[t] > mx) mx = probs[t];
-    }
+    for (int t = 0; t < n; ++t)
+      if (pj[t] > mx) mx = pj[t];
     float sum = 0.f;
     for (int t = 0; t < n; ++t) {
-      probs[t] = expf(probs[t] - mx);
-      sum += probs[t];
+      pj[t] = expf(pj[t] - mx);
+      sum += pj[t];
     }
-    for (int t = 0; t < n; ++t) probs[t] /= sum;
-    for (int t = 0; t < n; ++t) {
-      const float p = probs[t];
-      const float* vr = vg + (int64_t)t * D;
-      for (int d = 0; d < D; ++d) o[d] += p * vr[d];
-    }
+    for (int t = 0; t < n; ++t) pj[t] /= sum;
   }
+  if (D % 16 == 0)
+    probs_v_group(probs, vg, ov, n, D, g);
+  else
+    probs_v_any(probs, vg, ov, n, D, g);
+  memcpy(o, ov, sizeof(float) * (size_t)g * D);
 }
 
 static void* cpu_worker(void* arg) {
@@ -485,21 +648,24 @@ static void* cpu_worker(void* arg) {
   for (int s = 0; s < a->B; ++s)
     if (a->ctx[s] > max_ctx) max_ctx = a->ctx[s];
   const size_t n = (size_t)(max_ctx > 0 ? max_ctx : 1);
+  const size_t g = (size_t)(a->H / a->Hkv);
   float* kg = (float*)malloc(sizeof(float) * n * a->D);
   float* vg = (float*)malloc(sizeof(float) * n * a->D);
-  float* probs = (float*)malloc(sizeof(float) * n);
-  float* qv = (float*)malloc(sizeof(float) * a->D);
+  float* probs = (float*)malloc(sizeof(float) * n * g);
+  float* qv = (float*)malloc(sizeof(float) * g * a->D);
+  float* ov = (float*)malloc(sizeof(float) * g * a->D);
   for (;;) {
     pthread_mutex_lock(&job->mu);
     const int item = job->next++;
     pthread_mutex_unlock(&job->mu);
     if (item >= job->n_items) break;
-    cpu_item(a, job->out, item, kg, vg, probs, qv);
+    cpu_item(a, job->out, item, kg, vg, probs, qv, ov);
   }
   free(kg);
   free(vg);
   free(probs);
   free(qv);
+  free(ov);
   return NULL;
 }
 

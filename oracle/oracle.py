@@ -26,6 +26,8 @@ paged_attention_v2_partition/reduce    v2(P) == v1 for several P; a planted wron
                                        copy of the merge maths is caught
 prefill_packed                         torch SDPA is_causal (CPU, fp64); last row == decode
                                        with ctx = pos + 1
+prefill_packed_rows                    == prefill_packed on the listed rows, rows not listed
+                                       untouched
 cpu_attention_gathered                 == paged_attention_v1_plus; float64 numpy attention
 =====================================  =====================================================
 
@@ -68,6 +70,7 @@ def lib() -> ctypes.CDLL:
             "or_paged_attention_v2_partition": (None, [V, V, V, V, V, V, V, V, F, I, I, I, I, I, I, I, I, I, I64]),
             "or_paged_attention_v2_reduce": (None, [V, V, V, V, V, I, I, I, I, I]),
             "or_prefill_packed": (None, [V, V, V, V, V, V, V, F, I, I, I, I, I, I, I, I64]),
+            "or_prefill_packed_rows": (None, [V, V, V, V, V, V, V, I, V, F, I, I, I, I, I, I, I, I64, I]),
             "or_cpu_attention_gathered": (None, [V, V, V, V, V, V, F, I, I, I, I, I, I, I, I64, I]),
         }
         for name, (res, args) in sig.items():
@@ -211,6 +214,24 @@ def prefill_packed(q, k_cache, v_cache, block_table, context_lens, cu_seqlens, s
                             _p(_i32(context_lens)), _p(_i32(cu_seqlens)), _p(out), scale, S, H, hkv, D, bs,
                             int(block_table.shape[1]), DT[dt], stride)
     return out
+
+
+def prefill_packed_rows(q, k_cache, v_cache, block_table, context_lens, cu_seqlens, rows, scale: float, dt: str,
+                        nthreads: int = 1) -> np.ndarray:
+    """prefill_packed for the packed row indices `rows` only, threaded -> float32 [len(rows), H, D]
+    (row i of the result is row rows[i] of prefill_packed's output)."""
+    T, H, D = q.shape
+    _, hkv, bs, _ = k_cache.shape
+    stride = int(k_cache.strides[0] // k_cache.itemsize)
+    S = len(cu_seqlens) - 1
+    rows = _i32(rows)
+    if rows.size and (rows.min() < 0 or rows.max() >= T):
+        raise ValueError("row index outside the packed stream")
+    out = np.zeros((T, H, D), np.float32)
+    lib().or_prefill_packed_rows(_p(q), _cache_base(k_cache), _cache_base(v_cache), _p(_i32(block_table)),
+                                 _p(_i32(context_lens)), _p(_i32(cu_seqlens)), _p(rows), int(rows.size), _p(out),
+                                 scale, S, H, hkv, D, bs, int(block_table.shape[1]), DT[dt], stride, nthreads)
+    return out[rows]
 
 
 def cpu_attention_gathered(q, k_cache, v_cache, block_table, context_lens, scale: float, dt: str,

@@ -170,3 +170,77 @@ def test_llama_prefill_decode_mixed(device, kernels, name):
     # step 3: decode only, every sequence one token further
     ext = [rng.integers(0, cfg.vocab_size) for _ in lens]
     run(pack_step([], [DecodeSlot(int(t), n + 1, bt) for t, n, bt in zip(ext, lens, bts)], bs), "decode")
+
+
+def _hf_state_of(cfg: LlamaConfig, w: LlamaWeights) -> dict:
+    """Hugging Face-named float32 CPU copies of the GPU model's bf16 weights (the same values),
+    split back into q/k/v and gate/up."""
+    H, Hkv, D, inter = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.intermediate_size
+    f = lambda t: t.float().cpu()  # noqa: E731
+    sd = {"model.embed_tokens.weight": f(w.embed), "model.norm.weight": f(w.norm)}
+    for i, L in enumerate(w.layers):
+        p = f"model.layers.{i}."
+        qkv, gu = f(L.wqkv), f(L.w_gate_up)
+        sd[p + "self_attn.q_proj.weight"] = qkv[:H * D]
+        sd[p + "self_attn.k_proj.weight"] = qkv[H * D:(H + Hkv) * D]
+        sd[p + "self_attn.v_proj.weight"] = qkv[(H + Hkv) * D:]
+        sd[p + "self_attn.o_proj.weight"] = f(L.wo)
+        sd[p + "mlp.gate_proj.weight"] = gu[:inter]
+        sd[p + "mlp.up_proj.weight"] = gu[inter:]
+        sd[p + "mlp.down_proj.weight"] = f(L.w_down)
+        sd[p + "input_layernorm.weight"] = f(L.input_norm)
+        sd[p + "post_attention_layernorm.weight"] = f(L.post_norm)
+    return sd
+
+
+def test_llama_config5_decode_step(device, kernels):
+    """BASELINE config 5 at its own shape: random-init Llama-3.2-1B (16 layers, hidden 2048,
+    32 / 8 heads, head_dim 64, intermediate 8192, vocab 128256, bf16 weights ~ N(0, 0.02), tied
+    LM head), one decode step of 128 sequences with contexts U[64, 8192] over per-layer paged
+    pools pre-filled with N(0, 1) (block 16, shuffled tables).  The logits of 8 sequences —
+    the longest and the shortest among them — are compared with the float32 CPU model
+    (oracle/llama_ref.py) run on those sequences alone: decode rows are independent, so the
+    oracle gets a compact pool holding only their blocks, copied from the GPU pools."""
+    from railgun_amd import workloads as wl
+    from railgun_amd.llama import LLAMA_3_2_1B as cfg
+
+    w = wl.config5()
+    bs = w.block_size
+    weights = LlamaWeights.random(cfg, 5, device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(w.seed)
+    pool = GpuBlockPool.for_model(cfg, w.num_blocks, bs, device, fill=gen)
+    model = RailgunLlama(cfg, weights, pool, kernels, max_position=int(w.context_lens.max()))
+    rng = np.random.default_rng(w.seed)
+    toks = rng.integers(0, cfg.vocab_size, w.batch)
+    nblk = [(int(c) + bs - 1) // bs for c in w.context_lens]
+    slots = [DecodeSlot(int(t), int(c), w.block_table[s, :nblk[s]].tolist())
+             for s, (t, c) in enumerate(zip(toks, w.context_lens))]
+    logits = model.forward(DeviceStep.from_host(pack_step([], slots, bs, max_blocks=w.block_table.shape[1]), device))
+    torch.cuda.synchronize()
+    assert logits.shape == (128, 128256)
+
+    order = np.argsort(w.context_lens, kind="stable")
+    pick = sorted({int(order[i]) for i in np.linspace(0, w.batch - 1, 8).round().astype(int)})
+    assert len(pick) == 8 and int(order[-1]) in pick and int(order[0]) in pick
+    # compact pool: the picked sequences' blocks renumbered 0..n-1, every layer copied
+    ids = np.concatenate([w.block_table[s, :nblk[s]] for s in pick]).astype(np.int64)
+    assert len(set(ids.tolist())) == len(ids)
+    sub_slots, cur = [], 0
+    for s in pick:
+        sub_slots.append(DecodeSlot(int(toks[s]), int(w.context_lens[s]), list(range(cur, cur + nblk[s]))))
+        cur += nblk[s]
+    sub_step = pack_step([], sub_slots, bs)
+    sd = _hf_state_of(cfg, weights)
+    ref32 = llama_ref.ReferenceLlama(cfg, sd, 1, bs)
+    ref16 = llama_ref.ReferenceLlama(cfg, sd, 1, bs, act_dtype=torch.bfloat16)
+    dev_ids = torch.from_numpy(ids).to(device)
+    for layer in range(cfg.num_hidden_layers):
+        blocks = pool.storage[layer].index_select(0, dev_ids).float().cpu()   # [n, 2, H_kv, bs, D]
+        k, v = blocks[:, 0].contiguous(), blocks[:, 1].contiguous()
+        # each reference writes its own new-token row before reading: sharing the pool is safe
+        ref32.k[layer], ref32.v[layer] = k, v
+        ref16.k[layer], ref16.v[layer] = k, v
+    want32 = ref32.forward(sub_step)
+    want16 = ref16.forward(sub_step)
+    _check(logits[torch.as_tensor(pick, device=device)], want32, want16, "config 5 decode step")
