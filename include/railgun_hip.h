@@ -237,6 +237,35 @@ int rg_paged_attention_v1_plus(const void* query, const void* key_cache,
                                int32_t dtype, int64_t kv_block_stride,
                                void* workspace, size_t workspace_bytes, void* stream);
 
+/* Largest split-K scratch rg_paged_attention_v1_no_alloc can use: 16 MiB, a static
+ * device array of the library that every device holds from the library's load until the
+ * process ends.  The stream-K form needs (W + batch*num_kv_heads) * (G*head_dim + 2G) * 4
+ * bytes (+ 8 per segment), W = 4 per compute unit and G = num_heads/num_kv_heads: at
+ * G = 4, head_dim 128 on 256 compute units up to 7,000 (batch x kv-head) segments fit. */
+#define RG_NO_ALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+
+/* rg_paged_attention_v1 without a workspace argument and without any allocation: the
+ * stream-K split runs on the library's static scratch (RG_NO_ALLOC_SCRATCH_BYTES per
+ * device, its address looked up by rg_init or by the first call on a device) instead of a
+ * caller's workspace; shapes outside the stream-K path take the path
+ * rg_paged_attention_v1 takes with workspace == NULL, which uses no scratch.  Same results
+ * as rg_paged_attention_v1 with a workspace.  Returns RG_ERR_WORKSPACE, launching
+ * nothing, when the shape needs more scratch than the static array holds.  Calls no
+ * hipMalloc / hipFree / memset and records nothing that allocates, so it may run under HIP
+ * graph capture.  The scratch needs no clearing (every call writes what it reads), but it
+ * is shared by every call on a device: calls that overlap in time on one device (different
+ * streams or threads without ordering between them) race on it; calls on one stream are
+ * ordered and safe.
+ * No counterpart in the reference: an entry for callers that cannot allocate device
+ * memory (code under graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int rg_paged_attention_v1_no_alloc(const void* query, const void* key_cache,
+                                   const void* value_cache, const int32_t* block_table,
+                                   const int32_t* context_lens, void* output, float scale,
+                                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                   int32_t block_size, int32_t max_blocks_per_seq,
+                                   int32_t batch_size, int32_t dtype, int64_t kv_block_stride,
+                                   void* stream);
+
 /* ------------------------------------------------- decode, v2 split-K ------ */
 
 /* Bytes of the three fp32 scratch arrays of v2 (tmp_out, exp_sums, max_logits)

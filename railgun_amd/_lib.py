@@ -82,6 +82,11 @@ SIGNATURES = {
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32, c_int32,
          c_int32, c_int32, c_int32, c_int32, c_int64, c_void_p, c_size_t, c_void_p],
     ),
+    "rg_paged_attention_v1_no_alloc": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32, c_int32,
+         c_int32, c_int32, c_int32, c_int32, c_int64, c_void_p],
+    ),
     "rg_paged_attention_v1_plus": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32,

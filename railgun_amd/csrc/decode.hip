@@ -26,6 +26,8 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -1290,7 +1292,56 @@ int paged_v1(const char* op, const void* q, const void* kc, const void* vc, cons
   return run_partition(op, a, dtype, sh.B, 1, s);
 }
 
+// ---- entry without allocation ----
+//
+// rg_paged_attention_v1_no_alloc keeps the stream-K partials in `scratch` below, one copy per
+// device, instead of a caller's workspace.  Host code never passes `scratch` itself to a
+// kernel (on the host that name is a stand-in, not a device address): the address of each
+// device's copy comes from hipGetSymbolAddress, taken once per device with that device
+// current, and is kept in g_scratch_addr.
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
 }  // namespace
+
+static __device__ __align__(256) unsigned char scratch[RG_NO_ALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// Address of the current device's copy of `scratch`; looked up on the first call per device.
+int no_alloc_scratch(const char* op, void** addr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(RG_ERR_HIP, "%s: no current device: %s", op, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) {
+    return fail(RG_ERR_NOT_SUPPORTED, "%s: device ordinal %d beyond the %d devices supported", op, dev, kMaxDevices);
+  }
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr) {
+        return fail(RG_ERR_HIP, "%s: cannot locate the static scratch on device %d: %s", op, dev,
+                    hipGetErrorString(e));
+      }
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *addr = p;
+  return RG_OK;
+}
+
+}  // namespace
+
+// Called by rg_init with the device being initialised current.
+int setup_no_alloc_scratch() {
+  void* p = nullptr;
+  return no_alloc_scratch("rg_init", &p);
+}
 
 int probe_decode_kernels() {
   hipFuncAttributes at;
@@ -1471,4 +1522,42 @@ extern "C" int rg_paged_attention_v2(const void* query, const void* key_cache,
   MergeArgs m{output, sc.exp_sums, sc.max_logits, sc.tmp_out, context_lens, num_heads, head_dim,
               np, partition_size, 1};
   return run_merge(op, m, dtype, batch_size, s);
+}
+
+extern "C" int rg_paged_attention_v1_no_alloc(const void* query, const void* key_cache,
+                                              const void* value_cache, const int32_t* block_table,
+                                              const int32_t* context_lens, void* output, float scale,
+                                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                              int32_t block_size, int32_t max_blocks_per_seq,
+                                              int32_t batch_size, int32_t dtype, int64_t kv_block_stride,
+                                              void* stream) {
+  const char* op = "paged_attention_v1_no_alloc";
+  const Shape sh{num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, batch_size};
+  int st = check_decode_shape(op, sh, dtype, kv_block_stride);
+  if (st != RG_OK) return st;
+  if (sh.B == 0) return ok();
+  if (!query || !key_cache || !value_cache || !block_table || !context_lens || !output) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
+  }
+  const DecodeArgs a = make_args(query, key_cache, value_cache, block_table, context_lens, output, scale, sh,
+                                 kv_block_stride, kBS, 1, MODE_AUTO);
+  if (mfma_applies(a, dtype) && sh.MB > 0) {
+    // The stream-K kernels of rg_paged_attention_v1 with the static scratch as their workspace.
+    // Nothing in it needs clearing: every partial and segment descriptor the merge reads is
+    // written earlier in the same call.
+    const size_t need = stream_bytes(sh, stream_workers(sh), nullptr, nullptr);
+    if (need > (size_t)RG_NO_ALLOC_SCRATCH_BYTES) {
+      return fail(RG_ERR_WORKSPACE,
+                  "%s: this shape needs %zu bytes of split-K scratch, the static scratch holds %zu "
+                  "(call rg_paged_attention_v1 with a workspace instead)",
+                  op, need, (size_t)RG_NO_ALLOC_SCRATCH_BYTES);
+    }
+    void* ws = nullptr;
+    st = no_alloc_scratch(op, &ws);
+    if (st != RG_OK) return st;
+    return run_stream(op, a, dtype, sh, ws, RG_NO_ALLOC_SCRATCH_BYTES, as_stream(stream));
+  }
+  // The other paths of rg_paged_attention_v1 without a workspace use no scratch at all.
+  return paged_v1(op, query, key_cache, value_cache, block_table, context_lens, output, scale, sh, dtype,
+                  kv_block_stride, nullptr, 0, stream);
 }

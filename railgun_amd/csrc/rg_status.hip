@@ -54,6 +54,7 @@ namespace rg {
 int probe_cache_kernels();
 int probe_decode_kernels();
 int probe_prefill_kernels();
+int setup_no_alloc_scratch();
 }  // namespace rg
 
 extern "C" int rg_init(int device_ordinal) {
@@ -84,6 +85,7 @@ extern "C" int rg_init(int device_ordinal) {
   int st = rg::probe_cache_kernels();
   if (st == RG_OK) st = rg::probe_decode_kernels();
   if (st == RG_OK) st = rg::probe_prefill_kernels();
+  if (st == RG_OK) st = rg::setup_no_alloc_scratch();
   (void)hipSetDevice(cur);
   if (st != RG_OK) return st;
   return rg::ok();

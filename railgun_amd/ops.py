@@ -149,6 +149,19 @@ class PagedAttentionKernels:
             block_size, max_blocks_per_seq, batch_size, dtype_code(query), key_cache.stride(0),
             _ptr(workspace), ws_bytes, _stream(query)))
 
+    def launch_v1_no_alloc(self, query, key_cache, value_cache, block_table, context_lens, output, scale: float,
+                           num_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
+                           max_blocks_per_seq: int, batch_size: int) -> None:
+        """launch_v1 for callers that cannot allocate (graph capture, serving loops): the split-K
+        partials go to the library's static per-device scratch (rg_paged_attention_v1_no_alloc).
+        Calls that overlap in time on one device race on that scratch; one stream orders them."""
+        _require_cuda(query, key_cache, value_cache, block_table, context_lens, output)
+        _require_i32(block_table, context_lens)
+        check(self.lib.rg_paged_attention_v1_no_alloc(
+            query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
+            context_lens.data_ptr(), output.data_ptr(), float(scale), num_heads, num_kv_heads, head_dim,
+            block_size, max_blocks_per_seq, batch_size, dtype_code(query), key_cache.stride(0), _stream(query)))
+
     # mod.rs:350-399
     def launch_v1_plus(self, query, key_cache, value_cache, block_table, context_lens, output,
                        rotation_metadata, scale: float, num_heads: int, num_kv_heads: int, head_dim: int,
