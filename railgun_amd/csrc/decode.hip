@@ -533,7 +533,8 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 //
 // The decode work is the list of units (sequence s, kv-head, b) ordered with b fastest,
 // unit b covering blocks [b * BPU, b * BPU + BPU) of the sequence (sk_bpu: 1 at head_dim 128,
-// 4 at head_dim 64); segment g = s * num_kv_heads + kvh is the run of units of one (s, kv-head).
+// 4 at head_dim 64, 2 at head_dim 64 with G >= 8); segment g = s * num_kv_heads + kvh is the
+// run of units of one (s, kv-head).
 // Worker k (one wave) takes units [k*U/W, (k+1)*U/W) of the U units, so every wave streams
 // the same number of units whatever the context lengths are.  A worker emits one partial
 // (m, l, acc) for every segment it touches, at partial index k + g (distinct for all
@@ -564,9 +565,12 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 #ifndef RG_SK_PREFETCH_D64
 #define RG_SK_PREFETCH_D64 2
 #endif
-template <int D>
-constexpr int sk_bpu() { return D <= 64 ? RG_SK_BPU_D64 : RG_SK_BPU_D128; }
-template <int D>
+// With 8 or more q-heads per kv-head the accumulators take 8 * G registers per lane, so at
+// head_dim 64 the unit ring shrinks to two-block units (half the registers of the four-block
+// ring, which G >= 8 fills to the limit).
+template <int D, int G>
+constexpr int sk_bpu() { return D <= 64 ? (G >= 8 ? 2 : RG_SK_BPU_D64) : RG_SK_BPU_D128; }
+template <int D, int G>
 constexpr int sk_prefetch() { return D <= 64 ? RG_SK_PREFETCH_D64 : RG_SK_PREFETCH; }
 
 // Optional occupancy floor of the stream-K kernel (waves per SIMD).
@@ -658,9 +662,9 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   constexpr int HG = Tile::HG;
   constexpr int NK = Tile::NK;
   constexpr int NV = Tile::NV;
-  constexpr int kSkPrefetch = sk_prefetch<D>();
+  constexpr int kSkPrefetch = sk_prefetch<D, G>();
   constexpr int NBUF = kSkPrefetch + 1;
-  constexpr int BPU = sk_bpu<D>();
+  constexpr int BPU = sk_bpu<D, G>();
   __shared__ float p_lds[2][BPU * kBS * GP];
   __shared__ float alpha_lds[2][GP];
 
