@@ -50,7 +50,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-side", action="store_true", help="skip the config 3 / config 4 side figures")
-    ap.add_argument("--only", choices=["decode", "v2", "prefill", "model", "copy"], default=None,
+    ap.add_argument("--only", choices=["decode", "v2", "fp32", "prefill", "model", "copy"], default=None,
                     help="run one workload only and print its figures (for profiling); 'copy' is the plain "
                          "1 GiB device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
@@ -220,6 +220,41 @@ def side_v2(device, gen, steps: int) -> dict:
                                "frac_hbm_peak": round(gbs_pair / HBM_PEAK_GBS, 4)}}
 
 
+def side_fp32(device, gen, steps: int) -> dict:
+    """Config 2's decode (64 sequences, contexts U[512, 4096], 32 / 8 heads, head_dim 128) in fp32,
+    the reference launchers' element type: paged attention v1 with its workspace (the fp32
+    stream-K tile), K calls back to back.  Algorithmic bytes as for bf16, at 4 bytes per element."""
+    import dataclasses
+
+    import torch
+
+    from railgun_amd import workloads as wl
+    from railgun_amd.ops import PagedAttentionKernels
+
+    w = dataclasses.replace(wl.config2(), dtype="f32")
+    kernels = PagedAttentionKernels(0)
+    shape = (w.num_blocks, w.num_kv_heads, w.block_size, w.head_dim)
+    kc = torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
+    vc = torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
+    q = torch.randn((w.batch, w.num_heads, w.head_dim), generator=gen, device=device, dtype=torch.float32)
+    out = torch.empty_like(q)
+    bt, ctx = torch.from_numpy(w.block_table).to(device), torch.from_numpy(w.context_lens).to(device)
+    nbytes = kernels.v1_workspace_bytes(w.batch, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size, w.max_blocks)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+
+    def call():
+        kernels.launch_v1(q, kc, vc, bt, ctx, out, w.scale, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size,
+                          w.max_blocks, w.batch, workspace=ws)
+
+    ms = time_events(call, steps, 3)
+    gbs = w.decode_bytes() / (ms * 1e-3) / 1e9
+    del kc, vc, ws
+    torch.cuda.empty_cache()
+    return {"workload": "config2_shape_fp32_decode", "kernel": "paged_attention_v1 (fp32 stream-K + merge)",
+            "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes": w.decode_bytes()}
+
+
 def side_prefill(device, gen, steps: int) -> dict:
     import torch
 
@@ -351,6 +386,9 @@ def main() -> int:
     if args.only == "v2":
         print(json.dumps(side_v2(device, gen, args.steps)), flush=True)
         return 0
+    if args.only == "fp32":
+        print(json.dumps(side_fp32(device, gen, args.steps)), flush=True)
+        return 0
     if args.only == "prefill":
         print(json.dumps(side_prefill(device, gen, args.steps)), flush=True)
         return 0
@@ -412,6 +450,8 @@ def main() -> int:
     if not args.no_side:
         log("[bench] config3 v2 ...")
         result["v2_long_context"] = side_v2(device, gen, max(3, args.steps // 5))
+        log("[bench] config2 shape in fp32 ...")
+        result["fp32_decode"] = side_fp32(device, gen, max(3, args.steps // 5))
         log("[bench] config4 prefill ...")
         result["prefill"] = side_prefill(device, gen, 10)
         log("[bench] config5 model step ...")

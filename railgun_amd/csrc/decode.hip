@@ -234,6 +234,54 @@ constexpr int kThreads = kWaves * 64;
 #define RG_DEC_OCCUPANCY
 #endif
 
+// Online-softmax update of one step of NB blocks, shared by the decode tiles.  c[b] holds the
+// raw scores of block b in the MFMA output layout (lane (col, seg): token col, heads 4*seg + r);
+// tokens at context index >= ctx are masked.  Updates the wave-uniform running max m_run and
+// the per-lane sums l_run (exp2 domain), writes the probabilities of the NB * 16 tokens to
+// p_lds ([token][GP heads]) and the rescale factors to alpha_lds, and returns whether any
+// head's maximum moved (then acc needs the rescale).
+template <int NB, int GP, int HG>
+__device__ __forceinline__ bool softmax_block(const f32x4_t (&c)[NB], int col, int seg, int tok0, int ctx,
+                                              float scale_log2, float (&m_run)[4], float (&l_run)[4],
+                                              float* p_lds, float* alpha_lds) {
+  float x[NB][4];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const bool valid = tok0 + b * kBS + col < ctx;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[b][r] = valid ? c[b][r] * scale_log2 : -INFINITY;
+  }
+  float pr[NB][4], al[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float mx = x[0][r];
+#pragma unroll
+    for (int b = 1; b < NB; ++b) mx = fmaxf(mx, x[b][r]);
+    const float bm = row16_max(mx);
+    const float m_new = fmaxf(m_run[r], bm);
+    al[r] = fast_exp2(m_run[r] - m_new);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) pr[b][r] = fast_exp2(x[b][r] - m_new);
+    float ps = pr[0][r];
+#pragma unroll
+    for (int b = 1; b < NB; ++b) ps += pr[b][r];
+    l_run[r] = l_run[r] * al[r] + ps;
+    m_run[r] = m_new;
+  }
+  // The running max of a head moves on few blocks only: skip the rescale of acc when it
+  // moved for no head (a wave-uniform decision).
+  const bool rescale = __ballot(al[0] != 1.f || al[1] != 1.f || al[2] != 1.f || al[3] != 1.f) != 0;
+  if (seg < HG) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      *reinterpret_cast<float4*>(&p_lds[(b * kBS + col) * GP + 4 * seg]) =
+          make_float4(pr[b][0], pr[b][1], pr[b][2], pr[b][3]);
+    if (col == 0) *reinterpret_cast<float4*>(&alpha_lds[4 * seg]) = make_float4(al[0], al[1], al[2], al[3]);
+  }
+  wave_lds_sync();
+  return rescale;
+}
+
 // Per-wave state and block step of the MFMA decode path, shared by the grid kernel and the
 // stream-K kernel.  One wave owns one (sequence, kv-head) segment at a time and processes
 // 16-token blocks:
@@ -254,6 +302,7 @@ struct DecodeTile {
   static constexpr int NV = kBS / TPI;      // V loads per block
   static constexpr int GP = G < 4 ? 4 : G;  // padded heads per LDS row
   static constexpr int HG = (G + 3) / 4;    // MFMA output rows holding distinct heads
+  static constexpr int ACC = 8;             // output dims per lane and head (acc[h][0..ACC))
 
   int col, seg, vrow, vd0;
   uint4 qa[NK];
@@ -313,41 +362,7 @@ struct DecodeTile {
       for (int i = 0; i < NK; ++i) c[b] = MF::run(qa[i], kr[b * NK + i], c[b]);
     }
     const bool tail = tok0 + NB * kBS > ctx;
-    float x[NB][4];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const bool valid = tok0 + b * kBS + col < ctx;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[b][r] = valid ? c[b][r] * scale_log2 : -INFINITY;
-    }
-    float pr[NB][4], al[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float mx = x[0][r];
-#pragma unroll
-      for (int b = 1; b < NB; ++b) mx = fmaxf(mx, x[b][r]);
-      const float bm = row16_max(mx);
-      const float m_new = fmaxf(m_run[r], bm);
-      al[r] = fast_exp2(m_run[r] - m_new);
-#pragma unroll
-      for (int b = 0; b < NB; ++b) pr[b][r] = fast_exp2(x[b][r] - m_new);
-      float ps = pr[0][r];
-#pragma unroll
-      for (int b = 1; b < NB; ++b) ps += pr[b][r];
-      l_run[r] = l_run[r] * al[r] + ps;
-      m_run[r] = m_new;
-    }
-    // The running max of a head moves on few blocks only: skip the rescale of acc when it
-    // moved for no head (a wave-uniform decision).
-    const bool rescale = __ballot(al[0] != 1.f || al[1] != 1.f || al[2] != 1.f || al[3] != 1.f) != 0;
-    if (seg < HG) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-        *reinterpret_cast<float4*>(&p_lds[(b * kBS + col) * GP + 4 * seg]) =
-            make_float4(pr[b][0], pr[b][1], pr[b][2], pr[b][3]);
-      if (col == 0) *reinterpret_cast<float4*>(&alpha_lds[4 * seg]) = make_float4(al[0], al[1], al[2], al[3]);
-    }
-    wave_lds_sync();
+    const bool rescale = softmax_block<NB, GP, HG>(c, col, seg, tok0, ctx, scale_log2, m_run, l_run, p_lds, alpha_lds);
     if (rescale) {
       float alh[G];
 #pragma unroll
@@ -399,6 +414,136 @@ struct DecodeTile {
     for (int r = 0; r < 4; ++r) lsum[r] = row16_sum(l_run[r]);
   }
 };
+
+// The fp32 tile (the reference's own element type): the same per-wave state and step as
+// DecodeTile, with QK^T on v_mfma_f32_16x16x4_f32.  MFMA m of a block takes the k-slot s of
+// lane (col, seg) from dim DQ*s + m (DQ = D/4), so lane (col, seg) holds the contiguous run
+// K[col][DQ*seg .. DQ*seg + DQ) (DQ/4 16-byte loads) and, as the A operand, the same dims of
+// head col % G; the output has DecodeTile's layout (scores of heads 4*seg + r for token col),
+// so the softmax is softmax_block.  P.V runs on the VALU with 16-byte fp32 V loads: lane
+// (vrow, vd0) holds 4 dims of V rows vrow + i*TPI.
+template <int D, int G>
+struct DecodeTileF32 {
+  using S = float;
+  static constexpr int DQ = D / 4;          // dims per lane in QK (and MFMAs per block)
+  static constexpr int NK = DQ / 4;         // 16-byte K loads per block
+  static constexpr int ROWV = D / 4;        // 16-byte vectors per token row
+  static constexpr int TPI = 64 / ROWV;     // tokens covered by one V load instruction
+  static constexpr int NV = kBS / TPI;      // V loads per block
+  static constexpr int GP = G < 4 ? 4 : G;
+  static constexpr int HG = (G + 3) / 4;
+  static constexpr int ACC = 4;
+  static_assert(NK >= 1 && TPI >= 1 && NV >= 1, "head_dim 64 or 128");
+
+  int col, seg, vrow, vd0;
+  float qa[DQ];
+  float m_run[4], l_run[4];
+  float acc[G][4];
+
+  __device__ __forceinline__ void init(int lane) {
+    col = lane & 15;
+    seg = lane >> 4;
+    vrow = lane / ROWV;
+    vd0 = (lane % ROWV) * 4;
+  }
+  __device__ __forceinline__ void load_q(const float* qg) {
+    const float4* qrow = reinterpret_cast<const float4*>(qg + (int64_t)(col % G) * D + seg * DQ);
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const float4 v = qrow[i];
+      qa[4 * i] = v.x;
+      qa[4 * i + 1] = v.y;
+      qa[4 * i + 2] = v.z;
+      qa[4 * i + 3] = v.w;
+    }
+  }
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      m_run[r] = -INFINITY;
+      l_run[r] = 0.f;
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[h][e] = 0.f;
+  }
+  template <int NB, int B>
+  __device__ __forceinline__ void load_part(const float* kb, const float* vb, uint4 (&kk)[NB * NK],
+                                            uint4 (&vv)[NB * NV]) const {
+    const uint4* kp = reinterpret_cast<const uint4*>(kb + col * D + seg * DQ);
+#pragma unroll
+    for (int i = 0; i < NK; ++i) kk[B * NK + i] = kp[i];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) vv[B * NV + i] = *reinterpret_cast<const uint4*>(vb + (i * TPI + vrow) * D + vd0);
+  }
+  __device__ __forceinline__ void load(const float* kb, const float* vb, uint4 (&kk)[NK], uint4 (&vv)[NV]) const {
+    load_part<1, 0>(kb, vb, kk, vv);
+  }
+  template <int NB = 1>
+  __device__ __forceinline__ void step(const uint4 (&kr)[NB * NK], const uint4 (&vr)[NB * NV], int tok0, int ctx,
+                                       float scale_log2, float* p_lds, float* alpha_lds) {
+    f32x4_t c[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      c[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < NK; ++i) {
+        const uint4 k4 = kr[b * NK + i];
+        const uint32_t kw[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          c[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * i + e], __uint_as_float(kw[e]), c[b], 0, 0, 0);
+      }
+    }
+    const bool tail = tok0 + NB * kBS > ctx;
+    const bool rescale = softmax_block<NB, GP, HG>(c, col, seg, tok0, ctx, scale_log2, m_run, l_run, p_lds, alpha_lds);
+    if (rescale) {
+      float alh[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) alh[h] = alpha_lds[h];
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[h][e] *= alh[h];
+    }
+#pragma unroll
+    for (int i = 0; i < NB * NV; ++i) {
+      const int t = i * TPI + vrow;
+      float vf[4] = {__uint_as_float(vr[i].x), __uint_as_float(vr[i].y), __uint_as_float(vr[i].z),
+                     __uint_as_float(vr[i].w)};
+      if (tail && tok0 + t >= ctx) {
+        // Rows past the context may hold any bit pattern; keep them out of 0*x.
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vf[e] = 0.f;
+      }
+      float ph[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) ph[h] = p_lds[t * GP + h];
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[h][e] += ph[h] * vf[e];
+    }
+  }
+  __device__ __forceinline__ void reduce(float (&lsum)[4]) {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = acc[h][e];
+#pragma unroll
+        for (int o = ROWV; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+        acc[h][e] = v;
+      }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lsum[r] = row16_sum(l_run[r]);
+  }
+};
+
+// The tile type of element type T.
+template <typename T, int D, int G>
+using DecodeTileFor = std::conditional_t<std::is_same_v<T, f32_t>, DecodeTileF32<D, G>, DecodeTile<T, D, G>>;
 
 // Grid decomposition: workgroup = (partition p, kv-head, sequence), kWaves waves taking the
 // partition's blocks round-robin, merged through LDS at the end.
@@ -572,6 +717,13 @@ template <int D, int G>
 constexpr int sk_bpu() { return D <= 64 ? (G >= 8 ? 2 : RG_SK_BPU_D64) : RG_SK_BPU_D128; }
 template <int D, int G>
 constexpr int sk_prefetch() { return D <= 64 ? RG_SK_PREFETCH_D64 : RG_SK_PREFETCH; }
+// fp32 rows are twice as long: one-block units (8 KB of K and of V at head_dim 128), one in
+// flight ahead at head_dim 128 and two at head_dim 64 (the register ring of the 16-bit tiles'
+// depth would not fit).
+template <typename T, int D, int G>
+constexpr int sk_bpu_for() { return std::is_same_v<T, f32_t> ? 1 : sk_bpu<D, G>(); }
+template <typename T, int D, int G>
+constexpr int sk_prefetch_for() { return std::is_same_v<T, f32_t> ? (D <= 64 ? 2 : 1) : sk_prefetch<D, G>(); }
 
 // Optional occupancy floor of the stream-K kernel (waves per SIMD).
 #if defined(RG_SK_OCC) && RG_SK_OCC > 0
@@ -654,17 +806,17 @@ __device__ __forceinline__ int64_t scan_units(const int32_t* ctxl, int batch, in
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
-    StreamArgs a, const uint16_t* __restrict__ q_ptr, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_table,
-    const int32_t* __restrict__ context_lens) {
-  using Tile = DecodeTile<T, D, G>;
+    StreamArgs a, const typename DecodeTileFor<T, D, G>::S* __restrict__ q_ptr,
+    const typename DecodeTileFor<T, D, G>::S* __restrict__ kc, const typename DecodeTileFor<T, D, G>::S* __restrict__ vc,
+    const int32_t* __restrict__ block_table, const int32_t* __restrict__ context_lens) {
+  using Tile = DecodeTileFor<T, D, G>;
   constexpr int GP = Tile::GP;
   constexpr int HG = Tile::HG;
   constexpr int NK = Tile::NK;
   constexpr int NV = Tile::NV;
-  constexpr int kSkPrefetch = sk_prefetch<D, G>();
+  constexpr int kSkPrefetch = sk_prefetch_for<T, D, G>();
   constexpr int NBUF = kSkPrefetch + 1;
-  constexpr int BPU = sk_bpu<D, G>();
+  constexpr int BPU = sk_bpu_for<T, D, G>();
   __shared__ float p_lds[2][BPU * kBS * GP];
   __shared__ float alpha_lds[2][GP];
 
@@ -801,8 +953,10 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         float4* dst = reinterpret_cast<float4*>(pa + h * D + tile.vd0);
-        dst[0] = make_float4(tile.acc[h][0], tile.acc[h][1], tile.acc[h][2], tile.acc[h][3]);
-        dst[1] = make_float4(tile.acc[h][4], tile.acc[h][5], tile.acc[h][6], tile.acc[h][7]);
+#pragma unroll
+        for (int q4 = 0; q4 < Tile::ACC / 4; ++q4)
+          dst[q4] = make_float4(tile.acc[h][4 * q4], tile.acc[h][4 * q4 + 1], tile.acc[h][4 * q4 + 2],
+                                tile.acc[h][4 * q4 + 3]);
       }
     }
     if (tile.col == 0 && tile.seg < HG) {
@@ -883,7 +1037,7 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
 template <typename T, int D, int G>
 __global__ __launch_bounds__(64 * G) void decode_stream_merge_kernel(StreamArgs a,
                                                                     const int32_t* __restrict__ context_lens) {
-  using S = uint16_t;
+  using S = typename elem<T>::storage;
   constexpr int PER = D / 64;  // dims per lane
   static_assert(PER == 1 || PER == 2, "head_dim 64 or 128");
   const int kvh = blockIdx.x;
@@ -929,11 +1083,12 @@ __global__ __launch_bounds__(64 * G) void decode_stream_merge_kernel(StreamArgs 
     m = mn;
   }
   const float inv = l != 0.f ? 1.f / l : 1.f;
-  if constexpr (PER == 2) {
+  if constexpr (PER == 2 && !std::is_same_v<T, f32_t>) {
     const uint32_t packed = (uint32_t)elem<T>::from_f32(acc[0] * inv) | ((uint32_t)elem<T>::from_f32(acc[1] * inv) << 16);
     *reinterpret_cast<uint32_t*>(out) = packed;
   } else {
-    out[0] = elem<T>::from_f32(acc[0] * inv);
+#pragma unroll
+    for (int e = 0; e < PER; ++e) out[e] = elem<T>::from_f32(acc[e] * inv);
   }
 }
 
@@ -1086,6 +1241,15 @@ bool mfma_applies(const DecodeArgs& a, int32_t dtype) {
          (a.out == nullptr || (reinterpret_cast<uintptr_t>(a.out) & 3u) == 0);
 }
 
+// The stream-K decode: the MFMA shapes in bf16 / f16, and the same shapes in fp32.
+bool stream_applies(const DecodeArgs& a, int32_t dtype) {
+  if (dtype != RG_DTYPE_F32) return mfma_applies(a, dtype);
+  const int G = a.num_heads / a.num_kv_heads;
+  return a.block_size == kBS && (a.head_dim == 64 || a.head_dim == 128) &&
+         (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && aligned16(a.q) && aligned16(a.k_cache) &&
+         aligned16(a.v_cache) && (a.kv_stride * 4) % 16 == 0 && (a.out == nullptr || (reinterpret_cast<uintptr_t>(a.out) & 3u) == 0);
+}
+
 // Launches the partition kernel over grid (grid_parts, heads, batch).
 int run_partition(const char* op, const DecodeArgs& a, int32_t dtype, int32_t batch,
                   int32_t grid_parts, hipStream_t s) {
@@ -1204,9 +1368,10 @@ size_t stream_bytes(const Shape& sh, int32_t workers, StreamScratch* carve, void
 
 template <typename T, int D, int G>
 void launch_stream(const StreamArgs& sa, const DecodeArgs& a, hipStream_t s) {
+  using S = typename DecodeTileFor<T, D, G>::S;
   hipLaunchKernelGGL((decode_stream_kernel<T, D, G>), dim3(sa.num_workers), dim3(64), 0, s, sa,
-                     static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.k_cache),
-                     static_cast<const uint16_t*>(a.v_cache), a.block_table, a.context_lens);
+                     static_cast<const S*>(a.q), static_cast<const S*>(a.k_cache),
+                     static_cast<const S*>(a.v_cache), a.block_table, a.context_lens);
   hipLaunchKernelGGL((decode_stream_merge_kernel<T, D, G>), dim3(sa.num_kv_heads, sa.batch), dim3(64 * G), 0, s,
                      sa, a.context_lens);
 }
@@ -1245,9 +1410,12 @@ int run_stream(const char* op, const DecodeArgs& a, int32_t dtype, const Shape& 
   if (dtype == RG_DTYPE_BF16) {
     if (sh.D == 128) launch_stream_g<bf16_t, 128>(sa, a, G, s);
     else launch_stream_g<bf16_t, 64>(sa, a, G, s);
-  } else {
+  } else if (dtype == RG_DTYPE_F16) {
     if (sh.D == 128) launch_stream_g<f16_t, 128>(sa, a, G, s);
     else launch_stream_g<f16_t, 64>(sa, a, G, s);
+  } else {
+    if (sh.D == 128) launch_stream_g<f32_t, 128>(sa, a, G, s);
+    else launch_stream_g<f32_t, 64>(sa, a, G, s);
   }
   return check_launch(op);
 }
@@ -1265,7 +1433,7 @@ int paged_v1(const char* op, const void* q, const void* kc, const void* vc, cons
   hipStream_t s = as_stream(stream);
   if (ws != nullptr) {
     DecodeArgs a = make_args(q, kc, vc, bt, cl, out, scale, sh, kv_stride, kBS, 1, MODE_AUTO);
-    if (mfma_applies(a, dtype) && sh.MB > 0) {
+    if (stream_applies(a, dtype) && sh.MB > 0) {
       st = run_stream(op, a, dtype, sh, ws, ws_bytes, s);
       if (st != RG_ERR_WORKSPACE) return st;
       return fail(RG_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu required", op, ws_bytes,
@@ -1504,7 +1672,7 @@ extern "C" int rg_paged_attention_v2(const void* query, const void* key_cache,
     // it runs whenever it applies and the workspace holds its scratch.
     DecodeArgs a = make_args(query, key_cache, value_cache, block_table, context_lens, output, scale, sh,
                              kv_block_stride, partition_size, 1, MODE_AUTO);
-    if (mfma_applies(a, dtype) && max_blocks_per_seq > 0) {
+    if (stream_applies(a, dtype) && max_blocks_per_seq > 0) {
       st = run_stream(op, a, dtype, sh, workspace, workspace_bytes, s);
       if (st != RG_ERR_WORKSPACE) return st;
     }
@@ -1545,7 +1713,7 @@ extern "C" int rg_paged_attention_v1_no_alloc(const void* query, const void* key
   }
   const DecodeArgs a = make_args(query, key_cache, value_cache, block_table, context_lens, output, scale, sh,
                                  kv_block_stride, kBS, 1, MODE_AUTO);
-  if (mfma_applies(a, dtype) && sh.MB > 0) {
+  if (stream_applies(a, dtype) && sh.MB > 0) {
     // The stream-K kernels of rg_paged_attention_v1 with the static scratch as their workspace.
     // Nothing in it needs clearing: every partial and segment descriptor the merge reads is
     // written earlier in the same call.

@@ -101,11 +101,13 @@ def test_config1_fp32_all_entries(device, kernels):
 CTX_RAGGED = [1, 15, 16, 17, 33, 300, 0, 511, 1024]
 
 
-@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
 def test_mfma_path_shapes(device, kernels, dt, D, G):
-    """MFMA kernel (bf16/f16, block 16): every GQA ratio, ragged contexts incl. 0 and 1."""
+    """MFMA kernels (block 16): every GQA ratio, ragged contexts incl. 0 and 1.  bf16 / f16 run
+    the grid kernel without a workspace and stream-K with one; fp32 runs the generic kernel
+    without a workspace and the fp32 stream-K tile (QK^T on fp32 MFMA) with one."""
     Hkv = 2
     inp = make_inputs(device, CTX_RAGGED, dt, H=Hkv * G, Hkv=Hkv, D=D, seed=10 * G + D)
     want = oracle_v1_plus(inp)
@@ -163,17 +165,18 @@ def _threads() -> int:
     return max(1, min(16, len(os.sched_getaffinity(0))))
 
 
-@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 def test_stream_head_dim64_many_units_per_worker(device, kernels, dt):
     """The attention of BASELINE config 5 (Llama-3.2-1B: 32 / 8 heads, head_dim 64, 128 sequences
     with its contexts U[64, 8192], block 16, 512-entry tables) through the stream-K decode,
     whose head_dim-64 units are four blocks: about 67.5 units per worker, so every worker runs
     whole rounds of its unit ring, crosses segments mid-range, and refills its 64-unit
-    block-table window at least once.  Against the oracle at 2e-2 / 1e-2."""
+    block-table window at least once (fp32: one-block units, about 270 per worker).  Against the
+    oracle at 2e-2 / 1e-2 (bf16 / f16) and 1e-4 (fp32)."""
     w = wl.config5()
     ctx = w.context_lens
     inp = _big_decode_inputs(device, ctx, dt, 32, 8, 64, seed=500, mb=512)
-    units, workers = _stream_units(ctx, 8, 4), _stream_workers(device)
+    units, workers = _stream_units(ctx, 8, 1 if dt == "f32" else 4), _stream_workers(device)
     assert units > 64 * workers, (units, workers)
     want = orc.cpu_attention_gathered(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"], dt,
                                       nthreads=_threads())
@@ -418,3 +421,16 @@ def test_config3_v2_reference_contract(device, kernels):
     want = orc.paged_attention_v2_reduce(tmp, es, ml, w.context_lens, P)
     assert_close(got, want, "bf16", "v2 partition + reduce vs oracle")
     assert_close(got, gpu_v1(kernels, inp, True), "bf16", "v2 partition + reduce vs stream-K v1")
+
+
+def test_stream_fp32_config2_shape(device, kernels):
+    """The reference's element type at config 2's shape (64 sequences, contexts U[512, 4096], 32 / 8
+    heads, head_dim 128, block 16): the fp32 stream-K tile against the oracle at 1e-4, through v1,
+    v1_plus and the combined v2."""
+    w = wl.config2()
+    inp = _big_decode_inputs(device, w.context_lens, "f32", 32, 8, 128, seed=800, mb=w.max_blocks)
+    want = orc.cpu_attention_gathered(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"], "f32",
+                                      nthreads=_threads())
+    assert_close(gpu_v1(kernels, inp, True), want, "f32", "v1 stream-K")
+    assert_close(gpu_v1(kernels, inp, True, "v1_plus"), want, "f32", "v1_plus stream-K")
+    assert_close(gpu_v2(kernels, inp, 512), want, "f32", "v2")
