@@ -7,8 +7,8 @@
 //
 // prefill_generic_kernel: one wave per (row, q-head), any dtype / head_dim /
 // block size; each lane owns 4 dims and the keys are visited in order with an
-// online softmax.  prefill_mfma_kernel (bf16/f16, GQA 4, head_dim 64/128) is the
-// MFMA tile kernel used whenever it applies.
+// online softmax.  prefill_mfma_kernel (bf16/f16, head_dim 64/128, GQA 1, 2 or a multiple
+// of 4) is the MFMA tile kernel used whenever it applies.
 #include <math.h>
 
 #include <algorithm>
@@ -122,7 +122,9 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillArgs a) {
 
 // ------------------------------------------------------------------ MFMA ----
 //
-// Tile = 32 queries of one sequence x the G = 4 q-heads of one kv-head; one wave per head.
+// Tile = 32 queries of one sequence x one q-head per wave; the 4 waves of a workgroup share the
+// K/V tiles of one kv-head: 4 heads on one 32-row tile (GQA 4 and its multiples), 2 heads on
+// two consecutive 32-row tiles (GQA 2) or one head on four (no GQA).
 // Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16 (K rows as the A
 // operand straight from the paged cache, Q^T as the B operand held in registers), so that
 // lane l owns query column l % 32 and the other half of its 32 keys sits in lane l ^ 32:
@@ -152,7 +154,7 @@ template <> struct mfma32<f16_t> {
 };
 
 constexpr int kPT = 32;               // queries per tile and keys per key tile
-constexpr int kPWaves = 4;            // one wave per q-head of the group (GQA 4)
+constexpr int kPWaves = 4;            // waves per workgroup: (heads per workgroup) x (query subtiles)
 constexpr int kPThreads = kPWaves * 64;
 constexpr int kBlk = 16;              // KV block size on the MFMA path (two blocks per key tile)
 
@@ -258,7 +260,7 @@ struct PTile {
   __device__ static __forceinline__ int vchunk(int key, int c) { return c ^ (2 * (key & 3)); }
 };
 
-template <typename T, int D>
+template <typename T, int D, int GW>
 __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kernel(
     PrefillArgs a, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_table,
@@ -266,7 +268,11 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   using MF = mfma32<T>;
   using S = uint16_t;
   using TL = PTile<D>;
-  constexpr int G = kPWaves;
+  // Heads per workgroup GW (1, 2 or 4) and query subtiles QS = 4 / GW: wave w computes head
+  // w % GW on query subtile w / GW of the unit, which has UR = 32 * QS rows.
+  static_assert(GW == 1 || GW == 2 || GW == 4, "heads per workgroup");
+  constexpr int QS = kPWaves / GW;
+  constexpr int UR = kPT * QS;
   constexpr int NKC = TL::NKC;     // 16-element d chunks = QK MFMAs per key tile
   constexpr int NDB = D / 32;      // 32-row d blocks of O^T
   // Tile copies: waves 2b and 2b+1 copy block b of the tile, each half of its K and half of
@@ -280,28 +286,47 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hkv = a.num_kv_heads;
-  // Persistent workgroups: workgroup g serves kv-head g % hkv (so, with workgroups placed on
-  // the XCDs round-robin, each head's K/V stays in few L2s); the Q = gridDim / hkv workgroups
-  // of a head share its work items, one query tile (sequence s, tile t) each, taken in snake
-  // order (round i: position i * Q + q, or i * Q + Q - 1 - q on odd rounds) over a list sorted
-  // by work, longest first.  The work key of (s, t) is base_s + t, base_s = ceil(prior_s / 32)
-  // + 1 (key tiles of its first query tile, within one tile), so every key value occurs at most
-  // once per sequence: the list is "for k = kmax .. 1, for s ascending with base_s <= k <
-  // base_s + nt_s", and position -> (k, s) needs only the count B[k] of items with key >= k
-  // (built in LDS once per workgroup) and a scan of the sequences covering k.  Snake order over
-  // a work-sorted list keeps the workgroups within a few percent of each other where rank
-  // order (all sequences' last tiles first, then the next-to-last ...) left 30 % apart.
-  // Batches beyond the LDS tables (sched_kbound == 0) keep rank order: item (rank r, seq s) =
-  // r * num_seqs + s is the r-th tile of s from its end, the last rank taking every tile
-  // further from the end (when max_query_len understates a sequence).
-  const int kvh = blockIdx.x % hkv;
-  const int nq_wg = gridDim.x / hkv;
-  const int qw = blockIdx.x / hkv;
+  const int G = a.num_heads / hkv;
+  // Head groups: GW heads of one kv-head each, H / GW of them; group grp is kv-head grp % hkv
+  // and its heads hsub * GW .. hsub * GW + GW - 1 within the kv-head (hsub = grp / hkv).
+  const int ngroups = a.num_heads / GW;
+  // Persistent workgroups: workgroup g serves head group g % ngroups (so, with workgroups
+  // placed on the XCDs round-robin, every group of a kv-head lands on the same XCD when
+  // hkv is a multiple of 8 and each head's K/V stays in few L2s); the Q = gridDim / ngroups
+  // workgroups of a group share its work items, one unit (sequence s, unit tile t of UR rows)
+  // each, taken in snake order (round i: position i * Q + q, or i * Q + Q - 1 - q on odd
+  // rounds) over a list sorted by work, longest first.  The work key of (s, t) is base_s + t,
+  // base_s = ceil(prior_s / UR) + 1 (a unit's key tiles grow by QS per key step), so every key
+  // value occurs at most once per sequence: the list is "for k = kmax .. 1, for s ascending
+  // with base_s <= k < base_s + nt_s", and position -> (k, s) needs only the count B[k] of
+  // items with key >= k (built in LDS once per workgroup) and a scan of the sequences
+  // covering k.  Snake order over a work-sorted list keeps the workgroups within a few
+  // percent of each other where rank order (all sequences' last tiles first, then the
+  // next-to-last ...) left 30 % apart.  Batches beyond the LDS tables (sched_kbound == 0) keep
+  // rank order: item (rank r, seq s) = r * num_seqs + s is the r-th unit of s from its end,
+  // the last rank taking every unit further from the end (when max_query_len understates a
+  // sequence).
+  const int grp = blockIdx.x % ngroups;
+  const int kvh = grp % hkv;
+  const int nq_wg = gridDim.x / ngroups;
+  const int qw = blockIdx.x / ngroups;
   const bool sorted = a.sched_kbound > 0;
   const int kb = a.sched_kbound;  // sorted schedule: keys live in [1, kb]
   const int table_tokens = a.max_blocks * a.block_size;
   const int H = a.num_heads;
-  const int head = kvh * G + w;
+  const int head = kvh * G + (grp / hkv) * GW + w % GW;
+  // This wave's query subtile, w / GW (0 for GW = 4).  Formed where it is used from the thread
+  // index behind an empty asm, so that it is not held in a register across the unit loop (the
+  // kernel runs at the scalar-register limit).
+  auto wave_sub = [&]() -> int {
+    if constexpr (QS == 1) {
+      return 0;
+    } else {
+      int t = threadIdx.x;
+      asm volatile("" : "+v"(t));
+      return __builtin_amdgcn_readfirstlane(t >> 6) / GW;
+    }
+  };
   const int j = lane & 31;   // query column owned by this lane
   const int hh = lane >> 5;  // which half of the k-slots
   __shared__ int sched_b[kSchedKeys + 2];
@@ -312,8 +337,8 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   // Work keys of a sequence of L rows after `prior` cached positions: base ceil(prior / 32) + 1
   // (capped at kb + 1) and the number of its query tiles whose key is within the bound.
   auto seq_keys = [&](int L, int prior) {
-    const int nt = L > 0 ? (L + kPT - 1) / kPT : 0;
-    const int bq = min((max(prior, 0) + kPT - 1) / kPT + 1, kb + 1);
+    const int nt = L > 0 ? (L + UR - 1) / UR : 0;
+    const int bq = min((max(prior, 0) + UR - 1) / UR + 1, kb + 1);
     return make_int2(bq, min(nt, kb + 1 - bq));
   };
   int n_items = a.rank_tiles * a.num_seqs;
@@ -434,7 +459,7 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     const int rank = u / a.num_seqs;
     un.row0 = cu_seqlens[un.s];
     un.L = cu_seqlens[un.s + 1] - un.row0;
-    const int nts = (un.L + kPT - 1) / kPT;
+    const int nts = (un.L + UR - 1) / UR;
     if (rank >= nts) return false;
     un.prior = min(context_lens[un.s], table_tokens) - un.L;
     un.t = nts - 1 - rank;
@@ -465,12 +490,12 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     btw1 = bt[min(2 * wbase + 64 + lane, last_blk)];
   };
   auto load_unit = [&](const Unit& un) {
-    const int q0 = un.t * kPT;
-    const int nq = min(kPT, un.L - q0);
-    const int pos_max = un.prior + q0 + nq - 1;
-    const bool row_ok = j < nq && un.prior + q0 + j >= 0;
+    const int q0 = un.t * UR;
+    const int pos_max = un.prior + q0 + min(UR, un.L - q0) - 1;
+    const int wq0 = q0 + kPT * wave_sub();  // this wave's first row
+    const bool row_ok = j < un.L - wq0 && un.prior + wq0 + j >= 0;
     if (pos_max >= 0) load_window(un, 0, pos_max / kBlk);
-    const uint4* qr = reinterpret_cast<const uint4*>(q + ((int64_t)(un.row0 + q0 + (row_ok ? j : 0)) * H + head) * D);
+    const uint4* qr = reinterpret_cast<const uint4*>(q + ((int64_t)(un.row0 + (row_ok ? wq0 + j : 0)) * H + head) * D);
 #pragma unroll
     for (int i = 0; i < NKC; ++i) qb[i] = row_ok ? qr[2 * i + hh] : make_uint4(0, 0, 0, 0);
   };
@@ -486,10 +511,11 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   if (have) load_unit(cur);
   while (have) {
   const int row0 = cur.row0;
-  const int q0 = cur.t * kPT;                  // first query of the tile (within the sequence)
-  const int nq = min(kPT, cur.L - q0);
-  const int pos_min = cur.prior + q0;
-  const int pos_max = pos_min + nq - 1;
+  const int q0 = cur.t * UR;                   // first query of the unit (within the sequence)
+  const int pos_max = cur.prior + q0 + min(UR, cur.L - q0) - 1;  // the unit's last position
+  const int wq0 = q0 + kPT * wave_sub();       // this wave's first query
+  const int nq = min(kPT, cur.L - wq0);        // this wave's rows (<= 0: none)
+  const int pos_min = cur.prior + wq0;
   const bool row_ok = j < nq && pos_min + j >= 0;
   // Rows without a position attend like the tile's last row (finite scores; written as zeros).
   const int my_pos = row_ok ? pos_min + j : pos_max;
@@ -556,7 +582,9 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   const int grp = lane >> 4;
   const int e_row = (lane >> 2) & 3;
   const int qq = lane & 3;
-  const int kt_mask = pos_min / kPT;  // tiles from here on may hold keys past a query
+  // Tiles from here on may hold keys past one of this wave's queries (a wave without rows
+  // masks against the unit's last position).
+  const int kt_mask = (QS == 1 ? pos_min : min(pos_min, pos_max)) / kPT;
   const int xor32_addr = (lane ^ 32) << 2;  // ds_bpermute address of the other half's lane
 
   // S^T = K Q^T of the tile in stage st: c[4jb + r] is key 8jb + 4hh + r for query j.  The K
@@ -791,7 +819,7 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
         const int r = i * RPR + lr / CH, c = lr % CH;
         const uint4 v = *reinterpret_cast<const uint4*>(ebuf + r * (DP * 2) + ((c ^ (r & (CH - 1))) << 4));
         if (r < nq) {
-          S* orow = static_cast<S*>(a.out) + ((int64_t)(row0 + q0 + r) * H + head) * D;
+          S* orow = static_cast<S*>(a.out) + ((int64_t)(row0 + wq0 + r) * H + head) * D;
           *reinterpret_cast<uint4*>(orow + pass * DP + 8 * c) = v;
         }
       }
@@ -859,40 +887,54 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
                 max_blocks_per_seq, num_seqs, num_tokens, 0, 0, stride, 0};
   hipStream_t s = as_stream(stream);
   const int eb = dtype_bytes(dtype);
-  if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && scale > 0.f && num_heads == 4 * num_kv_heads &&
+  // The MFMA tile kernel: bf16 / f16, head_dim 64 / 128, block 16 and a GQA ratio G of 1, 2
+  // or a multiple of 4 (GW = min(G, 4) heads per workgroup).
+  const int G = num_heads / num_kv_heads;
+  const int GW = G >= 4 ? 4 : G;
+  if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && scale > 0.f && (G == 1 || G == 2 || G % 4 == 0) &&
       block_size == kBlk &&
       (head_dim == 64 || head_dim == 128) && max_blocks_per_seq > 0 && aligned16(query) &&
       aligned16(key_cache) && aligned16(value_cache) && (stride * eb) % 16 == 0 &&
       stride * eb <= (int64_t)UINT32_MAX && aligned16(output)) {
     a.kv_stride_bytes = (uint32_t)(stride * eb);
-    // Tile ranks per sequence from max_query_len (a hint: the kernel's last rank covers any
-    // tiles beyond it; no query run is longer than num_tokens).
+    const int64_t UR = (int64_t)kPT * (kPWaves / GW);  // rows per unit
+    // Units per sequence from max_query_len (a hint: the kernel's last rank covers any units
+    // beyond it; no query run is longer than num_tokens).
     const int64_t qmax = std::min<int64_t>(std::max<int32_t>(max_query_len, 1), num_tokens);
-    a.rank_tiles = (int32_t)((qmax + kPT - 1) / kPT);
-    // Work keys are at most ceil(prior / 32) + ceil(L / 32) <= (max(table, L) + 62) / 32 with
-    // prior + L <= the table's tokens and L <= num_tokens.
-    const int64_t kbound = (std::max<int64_t>((int64_t)max_blocks_per_seq * block_size, num_tokens) + 62) / kPT + 1;
+    a.rank_tiles = (int32_t)((qmax + UR - 1) / UR);
+    // Work keys are at most ceil(prior / UR) + ceil(L / UR) <= (max(table, L) + 2 UR - 2) / UR
+    // with prior + L <= the table's tokens and L <= num_tokens.
+    const int64_t kbound =
+        (std::max<int64_t>((int64_t)max_blocks_per_seq * block_size, num_tokens) + 2 * UR - 2) / UR + 1;
     a.sched_kbound = (kbound <= kSchedKeys && num_seqs <= kSchedSeqs) ? (int32_t)kbound : 0;
-    // RG_PF_WG_PER_CU resident workgroups per CU, split evenly over the kv-heads, at most one
-    // per item.
+    // RG_PF_WG_PER_CU resident workgroups per CU, split evenly over the head groups, at most
+    // one per item.
+    const int64_t ngroups = num_heads / GW;
     const int64_t items = (int64_t)a.rank_tiles * num_seqs;
-    const int64_t per_head = std::min<int64_t>(items, std::max<int64_t>(1, RG_PF_WG_PER_CU * device_cu_count() / num_kv_heads));
-    const dim3 grid((unsigned)(per_head * num_kv_heads));
-    auto go = [&](auto tag, auto dtag) {
+    const int64_t per_group =
+        std::min<int64_t>(items, std::max<int64_t>(1, RG_PF_WG_PER_CU * device_cu_count() / ngroups));
+    const dim3 grid((unsigned)(per_group * ngroups));
+    auto go = [&](auto tag, auto dtag, auto gtag) {
       using T = decltype(tag);
       constexpr int D = decltype(dtag)::value;
-      hipLaunchKernelGGL((prefill_mfma_kernel<T, D>), grid, dim3(kPThreads), 0, s, a,
+      constexpr int W = decltype(gtag)::value;
+      hipLaunchKernelGGL((prefill_mfma_kernel<T, D, W>), grid, dim3(kPThreads), 0, s, a,
                          static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key_cache),
                          static_cast<const uint16_t*>(value_cache), block_table, context_lens, cu_seqlens);
+    };
+    auto go_gw = [&](auto tag, auto dtag) {
+      if (GW == 4) go(tag, dtag, std::integral_constant<int, 4>{});
+      else if (GW == 2) go(tag, dtag, std::integral_constant<int, 2>{});
+      else go(tag, dtag, std::integral_constant<int, 1>{});
     };
     using D64 = std::integral_constant<int, 64>;
     using D128 = std::integral_constant<int, 128>;
     if (dtype == RG_DTYPE_BF16) {
-      if (head_dim == 128) go(bf16_t{}, D128{});
-      else go(bf16_t{}, D64{});
+      if (head_dim == 128) go_gw(bf16_t{}, D128{});
+      else go_gw(bf16_t{}, D64{});
     } else {
-      if (head_dim == 128) go(f16_t{}, D128{});
-      else go(f16_t{}, D64{});
+      if (head_dim == 128) go_gw(f16_t{}, D128{});
+      else go_gw(f16_t{}, D64{});
     }
     return check_launch(op);
   }

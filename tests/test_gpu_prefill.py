@@ -37,7 +37,7 @@ def _threads() -> int:
 
 
 def _run(device, kernels, w: wl.PrefillWorkload, seed: int, check_seqs=None, max_query_len=None,
-         row_sample: bool = False):
+         row_sample: bool = False, row_stride: int = 61):
     dt = w.dtype
     rng = np.random.default_rng(seed)
     T, H, hkv, D, bs = w.num_tokens, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
@@ -60,7 +60,7 @@ def _run(device, kernels, w: wl.PrefillWorkload, seed: int, check_seqs=None, max
     got = dev_f32(out)
     orc.rope_reshape_and_cache(q, k, v, kc, vc, table.numpy(), pos, slots, dt, bs)
     if row_sample:
-        rows = sample_rows(cu)
+        rows = sample_rows(cu, stride=row_stride)
         want = orc.prefill_packed_rows(q, kc, vc, w.block_table, w.context_lens, cu, rows, w.scale, dt,
                                        nthreads=_threads())
         for s in range(w.num_seqs):
@@ -95,6 +95,39 @@ def test_prefill_config4(device, kernels):
     w = wl.config4()
     assert w.num_seqs == 12 and int(w.seq_lens.max()) == 1890
     _run(device, kernels, w, seed=w.seed, row_sample=True)
+
+
+def _gqa_workload(G: int, D: int, lens, prior, seed: int, H: int = 32, mb: int = 0) -> wl.PrefillWorkload:
+    rng = np.random.default_rng(seed)
+    lens, prior = np.asarray(lens, np.int32), np.asarray(prior, np.int32)
+    hkv = H // G
+    need = int(((prior + lens + 15) // 16).sum())
+    mb = mb or int(((prior + lens + 15) // 16).max())
+    bt = wl.assign_blocks(prior + lens, 16, need + 4, mb, rng)
+    return wl.PrefillWorkload(f"gqa{G}_d{D}", "bf16", H, hkv, D, 16, need + 4, lens, bt, seed, prior=prior)
+
+
+@pytest.mark.parametrize("G", [1, 2, 8, 16])
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_mfma_gqa_ratios(device, kernels, G, D):
+    """The MFMA prefill beyond GQA 4: one head per workgroup on four 32-row subtiles (G 1), two
+    heads on two (G 2), two or four head groups of one kv-head (G 8, 16).  Ragged units (1 to 200
+    rows, lengths around the 32 / 64 / 128-row unit sizes), prior context, a sequence whose
+    rows end inside a unit's first subtile; every row against the oracle."""
+    H = 16 if G == 1 else 32
+    w = _gqa_workload(G, D, [1, 31, 33, 64, 65, 100, 129, 200, 7], [0, 0, 40, 0, 17, 300, 0, 64, 1000],
+                      seed=100 + G + D, H=H)
+    _run(device, kernels, w, seed=200 + G + D, row_sample=True, row_stride=1)
+
+
+@pytest.mark.parametrize("G", [1, 2, 8])
+def test_prefill_mfma_gqa_long(device, kernels, G):
+    """Longer sequences (up to 1,200 rows and 2,000 cached positions) for GQA 1, 2 and 8 (64 q /
+    8 kv heads, Llama-3-70B-like), bf16 head_dim 128: many units per workgroup, every sequence
+    on a row sample against the oracle."""
+    H = 8 * G
+    w = _gqa_workload(G, 128, [1200, 700, 333, 1023, 64], [0, 2000, 5, 0, 100], seed=300 + G, H=H)
+    _run(device, kernels, w, seed=400 + G, row_sample=True)
 
 
 @pytest.mark.parametrize("max_query_len", [None, 1])
