@@ -249,6 +249,9 @@ template <> __device__ __forceinline__ float pair_sum<f16_t>(uint32_t pair, floa
 // of d chunk i (chunk 2i + half of key j) is one 256-byte run per 16 lanes at a constant
 // offset 512 i.  V: row-major [key][D] with the 16-byte chunks of row `key` XOR-swizzled by
 // 2*(key & 3) so that the transposing reads of four consecutive rows hit distinct banks.
+// (At head_dim 128 the two 16-lane groups that one LDS cycle serves then share 32 banks, a
+// 2-way conflict; XOR 4*(key & 3) removes it (bank-conflict cycles / 11) but measured no faster
+// at config 4, so the LDS is not what limits the tile loop.)
 template <int D>
 struct PTile {
   static constexpr int NKC = D / 16;
