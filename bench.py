@@ -344,6 +344,7 @@ def side_model(device, steps: int) -> dict:
     attn_ms = time_events(lambda: [model._attention(i, q, o, st) for i in range(cfg.num_hidden_layers)], steps, 2)
     kv = w.kv_bytes(cfg.num_hidden_layers, cfg.num_key_value_heads, D)
     step_bytes = weights.nbytes() + kv
+    gemm = {f"{n}x{k}": "rg_linear" if v else "hipblaslt" for (_, n, k), v in model.linear_choice.items()}
     del model, pool, weights, graph
     torch.cuda.empty_cache()
     return {"workload": w.name, "model": "llama-3.2-1b (random init, bf16)", "batch": w.batch,
@@ -351,6 +352,7 @@ def side_model(device, steps: int) -> dict:
             "step_us": round(step_ms * 1e3, 1), "eager_step_us": round(eager_ms * 1e3, 1),
             "graph_matches_eager": same, "tokens_per_s": round(w.batch / (step_ms * 1e-3), 1),
             "attention_us": round(attn_ms * 1e3, 1), "attention_share": round(attn_ms / step_ms, 4),
+            "gemm": gemm,
             "attention_GB/s": round(kv / (attn_ms * 1e-3) / 1e9, 1),
             "step_bytes": step_bytes, "step_GB/s": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
             "frac_hbm_peak": round(step_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}

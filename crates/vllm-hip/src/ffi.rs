@@ -84,6 +84,14 @@ extern "C" {
         batch_size: i32, num_heads: i32, num_kv_heads: i32, head_dim: i32, block_size: i32,
         max_blocks_per_seq: i32,
     ) -> usize;
+    /// New: the decode-step projection x . weight^T (candle's Linear, architecture.rs:38-59, 80-84).
+    pub fn rg_linear(
+        x: *const c_void, weight: *const c_void, out: *mut c_void, num_rows: i32, out_features: i32,
+        in_features: i32, x_row_stride: i64, weight_row_stride: i64, out_row_stride: i64,
+        workspace: *mut c_void, workspace_bytes: usize, dtype: i32, stream: *mut c_void,
+    ) -> c_int;
+    /// Split-K workspace of rg_linear for this shape (0: runs unsplit).
+    pub fn rg_linear_workspace_bytes(num_rows: i32, out_features: i32, in_features: i32) -> usize;
     /// Replaces launch_v1 (mod.rs:305-348).
     pub fn rg_paged_attention_v1(
         query: *const c_void, key_cache: *const c_void, value_cache: *const c_void, block_table: *const i32,

@@ -451,6 +451,33 @@ impl PagedAttentionKernels {
                                 T::DTYPE, self.stream))
     }
 
+    /// Split-K workspace bytes of launch_linear for this shape on the current device.
+    pub fn linear_workspace_bytes(&self, num_rows: i32, out_features: i32, in_features: i32) -> usize {
+        // SAFETY: a pure size computation.
+        unsafe { ffi::rg_linear_workspace_bytes(num_rows, out_features, in_features) }
+    }
+
+    /// out [num_rows, out_features] = x [num_rows, in_features] . weight^T for decode batches
+    /// (num_rows <= 128); row strides in elements.  With a workspace of linear_workspace_bytes
+    /// narrow or deep layers split K over more workgroups.
+    pub unsafe fn launch_linear<T: KvElement>(
+        &self,
+        x: &HipSlice<T>,
+        weight: &HipSlice<T>,
+        out: &mut HipSlice<T>,
+        num_rows: i32,
+        out_features: i32,
+        in_features: i32,
+        x_row_stride: i64,
+        weight_row_stride: i64,
+        out_row_stride: i64,
+        workspace: Option<&mut HipSlice<u8>>,
+    ) -> CoreResult<()> {
+        let (ws, ws_len) = workspace.map_or((std::ptr::null_mut(), 0), |w| (w.as_mut_ptr(), w.len()));
+        status(ffi::rg_linear(x.as_ptr(), weight.as_ptr(), out.as_mut_ptr(), num_rows, out_features, in_features,
+                              x_row_stride, weight_row_stride, out_row_stride, ws, ws_len, T::DTYPE, self.stream))
+    }
+
     /// out = silu(gate) * up over the fused gate/up projection output.
     pub unsafe fn launch_silu_and_mul<T: KvElement>(
         &self,

@@ -197,6 +197,27 @@ int rg_rms_norm(const void* x, void* residual, const void* weight, void* out,
 int rg_silu_and_mul(const void* gate_up, void* out, int32_t num_rows,
                     int32_t intermediate_size, int32_t dtype, void* stream);
 
+/* Decode-step projection (candle's Linear::forward on a [tokens, in_features] activation,
+ * crates/vllm-models/src/llama/architecture.rs:38-59,80-84, attention.rs:104-133):
+ *   out[m, n] = round(sum_k x[m, k] * weight[n, k]),  m < num_rows, n < out_features,
+ * bf16 / f16 operands and output, fp32 accumulation in a fixed order (deterministic).  x is
+ * [num_rows, in_features], weight [out_features, in_features] (PyTorch / candle layout),
+ * out [num_rows, out_features]; each with its own row stride in elements.  Shaped for decode
+ * batches: num_rows <= 128, out_features a multiple of 16, in_features a positive multiple of
+ * 128, x and weight rows 16-byte aligned, out rows 8-byte aligned; RG_ERR_NOT_SUPPORTED
+ * otherwise (larger batches belong to a library GEMM).  A workspace of
+ * rg_linear_workspace_bytes (16-byte aligned) lets narrow or deep layers split K over more
+ * workgroups; without it (NULL, or smaller) the call runs unsplit.  New entry: the reference
+ * runs these projections through candle's cuBLAS GEMMs. */
+int rg_linear(const void* x, const void* weight, void* out, int32_t num_rows,
+              int32_t out_features, int32_t in_features, int64_t x_row_stride,
+              int64_t weight_row_stride, int64_t out_row_stride, void* workspace,
+              size_t workspace_bytes, int32_t dtype, void* stream);
+
+/* Bytes of the split-K workspace rg_linear uses for this shape on the current device (0: the
+ * shape runs unsplit, or is not supported). */
+size_t rg_linear_workspace_bytes(int32_t num_rows, int32_t out_features, int32_t in_features);
+
 /* ------------------------------------------------------- decode, v1 -------- */
 
 /* Bytes of workspace rg_paged_attention_v1 / _v1_plus use for the given shape on the

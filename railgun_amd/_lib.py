@@ -76,6 +76,9 @@ SIGNATURES = {
     ),
     "rg_rms_norm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32, c_int32, c_void_p]),
     "rg_silu_and_mul": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p]),
+    "rg_linear": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_void_p,
+                          c_size_t, c_int32, c_void_p]),
+    "rg_linear_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "rg_paged_attention_v1_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
     "rg_paged_attention_v1": (
         c_int,

@@ -1,0 +1,326 @@
+// Skinny GEMM of a decode step's projections: C[M, N] = X[M, K] . W[N, K]^T with M <= 128
+// (one row per decode token), bf16 / fp16 operands, fp32 accumulation, one rounding of each
+// output to the operand type — candle's Linear::forward on a [tokens, in] activation
+// (crates/vllm-models/src/llama/architecture.rs:38-59, 80-84; attention.rs:104-133).
+//
+// At M = 128 these GEMMs stream their weights once and are HBM-bound (128 flops per weight
+// byte against the chip's ~310): the kernel is shaped for the weight stream.
+//
+// * v_mfma_f32_16x16x32 with W as the A operand (16 output columns n) and X^T as the B operand
+//   (16 rows m): lane (r = lane % 16, g = lane / 16) takes W[n0 + r][k + 8g .. +8] and
+//   X[m0 + r][k + 8g .. +8] from LDS.
+// * Both operands reach LDS by direct global->LDS copies of 256-byte row pieces (chunks of 128
+//   k), RG_GEMM_AHEAD chunks ahead of the MFMAs.  Copies of whole row pieces stream several
+//   times faster per CU than 16-row x 64-byte register loads in the MFMA layout, which matters
+//   for X: every workgroup reads all of it (at most 128 x K) from L2.
+// * A workgroup is 4 waves over NB n-blocks of 16 columns (4 for wide layers such as gate/up and
+//   the LM head, 1 for narrow ones such as qkv and o_proj, so that there is a workgroup per CU);
+//   the waves take one k-step of 32 each from every chunk and hold all NB x MB fragments of
+//   their steps.  The four partial sums are added through LDS in a fixed order, so the result
+//   is deterministic (graph replays reproduce eager runs bit for bit).
+#include <math.h>
+
+#include <algorithm>
+#include <type_traits>
+#include <utility>
+
+#include "rg_common.hpp"
+
+namespace rg {
+namespace {
+
+typedef __bf16 gbf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 gf16x8_t __attribute__((ext_vector_type(8)));
+typedef float gf32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T> struct gemm_mfma;
+template <> struct gemm_mfma<bf16_t> {
+  __device__ static __forceinline__ gf32x4_t run(uint4 a, uint4 b, gf32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gbf16x8_t, a),
+                                                   __builtin_bit_cast(gbf16x8_t, b), c, 0, 0, 0);
+  }
+};
+template <> struct gemm_mfma<f16_t> {
+  __device__ static __forceinline__ gf32x4_t run(uint4 a, uint4 b, gf32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(gf16x8_t, a),
+                                                  __builtin_bit_cast(gf16x8_t, b), c, 0, 0, 0);
+  }
+};
+
+constexpr int kGemmWaves = 4;
+constexpr int kGemmMaxRows = 128;
+#ifndef RG_GEMM_AHEAD
+#define RG_GEMM_AHEAD 2
+#endif
+
+struct GemmArgs {
+  const uint16_t* x;
+  const uint16_t* w;
+  uint16_t* c;
+  float* part;            // [splits][M][N] fp32 partial products when K is split
+  int32_t M, N, K;
+  int64_t ldx, ldw, ldc;  // elements between consecutive rows
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt immediate (6 bits: [3:0] and [15:14])");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// Chunks of 128 k: 256 bytes of every row of X and W.
+constexpr int kChunkK = 128;
+constexpr int kChunkBytes = 2 * kChunkK;
+constexpr int kLdsBytes = 160 * 1024;
+constexpr int kGemmThreads = 64 * kGemmWaves;
+
+// LDS ring of one instantiation: a slot holds a chunk of X (16 MB rows) then of W (16 NB rows).
+template <int NB, int MB>
+struct GemmRing {
+  static constexpr int SLOT = 16 * (MB + NB) * kChunkBytes;
+  static constexpr int FIT = kLdsBytes / SLOT;
+  // AHEAD chunks in flight; with AHEAD + 2 slots the slot a wave refills was read two chunks ago,
+  // so one barrier per chunk orders it; with AHEAD + 1 a second barrier follows the MFMAs.
+  static constexpr int AHEAD = FIT >= RG_GEMM_AHEAD + 1 ? RG_GEMM_AHEAD : FIT - 1;
+  static constexpr int SLOTS = FIT >= AHEAD + 2 ? AHEAD + 2 : AHEAD + 1;
+  static constexpr bool TWO_BARRIERS = SLOTS == AHEAD + 1;
+  static constexpr int PER = MB + NB;  // copies per wave per chunk (1 KB each: 4 rows x 256 B)
+  static constexpr int RED = NB * MB * (kGemmWaves - 1) * 1024;
+  static constexpr int BYTES = SLOTS * SLOT > RED ? SLOTS * SLOT : RED;
+  static_assert(AHEAD >= 1 && AHEAD * PER < 64, "ring does not fit");
+};
+
+// NB: 16-column n-blocks per workgroup, MB: 16-row blocks of X (M <= 16 * MB).  blockIdx.y
+// selects a split of K (chunks [y C / S, (y + 1) C / S) of the C chunks); with S > 1 the
+// workgroup writes its fp32 partial tile to a.part[y] and splitk_reduce_kernel finishes.
+//
+// X and W reach LDS by direct copies of whole 256-byte row pieces (1 KB per wave instruction:
+// 4 rows); 16-byte piece p of row R sits at piece p ^ (R % 16), so the MFMA fragment reads
+// below (16 rows at one piece) touch every bank once.  The 4 waves take one k-step of 32
+// each from every chunk, so the workgroup reads each operand byte once, and each X fragment
+// feeds NB MFMAs.  The quarters are summed through LDS in a fixed order.
+template <typename T, int NB, int MB>
+__global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
+  using MF = gemm_mfma<T>;
+  using RG = GemmRing<NB, MB>;
+  constexpr int KS = kGemmWaves;
+  constexpr int D = RG::AHEAD;
+  __shared__ __attribute__((aligned(16))) char lds[RG::BYTES];
+  const uint32_t lds_base = (uint32_t)(uintptr_t)((RG_LDS char*)lds);
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int total = a.K / kChunkK;
+  const int cb = (int)((int64_t)blockIdx.y * total / gridDim.y);
+  const int chunks = (int)((int64_t)(blockIdx.y + 1) * total / gridDim.y) - cb;
+  const int n0 = blockIdx.x * NB * 16;
+
+  // Copy sources: instruction q of wave w moves rows 4 (w * MB + q) .. +3 of X (then rows
+  // 4 (w * NB + q) .. +3 of W), lane (row 4q' + lane / 16, piece (lane % 16) ^ (row % 16)).
+  const char* xbase = reinterpret_cast<const char*>(a.x) + (int64_t)cb * kChunkBytes;
+  const char* wbase = reinterpret_cast<const char*>(a.w + (int64_t)n0 * a.ldw) + (int64_t)cb * kChunkBytes;
+  uint32_t xoff[MB], woff[NB];
+#pragma unroll
+  for (int q = 0; q < MB; ++q) {
+    const int row = 4 * (w * MB + q) + (lane >> 4);
+    xoff[q] = (uint32_t)(min(row, a.M - 1) * a.ldx * 2 + (((lane & 15) ^ (row & 15)) << 4));
+  }
+#pragma unroll
+  for (int q = 0; q < NB; ++q) {
+    const int row = 4 * (w * NB + q) + (lane >> 4);
+    woff[q] = (uint32_t)(row * a.ldw * 2 + (((lane & 15) ^ (row & 15)) << 4));
+  }
+  auto issue = [&](int c) __attribute__((always_inline)) {
+    const uint32_t slot = lds_base + (uint32_t)((c % RG::SLOTS) * RG::SLOT);
+    const int64_t kb = (int64_t)c * kChunkBytes;
+#pragma unroll
+    for (int q = 0; q < MB; ++q) lds_dma16_s(xbase + kb, xoff[q], slot + (w * MB + q) * 1024);
+#pragma unroll
+    for (int q = 0; q < NB; ++q) lds_dma16_s(wbase + kb, woff[q], slot + 16 * MB * kChunkBytes + (w * NB + q) * 1024);
+  };
+
+  gf32x4_t acc[NB][MB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[i][mb] = gf32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Fragment reads: row R of the slot's X (or W) rows, piece 4w + g of the chunk.
+  const int piece = ((4 * w + g) ^ r) << 4;
+  for (int c = 0; c < D && c < chunks; ++c) issue(c);
+  for (int c = 0; c < chunks; ++c) {
+    if (c + D < chunks) issue(c + D);
+    // Wait until at most min(D, chunks - 1 - c) chunks of this wave's copies are in flight.
+    const int ahead = min(D, chunks - 1 - c);
+    [&]<int... J>(std::integer_sequence<int, J...>) __attribute__((always_inline)) {
+      ((ahead == J ? wait_vmcnt<J * RG::PER>() : void()), ...);
+    }(std::make_integer_sequence<int, D + 1>{});
+    tile_barrier();
+    const char* slot = lds + (c % RG::SLOTS) * RG::SLOT;
+    uint4 wv[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      wv[i] = *reinterpret_cast<const uint4*>(slot + (16 * MB + 16 * i + r) * kChunkBytes + piece);
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(slot + (16 * mb + r) * kChunkBytes + piece);
+#pragma unroll
+      for (int i = 0; i < NB; ++i) acc[i][mb] = MF::run(wv[i], xv, acc[i][mb]);
+    }
+    if constexpr (RG::TWO_BARRIERS) tile_barrier();
+  }
+
+  // Fragment f = i * MB + mb is finished by wave f % KS; the other waves leave their partials of
+  // it at [f][(w - owner - 1) mod KS][lane].  Every copy has landed (the last wait was for 0).
+  tile_barrier();
+  gf32x4_t* red = reinterpret_cast<gf32x4_t*>(lds);
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int f = i * MB + mb, own = f % KS;
+      if (w != own) red[(f * (KS - 1) + (w - own - 1 + KS) % KS) * 64 + lane] = acc[i][mb];
+    }
+  __syncthreads();
+
+  // Lane (r, g) holds C[m = 16 mb + r][n0 + 16 i + 4g .. +3].
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int f = i * MB + mb;
+      const int m = 16 * mb + r;
+      if (w != f % KS) continue;
+      gf32x4_t v = acc[i][mb];
+#pragma unroll
+      for (int j = 0; j < KS - 1; ++j) v += red[(f * (KS - 1) + j) * 64 + lane];
+      if (m >= a.M) continue;
+      const int n = n0 + 16 * i + 4 * g;
+      if (gridDim.y > 1) {
+        *reinterpret_cast<gf32x4_t*>(a.part + ((int64_t)blockIdx.y * a.M + m) * a.N + n) = v;
+      } else {
+        const uint32_t lo = (uint32_t)elem<T>::from_f32(v[0]) | ((uint32_t)elem<T>::from_f32(v[1]) << 16);
+        const uint32_t hi = (uint32_t)elem<T>::from_f32(v[2]) | ((uint32_t)elem<T>::from_f32(v[3]) << 16);
+        *reinterpret_cast<uint2*>(a.c + (int64_t)m * a.ldc + n) = make_uint2(lo, hi);
+      }
+    }
+}
+
+// out[m][n] = round(sum over the S splits, in split order, of part[s][m][n]): 4 columns per lane.
+template <typename T>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a, int S) {
+  const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (idx >= (int64_t)a.M * a.N) return;
+  const int m = (int)(idx / a.N), n = (int)(idx % a.N);
+  gf32x4_t v = *reinterpret_cast<const gf32x4_t*>(a.part + idx);
+  for (int s = 1; s < S; ++s) v += *reinterpret_cast<const gf32x4_t*>(a.part + (int64_t)s * a.M * a.N + idx);
+  const uint32_t lo = (uint32_t)elem<T>::from_f32(v[0]) | ((uint32_t)elem<T>::from_f32(v[1]) << 16);
+  const uint32_t hi = (uint32_t)elem<T>::from_f32(v[2]) | ((uint32_t)elem<T>::from_f32(v[3]) << 16);
+  *reinterpret_cast<uint2*>(a.c + (int64_t)m * a.ldc + n) = make_uint2(lo, hi);
+}
+
+template <typename T, int NB>
+void launch_gemm_mb(const GemmArgs& a, int mb, int splits, hipStream_t s) {
+  const dim3 grid((unsigned)(a.N / (16 * NB)), (unsigned)splits);
+  switch (mb) {
+    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 1>), grid, dim3(kGemmThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 2>), grid, dim3(kGemmThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 4>), grid, dim3(kGemmThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 8>), grid, dim3(kGemmThreads), 0, s, a); break;
+  }
+  if (splits > 1) {
+    const int64_t quads = (int64_t)a.M * a.N / 4;
+    hipLaunchKernelGGL(splitk_reduce_kernel<T>, dim3((unsigned)ceil_div(quads, 256)), dim3(256), 0, s, a, splits);
+  }
+}
+
+template <typename T>
+void launch_gemm(const GemmArgs& a, int nb, int mb, int splits, hipStream_t s) {
+  if (nb == 4) launch_gemm_mb<T, 4>(a, mb, splits, s);
+  else if (nb == 2) launch_gemm_mb<T, 2>(a, mb, splits, s);
+  else launch_gemm_mb<T, 1>(a, mb, splits, s);
+}
+
+// Workgroup shape: n-blocks per workgroup and splits of K.  A split costs an fp32 partial tile
+// and a reduce launch, so K is split only into ranges of at least kMinSplitChunks chunks and
+// only as far as one round of workgroups (one per CU: the ring takes most of the LDS) reaches.
+// The shape that occupies the most CUs wins; ties go to the widest n-tile (fewest re-reads of
+// X).  Measured at the Llama-3.2-1B projections for 1 to 128 rows, this picks the fastest of
+// the (NB, splits) grid or one within 8 % of it.
+constexpr int kMinSplitChunks = 16;
+struct GemmPlan { int nb, splits; };
+GemmPlan gemm_plan(int N, int K, int cus) {
+  const int nblk = N / 16, chunks = K / kChunkK;
+  GemmPlan best{1, 1};
+  int64_t best_used = -1;
+  for (int nb : {4, 2, 1}) {
+    if (nblk % nb != 0) continue;
+    const int tiles = nblk / nb;
+    const int splits = std::max(1, std::min(cus / tiles, chunks / kMinSplitChunks));
+    const int64_t used = std::min<int64_t>((int64_t)tiles * splits, cus);
+    if (used > best_used) best = GemmPlan{nb, splits}, best_used = used;
+  }
+  return best;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace rg
+
+using namespace rg;
+
+extern "C" size_t rg_linear_workspace_bytes(int32_t num_rows, int32_t out_features, int32_t in_features) {
+  if (num_rows <= 0 || num_rows > kGemmMaxRows || out_features <= 0 || out_features % 16 != 0 ||
+      in_features <= 0 || in_features % kChunkK != 0) {
+    return 0;
+  }
+  const GemmPlan p = gemm_plan(out_features, in_features, device_cu_count());
+  return p.splits > 1 ? (size_t)p.splits * num_rows * out_features * sizeof(float) : 0;
+}
+
+extern "C" int rg_linear(const void* x, const void* weight, void* out, int32_t num_rows, int32_t out_features,
+                         int32_t in_features, int64_t x_row_stride, int64_t weight_row_stride,
+                         int64_t out_row_stride, void* workspace, size_t workspace_bytes, int32_t dtype,
+                         void* stream) {
+  const char* op = "linear";
+  const int32_t M = num_rows, N = out_features, K = in_features;
+  if (dtype != RG_DTYPE_BF16 && dtype != RG_DTYPE_F16) {
+    return fail(RG_ERR_NOT_SUPPORTED, "%s: bf16 or f16 operands only, got dtype %d", op, dtype);
+  }
+  if (M < 0 || N < 0 || K < 0) return fail(RG_ERR_INVALID_ARGUMENT, "%s: negative size", op);
+  if (M == 0 || N == 0) return ok();
+  if (M > kGemmMaxRows || N % 16 != 0 || K % kChunkK != 0 || K == 0) {
+    return fail(RG_ERR_NOT_SUPPORTED,
+                "%s: needs num_rows <= %d, out_features a multiple of 16 and in_features a positive "
+                "multiple of %d (got %d, %d, %d)", op, kGemmMaxRows, kChunkK, M, N, K);
+  }
+  if (!x || !weight || !out) return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
+  if (x_row_stride < K || weight_row_stride < K || out_row_stride < N) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: a row stride is shorter than its row", op);
+  }
+  if (!aligned16(x) || !aligned16(weight) || x_row_stride % 8 != 0 || weight_row_stride % 8 != 0 ||
+      (reinterpret_cast<uintptr_t>(out) & 7u) != 0 || out_row_stride % 4 != 0) {
+    return fail(RG_ERR_NOT_SUPPORTED,
+                "%s: operands and row strides must be 16-byte aligned (output 8-byte aligned)", op);
+  }
+  // The copies address a row as a 32-bit byte offset from X (from the workgroup's first W row).
+  if ((int64_t)(M - 1) * x_row_stride * 2 + 2 * (int64_t)K > INT32_MAX ||
+      (int64_t)63 * weight_row_stride * 2 + 2 * (int64_t)K > INT32_MAX) {
+    return fail(RG_ERR_NOT_SUPPORTED, "%s: row strides too large for 32-bit copy offsets", op);
+  }
+  GemmPlan plan = gemm_plan(N, K, device_cu_count());
+  const size_t need = plan.splits > 1 ? (size_t)plan.splits * M * N * sizeof(float) : 0;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))) {
+    plan.splits = 1;  // no (or too small a) workspace: one pass over K
+  }
+  GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
+             static_cast<float*>(workspace), M, N, K, x_row_stride, weight_row_stride, out_row_stride};
+  const int mb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+  hipStream_t s = as_stream(stream);
+  if (dtype == RG_DTYPE_BF16) launch_gemm<bf16_t>(a, plan.nb, mb, plan.splits, s);
+  else launch_gemm<f16_t>(a, plan.nb, mb, plan.splits, s);
+  return check_launch(op);
+}

@@ -159,7 +159,6 @@ constexpr int kPThreads = kPWaves * 64;
 constexpr int kBlk = 16;              // KV block size on the MFMA path (two blocks per key tile)
 
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
-#define RG_LDS __attribute__((address_space(3)))
 
 #ifndef RG_PF_STAGES
 #define RG_PF_STAGES 3
@@ -169,26 +168,6 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 #define RG_PF_WG_PER_CU 3
 #endif
 
-// 16 bytes per lane from global memory straight into LDS at lds_addr + 16 * lane (the
-// vector memory counter tracks completion).  Issued through asm so that the compiler does
-// not add a full vector-memory wait in front of every LDS read; the kernel orders the
-// copies itself with wait_tiles + tile_barrier.
-__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
-}
-// The same copy from a wave-uniform base plus a 32-bit per-lane byte offset.
-__device__ __forceinline__ void lds_dma16_s(const char* base, uint32_t lane_bytes, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(lane_bytes), "s"(base), "s"(lds_addr)
-               : "memory", "m0");
-}
-// Workgroup barrier without the memory fence of __syncthreads (which would also wait for
-// every prefetch in flight); the asm statements keep the compiler from moving memory
-// accesses across it.
-__device__ __forceinline__ void tile_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 constexpr int kPStages = RG_PF_STAGES;  // K/V tiles in flight (ring in LDS)
 // LDS operand reads in flight ahead of the MFMA that uses them: K (QK^T) and V (PV).
 #ifndef RG_PF_KAHEAD

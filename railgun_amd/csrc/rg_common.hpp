@@ -135,4 +135,30 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+
+// ------------------------------------------------------------ LDS staging --
+
+#define RG_LDS __attribute__((address_space(3)))
+
+// 16 bytes per lane from global memory straight into LDS at lds_addr + 16 * lane (the
+// vector memory counter tracks completion).  Issued through asm so that the compiler does
+// not add a full vector-memory wait in front of every LDS read; each kernel orders the
+// copies itself with an explicit vmcnt wait + tile_barrier.
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
+}
+// The same copy from a wave-uniform base plus a 32-bit per-lane byte offset.
+__device__ __forceinline__ void lds_dma16_s(const char* base, uint32_t lane_bytes, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(lane_bytes), "s"(base), "s"(lds_addr)
+               : "memory", "m0");
+}
+// Workgroup barrier without the memory fence of __syncthreads (which would also wait for
+// every prefetch in flight); the asm statements keep the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void tile_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 }  // namespace rg

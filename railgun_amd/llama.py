@@ -13,7 +13,11 @@ then decode slots, :mod:`railgun_amd.batch`) runs as:
   ``rg_paged_attention_v1`` for the decode rows (the reference sends prefill rows through
   the decode op, D7);
 * ``rg_rms_norm`` fuses each residual add with the next RMSNorm; ``rg_silu_and_mul`` is the
-  SwiGLU gate; the GEMMs are hipBLASLt through torch (``F.linear``).
+  SwiGLU gate;
+* the projections of decode-sized steps (at most 128 rows) run on ``rg_linear``, the skinny
+  MFMA GEMM, unless hipBLASLt (``F.linear``) measured faster for that shape on this device:
+  each (rows, out, in) shape is timed once, under graph replay, the first time an eager step
+  meets it.  Larger (prefill) steps use hipBLASLt.
 
 Every layer owns a KV pool in Railgun's fused layout ``[NB, 2, H_kv, bs, D]``
 (crates/vllm-paged-attention/src/block.rs:70,89-95); the reference shares one pool across
@@ -32,7 +36,29 @@ import torch.nn.functional as F
 
 from .batch import StepBatch
 from .kv_pool import GpuBlockPool
-from .ops import PagedAttentionKernels, rms_norm, rope_cos_sin_table, silu_and_mul
+from .ops import (LINEAR_MAX_ROWS, PagedAttentionKernels, linear, linear_workspace_bytes, rms_norm,
+                  rope_cos_sin_table, silu_and_mul)
+
+
+def _graph_us(fn, calls: int = 10, replays: int = 3) -> float:
+    """Mean device time of ``fn`` (a few launches) over graph replays."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()                                   # warm-up outside the capture (library set-up)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    g.replay()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) * 1e3 / (calls * replays)
 
 
 @dataclass(frozen=True)
@@ -168,6 +194,8 @@ class RailgunLlama:
         self.cos_sin = rope_cos_sin_table(max_pos, cfg.head_dim, cfg.rope_theta, self.device)
         self.scale = 1.0 / math.sqrt(cfg.head_dim)  # attention.rs:69-70
         self._ws = torch.empty(0, dtype=torch.uint8, device=self.device)
+        # (rows, out_features, in_features) -> True for rg_linear, False for hipBLASLt
+        self.linear_choice: dict = {}
         # Hook for measurements: called as attention_hook("begin"/"end", layer) around each
         # layer's attention kernels (None in normal use).
         self.attention_hook = None
@@ -191,6 +219,35 @@ class RailgunLlama:
             ws = self._workspace(k.v1_workspace_bytes(nd, H, Hkv, D, bs, mb))
             k.launch_v1(q[TP:], kc, vc, st.block_table[P:], st.context_lens[P:], out[TP:], self.scale, H, Hkv, D,
                         bs, mb, nd, workspace=ws if ws.numel() else None)
+
+    def _rg_linear_fits(self, x: torch.Tensor, weight: torch.Tensor) -> bool:
+        rows, k = (int(d) for d in x.shape)
+        n = int(weight.shape[0])
+        return (0 < rows <= LINEAR_MAX_ROWS and n % 16 == 0 and k % 128 == 0 and x.stride(1) == 1
+                and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 and weight.is_contiguous()
+                and weight.data_ptr() % 16 == 0 and x.dtype in (torch.bfloat16, torch.float16))
+
+    def _linear(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        """x @ weight^T on rg_linear or hipBLASLt, per the measured choice for the shape."""
+        if not self._rg_linear_fits(x, weight):
+            return F.linear(x, weight)
+        rows, k, n = int(x.shape[0]), int(x.shape[1]), int(weight.shape[0])
+        key = (rows, n, k)
+        use_rg = self.linear_choice.get(key)
+        ws_bytes = linear_workspace_bytes(rows, n, k)
+        if use_rg is None:
+            if torch.cuda.is_current_stream_capturing():
+                use_rg = True                  # no timing inside a capture: the kernel built for it
+            else:
+                out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+                ws = self._workspace(ws_bytes)
+                t_rg = _graph_us(lambda: linear(x, weight, out, ws))
+                t_blas = _graph_us(lambda: F.linear(x, weight))
+                use_rg = not t_blas < 0.95 * t_rg
+            self.linear_choice[key] = use_rg
+        if not use_rg:
+            return F.linear(x, weight)
+        return linear(x, weight, workspace=self._workspace(ws_bytes) if ws_bytes else None)
 
     def check_step(self, b: StepBatch) -> None:
         """The kernels trust their indices (as the reference's do): check them on the host."""
@@ -217,7 +274,7 @@ class RailgunLlama:
         for i, L in enumerate(w.layers):
             # input_layernorm (with the previous MLP's residual add), architecture.rs:49-50
             rms_norm(delta if delta is not None else x, L.input_norm, h, eps, residual=x if delta is not None else None)
-            qkv = F.linear(h, L.wqkv)
+            qkv = self._linear(h, L.wqkv)
             self.kernels.launch_qkv_rope_reshape_and_cache(qkv, q, self.pool.k_cache(i), self.pool.v_cache(i),
                                                           self.cos_sin, st.positions, st.slot_mapping, H, Hkv, D,
                                                           self.pool.block_size, T)
@@ -226,13 +283,13 @@ class RailgunLlama:
             self._attention(i, q, attn, st)
             if self.attention_hook:
                 self.attention_hook("end", i)
-            delta = F.linear(attn.view(T, H * D), L.wo)
+            delta = self._linear(attn.view(T, H * D), L.wo)
             # residual add + post_attention_layernorm, architecture.rs:53-57
             rms_norm(delta, L.post_norm, h, eps, residual=x)
-            silu_and_mul(F.linear(h, L.w_gate_up), act)         # LlamaMLP, architecture.rs:80-84
-            delta = F.linear(act, L.w_down)
+            silu_and_mul(self._linear(h, L.w_gate_up), act)     # LlamaMLP, architecture.rs:80-84
+            delta = self._linear(act, L.w_down)
         rms_norm(delta, w.norm, h, eps, residual=x)            # last residual add + model.norm
-        return F.linear(h.index_select(0, st.last_rows), w.lm_head)
+        return self._linear(h.index_select(0, st.last_rows), w.lm_head)
 
 
 __all__ = ["DeviceStep", "LLAMA_3_2_1B", "LayerWeights", "LlamaConfig", "LlamaWeights",

@@ -408,5 +408,43 @@ def silu_and_mul(gate_up: torch.Tensor, out: torch.Tensor) -> None:
                                          _stream(out)))
 
 
-__all__ = ["PagedAttentionKernels", "PagedAttentionOp", "RailgunError", "cache_geometry", "dtype_code",
-           "rms_norm", "rope_cos_sin_table", "silu_and_mul", "V1_MAX_CONTEXT", "V2_PARTITION_SIZE"]
+# Rows up to which rg_linear serves a projection (decode batches); larger ones go to hipBLASLt.
+LINEAR_MAX_ROWS = 128
+
+
+def linear_workspace_bytes(rows: int, out_features: int, in_features: int) -> int:
+    """Split-K workspace bytes rg_linear uses for this shape on the current device (0: unsplit)."""
+    return int(load_library().rg_linear_workspace_bytes(rows, out_features, in_features))
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tensor] = None,
+           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out [rows, N] = x [rows, K] @ weight [N, K]^T (rg_linear: the decode-step projection, fp32
+    accumulation, one rounding).  x may be a row-strided view; weight and out rows contiguous.
+    ``workspace`` (a uint8 tensor of at least linear_workspace_bytes) lets narrow or deep layers
+    split K; when omitted, one is allocated for shapes that split."""
+    _require_cuda(x, weight, out)
+    if x.dim() != 2 or weight.dim() != 2 or x.stride(1) != 1 or not weight.is_contiguous() or x.dtype != weight.dtype:
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "linear: x [rows, K] with unit column stride and a "
+                                                         "contiguous weight [N, K] of the same dtype")
+    rows, k = (int(d) for d in x.shape)
+    n = int(weight.shape[0])
+    if int(weight.shape[1]) != k:
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, f"linear: x has {k} features, weight {int(weight.shape[1])}")
+    if out is None:
+        out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+    elif tuple(out.shape) != (rows, n) or out.stride(1) != 1 or out.dtype != x.dtype:
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "linear: out must be [rows, N] with unit column stride")
+    if workspace is None:
+        ws_bytes = linear_workspace_bytes(rows, n, k)
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    ws_ptr, ws_len = (workspace.data_ptr(), workspace.numel() * workspace.element_size()) if workspace is not None \
+        else (None, 0)
+    check(load_library().rg_linear(x.data_ptr(), weight.data_ptr(), out.data_ptr(), rows, n, k, x.stride(0),
+                                   weight.stride(0), out.stride(0), ws_ptr, ws_len, dtype_code(x), _stream(x)))
+    return out
+
+
+__all__ = ["LINEAR_MAX_ROWS", "PagedAttentionKernels", "PagedAttentionOp", "RailgunError", "cache_geometry",
+           "dtype_code", "linear", "linear_workspace_bytes", "rms_norm", "rope_cos_sin_table", "silu_and_mul", "V1_MAX_CONTEXT",
+           "V2_PARTITION_SIZE"]

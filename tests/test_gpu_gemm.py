@@ -1,0 +1,93 @@
+"""rg_linear, the decode-step projection kernel, against a float32 reference on the CPU.
+
+out = x . weight^T with bf16 / f16 operands: the kernel accumulates in fp32 and rounds each
+output once, so it must equal the fp32 product of the same rounded operands within one
+rounding of the output type (plus the fp32 reordering, far smaller).  Shapes: the Llama-3.2-1B
+decode projections at 128 rows (qkv, o_proj, gate/up, down) and edge cases — rows not a
+multiple of 16, a single row, the smallest K (one 128-wide chunk, shorter than the copy ring),
+row-strided x and out, every workgroup shape (4, 2 and 1 n-blocks per workgroup).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from railgun_amd import _lib
+from railgun_amd.ops import RailgunError, linear
+
+pytestmark = pytest.mark.gpu
+
+TORCH = {"bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def _check(out: torch.Tensor, x: torch.Tensor, w: torch.Tensor, what: str) -> None:
+    ref = x.float().cpu() @ w.float().cpu().T
+    got = out.float().cpu()
+    # one rounding of the output type (2^-8 relative for bf16, 2^-11 for f16), on a floor of the
+    # typical magnitude for outputs near zero
+    rtol = 2 ** -8 if out.dtype == torch.bfloat16 else 2 ** -11
+    err = (got - ref).abs()
+    bound = rtol * ref.abs() + 1e-3 * ref.abs().mean() + 1e-6
+    assert bool((err <= bound).all()), f"{what}: max excess {float((err - bound).max()):.3g}"
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("M,N,K", [(128, 3072, 2048), (128, 2048, 2048), (128, 16384, 2048), (128, 2048, 8192),
+                                   (1, 16, 128), (7, 48, 256), (33, 4096, 128), (100, 8192, 384), (16, 2064, 512),
+                                   (1, 16384, 2048), (64, 128256, 256)])
+def test_linear_matches_fp32(device, M, N, K, dt):
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    x = torch.randn(M, K, generator=g).to(TORCH[dt]).to(device)
+    w = (0.02 * torch.randn(N, K, generator=g)).to(TORCH[dt]).to(device)
+    out = linear(x, w)
+    torch.cuda.synchronize()
+    _check(out, x, w, f"{M}x{N}x{K} {dt}")
+    again = linear(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(again.view(torch.int16), out.view(torch.int16)), "not deterministic"
+
+
+def test_linear_strided_rows(device):
+    """x a column slice of a wider activation and out a column slice of a wider buffer."""
+    g = torch.Generator().manual_seed(3)
+    wide = torch.randn(37, 2048 + 64, generator=g).to(torch.bfloat16).to(device)
+    x = wide[:, 64:]                                   # row stride 2112
+    w = (0.02 * torch.randn(512, 2048, generator=g)).to(torch.bfloat16).to(device)
+    buf = torch.full((37, 512 + 32), 7.0, dtype=torch.bfloat16, device=device)
+    out = buf[:, 16:16 + 512]
+    linear(x, w, out)
+    torch.cuda.synchronize()
+    _check(out, x, w, "strided")
+    assert bool((buf[:, :16] == 7.0).all()) and bool((buf[:, 16 + 512:] == 7.0).all()), "wrote outside out"
+
+
+def test_linear_refuses_unsupported_shapes(device):
+    w = torch.zeros(32, 64, dtype=torch.bfloat16, device=device)
+    with pytest.raises(RailgunError) as e:
+        linear(torch.zeros(129, 64, dtype=torch.bfloat16, device=device), w)   # more rows than a decode batch
+    assert e.value.code == _lib.RG_ERR_NOT_SUPPORTED
+    with pytest.raises(RailgunError):
+        linear(torch.zeros(4, 96, dtype=torch.bfloat16, device=device),
+               torch.zeros(32, 96, dtype=torch.bfloat16, device=device))     # K not a multiple of 128
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 2048, 8192), (1, 2048, 8192), (37, 3072, 4096), (128, 1024, 4096),
+                                   (16, 2048, 16384)])
+def test_linear_split_k(device, M, N, K):
+    """Narrow / deep layers split K over workgroups into an fp32 workspace and a fixed-order
+    reduce; the split result, the unsplit one (no workspace) and fp32 all agree, and repeated
+    split calls are bit-identical."""
+    from railgun_amd.ops import linear_workspace_bytes
+    ws_bytes = linear_workspace_bytes(M, N, K)
+    assert ws_bytes > 0, "K >= 4096 with few n-blocks splits on a 256-CU device"
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(device)
+    w = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).to(device)
+    ws = torch.full((ws_bytes,), 0xFF, dtype=torch.uint8, device=device)   # NaN-filled: every partial is written
+    split = linear(x, w, workspace=ws)
+    again = linear(x, w, workspace=ws)
+    unsplit = linear(x, w, workspace=torch.empty(16, dtype=torch.uint8, device=device))  # too small: one pass
+    torch.cuda.synchronize()
+    _check(split, x, w, f"split {M}x{N}x{K}")
+    _check(unsplit, x, w, f"unsplit {M}x{N}x{K}")
+    assert torch.equal(again.view(torch.int16), split.view(torch.int16)), "split K not deterministic"

@@ -141,14 +141,27 @@ CONFIGS = {
 }
 
 
+class _AlwaysRgLinear(dict):
+    """A projection choice table that sends every eligible shape to rg_linear."""
+
+    def get(self, key, default=None):
+        return True
+
+
+@pytest.mark.parametrize("gemm", ["measured", "rg_linear"])
 @pytest.mark.parametrize("name", list(CONFIGS))
-def test_llama_prefill_decode_mixed(device, kernels, name):
+def test_llama_prefill_decode_mixed(device, kernels, name, gemm):
+    """Prefill, mixed and decode steps against the CPU model.  With gemm="rg_linear" every
+    projection of the mixed (113 rows) and decode (4 rows) steps runs on rg_linear; "measured"
+    keeps the per-shape timing choice of normal use."""
     cfg = CONFIGS[name]
     bs, nb = 16, 96
     sd = _hf_state(cfg, 11)
     w = LlamaWeights.from_state_dict(cfg, sd, device)
     pool = GpuBlockPool.for_model(cfg, nb, bs, device)
     model = RailgunLlama(cfg, w, pool, kernels, max_position=4096)
+    if gemm == "rg_linear":
+        model.linear_choice = _AlwaysRgLinear()
     ref32 = llama_ref.ReferenceLlama(cfg, sd, nb, bs)
     ref16 = llama_ref.ReferenceLlama(cfg, sd, nb, bs, act_dtype=torch.bfloat16)
     rng = np.random.default_rng(7)
