@@ -50,7 +50,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-side", action="store_true", help="skip the config 3 / config 4 side figures")
-    ap.add_argument("--only", choices=["decode", "v2", "fp32", "prefill", "model", "copy"], default=None,
+    ap.add_argument("--only", choices=["decode", "v2", "fp32", "prefill", "model", "gemm", "copy"], default=None,
                     help="run one workload only and print its figures (for profiling); 'copy' is the plain "
                          "1 GiB device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
@@ -358,6 +358,38 @@ def side_model(device, steps: int) -> dict:
             "frac_hbm_peak": round(step_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def side_gemm(device) -> dict:
+    """The Llama-3.2-1B decode projections (qkv, o_proj, gate/up, down, LM head) at 1 row and at
+    config 5's 128 rows: rg_linear against hipBLASLt (torch F.linear), each the mean of 30 calls
+    over HIP-graph replays.  Weights bf16 ~ N(0, 0.02), activations N(0, 1)."""
+    import torch
+    import torch.nn.functional as F
+
+    from railgun_amd.llama import graph_us
+    from railgun_amd.ops import linear, linear_workspace_bytes
+
+    shapes = {"qkv": (3072, 2048), "o_proj": (2048, 2048), "gate_up": (16384, 2048), "down": (2048, 8192),
+              "lm_head": (128256, 2048)}
+    g = torch.Generator(device=device)
+    g.manual_seed(5)
+    out = {}
+    for rows in (1, 128):
+        per = {}
+        for name, (n, k) in shapes.items():
+            x = torch.randn((rows, k), device=device, generator=g).to(torch.bfloat16)
+            w = (0.02 * torch.randn((n, k), device=device, generator=g)).to(torch.bfloat16)
+            o = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
+            ws = torch.empty(max(16, linear_workspace_bytes(rows, n, k)), dtype=torch.uint8, device=device)
+            t_rg = graph_us(lambda: linear(x, w, o, ws))
+            t_blas = graph_us(lambda: F.linear(x, w))
+            per[name] = {"rg_linear_us": round(t_rg, 2), "hipblaslt_us": round(t_blas, 2),
+                         "rg_linear_weight_TB/s": round(n * k * 2 / (t_rg * 1e-6) / 1e12, 3)}
+            del x, w, o, ws
+        out[f"rows_{rows}"] = per
+    torch.cuda.empty_cache()
+    return out
+
+
 def copy_calibration(device, steps: int) -> dict:
     """A plain device copy of 1 GiB (torch's copy kernel): reads and writes exactly 1 GiB per
     launch, which is what the HBM counters of a profile are scaled against."""
@@ -399,6 +431,9 @@ def main() -> int:
         return 0
     if args.only == "copy":
         print(json.dumps(copy_calibration(device, args.steps)), flush=True)
+        return 0
+    if args.only == "gemm":
+        print(json.dumps(side_gemm(device)), flush=True)
         return 0
     w = wl.config2()
     log(f"[bench] config2: B={w.batch} tokens={int(w.context_lens.sum())} pool={w.num_blocks} blocks")
@@ -458,6 +493,8 @@ def main() -> int:
         result["prefill"] = side_prefill(device, gen, 10)
         log("[bench] config5 model step ...")
         result["model_step"] = side_model(device, 10)
+        log("[bench] config5 projections ...")
+        result["gemm"] = side_gemm(device)
     if not args.no_cpu:
         log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w)

@@ -13,11 +13,11 @@
 //   k), RG_GEMM_AHEAD chunks ahead of the MFMAs.  Copies of whole row pieces stream several
 //   times faster per CU than 16-row x 64-byte register loads in the MFMA layout, which matters
 //   for X: every workgroup reads all of it (at most 128 x K) from L2.
-// * A workgroup is 4 waves over NB n-blocks of 16 columns (4 for wide layers such as gate/up and
-//   the LM head, 1 for narrow ones such as qkv and o_proj, so that there is a workgroup per CU);
-//   the waves take one k-step of 32 each from every chunk and hold all NB x MB fragments of
-//   their steps.  The four partial sums are added through LDS in a fixed order, so the result
-//   is deterministic (graph replays reproduce eager runs bit for bit).
+// * A workgroup is 4 waves over a tile of 16 MB rows x 16 NB columns (gemm_plan picks MB, NB,
+//   the row tiles and splits of K per shape from a cost model of the per-CU operand stream); the
+//   waves take one k-step of 32 each from every chunk and hold all NB x MB fragments of their
+//   steps.  The four partial sums are added through LDS in a fixed order, so the result is
+//   deterministic (graph replays reproduce eager runs bit for bit).
 #include <math.h>
 
 #include <algorithm>
@@ -60,6 +60,8 @@ struct GemmArgs {
   float* part;            // [splits][M][N] fp32 partial products when K is split
   int32_t M, N, K;
   int64_t ldx, ldw, ldc;  // elements between consecutive rows
+  int32_t mtiles;         // row tiles of 16 MB rows (1: one tile holds every row)
+  int32_t xcd_map;        // 1: the row tiles of a column tile run on one XCD (see the kernel)
 };
 
 template <int N>
@@ -90,9 +92,12 @@ struct GemmRing {
   static_assert(AHEAD >= 1 && AHEAD * PER < 64, "ring does not fit");
 };
 
-// NB: 16-column n-blocks per workgroup, MB: 16-row blocks of X (M <= 16 * MB).  blockIdx.y
-// selects a split of K (chunks [y C / S, (y + 1) C / S) of the C chunks); with S > 1 the
-// workgroup writes its fp32 partial tile to a.part[y] and splitk_reduce_kernel finishes.
+// NB: 16-column n-blocks per workgroup, MB: 16-row blocks of X per row tile.  blockIdx.x is
+// a (column tile, row tile) pair: with xcd_map the a.mtiles row tiles of one column tile take
+// consecutive slots of one XCD (workgroup b runs on XCD b % 8), so that their W tile comes from
+// HBM once and from that XCD's L2 after.  blockIdx.y selects a split of K (chunks
+// [y C / S, (y + 1) C / S) of the C chunks); with S > 1 the workgroup writes its fp32 partial
+// tile to a.part[y] and splitk_reduce_kernel finishes.
 //
 // X and W reach LDS by direct copies of whole 256-byte row pieces (1 KB per wave instruction:
 // 4 rows); 16-byte piece p of row R sits at piece p ^ (R % 16), so the MFMA fragment reads
@@ -114,17 +119,30 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
   const int total = a.K / kChunkK;
   const int cb = (int)((int64_t)blockIdx.y * total / gridDim.y);
   const int chunks = (int)((int64_t)(blockIdx.y + 1) * total / gridDim.y) - cb;
-  const int n0 = blockIdx.x * NB * 16;
+  int nt = blockIdx.x, mt = 0;
+  if (a.mtiles > 1) {
+    if (a.xcd_map) {
+      const int k = blockIdx.x >> 3;
+      mt = k % a.mtiles;
+      nt = (k / a.mtiles) * 8 + (blockIdx.x & 7);
+    } else {
+      mt = blockIdx.x % a.mtiles;
+      nt = blockIdx.x / a.mtiles;
+    }
+  }
+  const int n0 = nt * NB * 16;
+  const int m0 = mt * 16 * MB;
+  const int mrows = min(16 * MB, a.M - m0);  // rows of this tile
 
   // Copy sources: instruction q of wave w moves rows 4 (w * MB + q) .. +3 of X (then rows
   // 4 (w * NB + q) .. +3 of W), lane (row 4q' + lane / 16, piece (lane % 16) ^ (row % 16)).
-  const char* xbase = reinterpret_cast<const char*>(a.x) + (int64_t)cb * kChunkBytes;
+  const char* xbase = reinterpret_cast<const char*>(a.x + (int64_t)m0 * a.ldx) + (int64_t)cb * kChunkBytes;
   const char* wbase = reinterpret_cast<const char*>(a.w + (int64_t)n0 * a.ldw) + (int64_t)cb * kChunkBytes;
   uint32_t xoff[MB], woff[NB];
 #pragma unroll
   for (int q = 0; q < MB; ++q) {
     const int row = 4 * (w * MB + q) + (lane >> 4);
-    xoff[q] = (uint32_t)(min(row, a.M - 1) * a.ldx * 2 + (((lane & 15) ^ (row & 15)) << 4));
+    xoff[q] = (uint32_t)(min(row, mrows - 1) * a.ldx * 2 + (((lane & 15) ^ (row & 15)) << 4));
   }
 #pragma unroll
   for (int q = 0; q < NB; ++q) {
@@ -185,18 +203,18 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
     }
   __syncthreads();
 
-  // Lane (r, g) holds C[m = 16 mb + r][n0 + 16 i + 4g .. +3].
+  // Lane (r, g) holds C[m0 + 16 mb + r][n0 + 16 i + 4g .. +3].
 #pragma unroll
   for (int i = 0; i < NB; ++i)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       const int f = i * MB + mb;
-      const int m = 16 * mb + r;
+      const int m = m0 + 16 * mb + r;
       if (w != f % KS) continue;
       gf32x4_t v = acc[i][mb];
 #pragma unroll
       for (int j = 0; j < KS - 1; ++j) v += red[(f * (KS - 1) + j) * 64 + lane];
-      if (m >= a.M) continue;
+      if (16 * mb + r >= mrows) continue;
       const int n = n0 + 16 * i + 4 * g;
       if (gridDim.y > 1) {
         *reinterpret_cast<gf32x4_t*>(a.part + ((int64_t)blockIdx.y * a.M + m) * a.N + n) = v;
@@ -223,7 +241,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a, int S) {
 
 template <typename T, int NB>
 void launch_gemm_mb(const GemmArgs& a, int mb, int splits, hipStream_t s) {
-  const dim3 grid((unsigned)(a.N / (16 * NB)), (unsigned)splits);
+  const dim3 grid((unsigned)(a.N / (16 * NB) * a.mtiles), (unsigned)splits);
   switch (mb) {
     case 1: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 1>), grid, dim3(kGemmThreads), 0, s, a); break;
     case 2: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 2>), grid, dim3(kGemmThreads), 0, s, a); break;
@@ -243,24 +261,52 @@ void launch_gemm(const GemmArgs& a, int nb, int mb, int splits, hipStream_t s) {
   else launch_gemm_mb<T, 1>(a, mb, splits, s);
 }
 
-// Workgroup shape: n-blocks per workgroup and splits of K.  A split costs an fp32 partial tile
-// and a reduce launch, so K is split only into ranges of at least kMinSplitChunks chunks and
-// only as far as one round of workgroups (one per CU: the ring takes most of the LDS) reaches.
-// The shape that occupies the most CUs wins; ties go to the widest n-tile (fewest re-reads of
-// X).  Measured at the Llama-3.2-1B projections for 1 to 128 rows, this picks the fastest of
-// the (NB, splits) grid or one within 8 % of it.
-constexpr int kMinSplitChunks = 16;
-struct GemmPlan { int nb, splits; };
-GemmPlan gemm_plan(int N, int K, int cus) {
+// LDS bytes of a workgroup of the (NB, MB) instantiation (GemmRing<NB, MB>::BYTES).
+int ring_bytes(int nb, int mb) {
+  const int slot = 16 * (mb + nb) * kChunkBytes;
+  const int fit = kLdsBytes / slot;
+  const int ahead = fit >= RG_GEMM_AHEAD + 1 ? RG_GEMM_AHEAD : fit - 1;
+  const int slots = fit >= ahead + 2 ? ahead + 2 : ahead + 1;
+  return std::max(slots * slot, nb * mb * (kGemmWaves - 1) * 1024);
+}
+
+// Workgroup shape: 16-column n-blocks (NB) and 16-row blocks (MB) per workgroup, row tiles
+// ceil(M / 16 MB) and splits of K, chosen by a cost model of the per-CU operand stream
+// calibrated on MI355X (a sweep of every shape at the Llama-3.2-1B projections for 1 to 128
+// rows; the model's pick is the measured best or within 10 % of it):
+//   workgroups = row tiles x column tiles x splits, R = CUs x resident workgroups per CU (LDS),
+//   stream = 3 us x ceil(workgroups / R) + 0.047 us x ceil(workgroups / CUs) x (MB + NB) x chunks / S
+//            (0.047 us per 16 rows x 128 k: 4 KB of copies),
+//   weights = N K 2 B / 5.5 TB/s,
+//   time = max(stream, weights) + 0.2 min(stream, weights) + (S > 1: 2 us + S M N 8 B / 3 TB/s for
+//          the partials and their reduce).
+// Each workgroup streams its rows of X and its columns of W once per K range; small row tiles
+// cut the X bytes of narrow layers, and the XCD-aware order keeps their re-reads of W in L2.
+struct GemmPlan { int nb, mb, mtiles, splits, xcd; };
+GemmPlan gemm_plan(int M, int N, int K, int cus) {
   const int nblk = N / 16, chunks = K / kChunkK;
-  GemmPlan best{1, 1};
-  int64_t best_used = -1;
-  for (int nb : {4, 2, 1}) {
-    if (nblk % nb != 0) continue;
-    const int tiles = nblk / nb;
-    const int splits = std::max(1, std::min(cus / tiles, chunks / kMinSplitChunks));
-    const int64_t used = std::min<int64_t>((int64_t)tiles * splits, cus);
-    if (used > best_used) best = GemmPlan{nb, splits}, best_used = used;
+  GemmPlan best{1, 1, M, 1, 0};
+  double best_t = 1e30;
+  for (int mb : {1, 2, 4, 8}) {
+    if (mb > 1 && 16 * (mb / 2) >= M) continue;  // a smaller row tile already holds every row
+    const int mtiles = (M + 16 * mb - 1) / (16 * mb);
+    for (int nb : {4, 2, 1}) {
+      if (nblk % nb != 0) continue;
+      const int resident = std::max(1, std::min(4, kLdsBytes / ring_bytes(nb, mb)));
+      for (int splits : {1, 2, 4}) {
+        if (splits > 1 && chunks / splits < 8) continue;
+        const int64_t wgs = (int64_t)mtiles * (nblk / nb) * splits;
+        const double stream = 3.0 * (double)ceil_div(wgs, (int64_t)cus * resident) +
+                              0.047 * (double)ceil_div(wgs, cus) * (mb + nb) * (chunks / splits);
+        const double weights = (double)N * K * 2 / 5.5e6;
+        double t = std::max(stream, weights) + 0.2 * std::min(stream, weights);
+        if (splits > 1) t += 2.0 + (double)splits * M * N * 8 / 3.0e6;
+        if (t < best_t - 1e-9) {
+          best_t = t;
+          best = GemmPlan{nb, mb, mtiles, splits, mtiles > 1 && (nblk / nb) % 8 == 0 ? 1 : 0};
+        }
+      }
+    }
   }
   return best;
 }
@@ -277,7 +323,7 @@ extern "C" size_t rg_linear_workspace_bytes(int32_t num_rows, int32_t out_featur
       in_features <= 0 || in_features % kChunkK != 0) {
     return 0;
   }
-  const GemmPlan p = gemm_plan(out_features, in_features, device_cu_count());
+  const GemmPlan p = gemm_plan(num_rows, out_features, in_features, device_cu_count());
   return p.splits > 1 ? (size_t)p.splits * num_rows * out_features * sizeof(float) : 0;
 }
 
@@ -311,16 +357,16 @@ extern "C" int rg_linear(const void* x, const void* weight, void* out, int32_t n
       (int64_t)63 * weight_row_stride * 2 + 2 * (int64_t)K > INT32_MAX) {
     return fail(RG_ERR_NOT_SUPPORTED, "%s: row strides too large for 32-bit copy offsets", op);
   }
-  GemmPlan plan = gemm_plan(N, K, device_cu_count());
+  GemmPlan plan = gemm_plan(M, N, K, device_cu_count());
   const size_t need = plan.splits > 1 ? (size_t)plan.splits * M * N * sizeof(float) : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))) {
     plan.splits = 1;  // no (or too small a) workspace: one pass over K
   }
   GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
-             static_cast<float*>(workspace), M, N, K, x_row_stride, weight_row_stride, out_row_stride};
-  const int mb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+             static_cast<float*>(workspace), M, N, K, x_row_stride, weight_row_stride, out_row_stride,
+             plan.mtiles, plan.xcd};
   hipStream_t s = as_stream(stream);
-  if (dtype == RG_DTYPE_BF16) launch_gemm<bf16_t>(a, plan.nb, mb, plan.splits, s);
-  else launch_gemm<f16_t>(a, plan.nb, mb, plan.splits, s);
+  if (dtype == RG_DTYPE_BF16) launch_gemm<bf16_t>(a, plan.nb, plan.mb, plan.splits, s);
+  else launch_gemm<f16_t>(a, plan.nb, plan.mb, plan.splits, s);
   return check_launch(op);
 }

@@ -40,7 +40,7 @@ from .ops import (LINEAR_MAX_ROWS, PagedAttentionKernels, linear, linear_workspa
                   rope_cos_sin_table, silu_and_mul)
 
 
-def _graph_us(fn, calls: int = 10, replays: int = 3) -> float:
+def graph_us(fn, calls: int = 10, replays: int = 3) -> float:
     """Mean device time of ``fn`` (a few launches) over graph replays."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -241,8 +241,8 @@ class RailgunLlama:
             else:
                 out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
                 ws = self._workspace(ws_bytes)
-                t_rg = _graph_us(lambda: linear(x, weight, out, ws))
-                t_blas = _graph_us(lambda: F.linear(x, weight))
+                t_rg = graph_us(lambda: linear(x, weight, out, ws))
+                t_blas = graph_us(lambda: F.linear(x, weight))
                 use_rg = not t_blas < 0.95 * t_rg
             self.linear_choice[key] = use_rg
         if not use_rg:
@@ -293,4 +293,4 @@ class RailgunLlama:
 
 
 __all__ = ["DeviceStep", "LLAMA_3_2_1B", "LayerWeights", "LlamaConfig", "LlamaWeights",
-           "RailgunLlama"]
+           "RailgunLlama", "graph_us"]

@@ -5,7 +5,9 @@ output once, so it must equal the fp32 product of the same rounded operands with
 rounding of the output type (plus the fp32 reordering, far smaller).  Shapes: the Llama-3.2-1B
 decode projections at 128 rows (qkv, o_proj, gate/up, down) and edge cases — rows not a
 multiple of 16, a single row, the smallest K (one 128-wide chunk, shorter than the copy ring),
-row-strided x and out, every workgroup shape (4, 2 and 1 n-blocks per workgroup).
+row-strided x and out, workgroup shapes of 4, 2 and 1 n-blocks and 1 to 8 row blocks, row tiles
+with a partial last tile, and column-tile counts that are and are not multiples of 8 (the
+XCD-aware and the plain tile order).
 """
 from __future__ import annotations
 
@@ -34,7 +36,8 @@ def _check(out: torch.Tensor, x: torch.Tensor, w: torch.Tensor, what: str) -> No
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("M,N,K", [(128, 3072, 2048), (128, 2048, 2048), (128, 16384, 2048), (128, 2048, 8192),
                                    (1, 16, 128), (7, 48, 256), (33, 4096, 128), (100, 8192, 384), (16, 2064, 512),
-                                   (1, 16384, 2048), (64, 128256, 256)])
+                                   (1, 16384, 2048), (64, 128256, 256), (128, 192, 2048), (100, 8192, 2048),
+                                   (77, 1040, 1024)])
 def test_linear_matches_fp32(device, M, N, K, dt):
     g = torch.Generator().manual_seed(M * 7 + N + K)
     x = torch.randn(M, K, generator=g).to(TORCH[dt]).to(device)
@@ -71,7 +74,7 @@ def test_linear_refuses_unsupported_shapes(device):
                torch.zeros(32, 96, dtype=torch.bfloat16, device=device))     # K not a multiple of 128
 
 
-@pytest.mark.parametrize("M,N,K", [(128, 2048, 8192), (1, 2048, 8192), (37, 3072, 4096), (128, 1024, 4096),
+@pytest.mark.parametrize("M,N,K", [(128, 2048, 8192), (1, 2048, 8192), (64, 2048, 8192), (8, 512, 8192),
                                    (16, 2048, 16384)])
 def test_linear_split_k(device, M, N, K):
     """Narrow / deep layers split K over workgroups into an fp32 workspace and a fixed-order
@@ -79,7 +82,7 @@ def test_linear_split_k(device, M, N, K):
     split calls are bit-identical."""
     from railgun_amd.ops import linear_workspace_bytes
     ws_bytes = linear_workspace_bytes(M, N, K)
-    assert ws_bytes > 0, "K >= 4096 with few n-blocks splits on a 256-CU device"
+    assert ws_bytes > 0, "deep, narrow layers split K on a 256-CU device"
     g = torch.Generator().manual_seed(M + N + K)
     x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(device)
     w = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).to(device)
