@@ -9,10 +9,10 @@
 //   MODE_AUTO   : MODE_FINAL for sequences that fit one partition, MODE_PARTIAL
 //                 otherwise; the merge kernel then skips the single-partition ones.
 //
-// * decode_mfma_kernel (bf16/f16, head_dim 64/128, block_size 16): the GQA
-//   group's query heads are replicated into the 16 rows of a
-//   v_mfma_f32_16x16x32 A operand, each 16-token K block is the B operand, so
-//   one K/V block is read from HBM once per kv-head for all of its q-heads.
+// * decode_mfma_kernel (bf16/f16, head_dim 64/128/256, block_size 16 << j; 16-token
+//   sub-blocks of larger blocks): the GQA group's query heads are replicated into the 16 rows
+//   of a v_mfma_f32_16x16x32 A operand, each 16-token K sub-block is the B operand, so one K/V
+//   block is read from HBM once per kv-head for all of its q-heads.
 //   Scores go through an exp2 online softmax whose max is shared by the whole
 //   wave (DPP row reductions), P.V runs on the VALU in fp32 with 16-byte V
 //   loads, and four waves split the partition's blocks and merge through LDS.
@@ -61,6 +61,10 @@ struct DecodeArgs {
   int32_t partition_size;  // tokens per partition
   int64_t kv_stride;       // elements between blocks
   int32_t mode;
+  // block_size = 16 << bs_shift for the MFMA and stream-K kernels (-1: another size).  They work
+  // in 16-token sub-blocks: sub-block b of a sequence is rows 16 (b & mask) .. of the kv-head's
+  // slice of physical block table[b >> bs_shift].
+  int32_t bs_shift;
 };
 
 __device__ __forceinline__ int num_parts_for(int ctx, int P) { return (ctx + P - 1) / P; }
@@ -572,7 +576,7 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  const int ctx = max(0, min(context_lens[s], a.max_blocks * kBS));
+  const int ctx = max(0, min(context_lens[s], a.max_blocks * a.block_size));
   const int P = a.partition_size;
   const int np_s = min(num_parts_for(ctx, P), a.num_partitions);
   const bool final_out = a.mode == MODE_FINAL || (a.mode == MODE_AUTO && np_s <= 1);
@@ -586,7 +590,7 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
     return;
   }
 
-  // Blocks of this partition; wave w takes blocks b0+w, b0+w+kWaves, ...
+  // 16-token sub-blocks of this partition; wave w takes sub-blocks b0+w, b0+w+kWaves, ...
   const int nblk_ctx = (ctx + kBS - 1) / kBS;
   const int b0 = p * (P / kBS);
   const int b1 = min(nblk_ctx, b0 + P / kBS);
@@ -597,9 +601,11 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
   tile.load_q(q_ptr + ((int64_t)s * H + (int64_t)kvh * G) * D);
   tile.reset();
   const int32_t* bt = block_table + (int64_t)s * a.max_blocks;
-  const int64_t head_off = (int64_t)kvh * kBS * D;
+  const int64_t head_off = (int64_t)kvh * a.block_size * D;
+  const int sh = a.bs_shift, sub_mask = (1 << sh) - 1;
   auto load_block = [&](int j, uint4 (&kk)[NK], uint4 (&vv)[NV]) {
-    const int64_t off = (int64_t)bt[b0 + w + j * kWaves] * a.kv_stride + head_off;
+    const int lb = b0 + w + j * kWaves;
+    const int64_t off = (int64_t)bt[lb >> sh] * a.kv_stride + head_off + (int64_t)(lb & sub_mask) * (kBS * D);
     tile.load(kc + off, vc + off, kk, vv);
   };
 
@@ -715,8 +721,9 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 // ring, which G >= 8 fills to the limit).
 template <int D, int G>
 constexpr int sk_bpu() { return D <= 64 ? (G >= 8 ? 2 : RG_SK_BPU_D64) : RG_SK_BPU_D128; }
+// head_dim 256 (bf16 / f16): one-block units of 16 KB (8 KB of K, 8 KB of V) two deep.
 template <int D, int G>
-constexpr int sk_prefetch() { return D <= 64 ? RG_SK_PREFETCH_D64 : RG_SK_PREFETCH; }
+constexpr int sk_prefetch() { return D <= 64 ? RG_SK_PREFETCH_D64 : D >= 256 ? 2 : RG_SK_PREFETCH; }
 // fp32 rows are twice as long: one-block units (8 KB of K and of V at head_dim 128), one in
 // flight ahead at head_dim 128 and two at head_dim 64 (the register ring of the 16-bit tiles'
 // depth would not fit).
@@ -744,13 +751,16 @@ struct StreamArgs {
   int32_t batch;
   int32_t num_workers;
   int64_t kv_stride;
+  int32_t table_stride;  // entries per block-table row (max_blocks counts 16-token sub-blocks)
+  int32_t bs_shift;      // block_size = 16 << bs_shift
 };
 
 __device__ __forceinline__ int64_t worker_start(int64_t k, int64_t U, int64_t W) { return k * U / W; }
 // The worker whose range contains unit u (the last k with worker_start(k) <= u).
 __device__ __forceinline__ int64_t worker_of(int64_t u, int64_t U, int64_t W) { return ((u + 1) * W - 1) / U; }
 
-// Blocks of sequence s: ceil(ctx/16) per kv-head (context clamped to the table row).
+// 16-token sub-blocks of sequence s: ceil(ctx/16) per kv-head (context clamped to the table
+// row, max_blocks of them).
 __device__ __forceinline__ int seq_blocks(const int32_t* ctxl, int s, int max_blocks) {
   const int c = max(0, min(ctxl[s], max_blocks * kBS));
   return (c + kBS - 1) / kBS;
@@ -885,8 +895,9 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
     }
   };
   // Block numbers of the worker's units in a register window: lane i holds the blocks of
-  // unit wbase + i (units counted from u0; btw[r] is block r of the unit, and a short last
-  // unit repeats its first block, which the step masks).  Filling it walks each lane's cursor
+  // unit wbase + i (units counted from u0; btw[r] is sub-block r of the unit as
+  // (physical block << bs_shift) | sub-block within it, and a short last unit repeats its
+  // first sub-block, which the step masks).  Filling it walks each lane's cursor
   // i units on (a few steps: ranges cross few segments) and reads all 64 units' entries with
   // BPU loads, so the per-unit address needs a v_readlane instead of a scalar load waited on
   // in the loop.
@@ -905,12 +916,12 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
       }
     }
     const bool live = base + lane < u1 - u0 && ss < a.batch;
-    const int32_t* row = block_table + (int64_t)(live ? ss : 0) * a.max_blocks;
+    const int32_t* row = block_table + (int64_t)(live ? ss : 0) * a.table_stride;
     const int nbk = live ? seq_blocks(context_lens, ss, a.max_blocks) : 0;
 #pragma unroll
     for (int r = 0; r < BPU; ++r) {
       const int bk = b * BPU + r < nbk ? b * BPU + r : b * BPU;
-      btw[r] = live ? row[bk] : 0;
+      btw[r] = live ? (row[bk >> a.bs_shift] << a.bs_shift) | (bk & ((1 << a.bs_shift) - 1)) : 0;
     }
   };
   // ldi: index of the unit cursor c points at.  A window refill (every 64 units) waits for
@@ -922,11 +933,14 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
       fill_window(c, ldi);
       __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
     }
-    const int64_t head = (int64_t)c.kvh * kBS * D;
+    const int64_t head = (int64_t)c.kvh * (kBS << a.bs_shift) * D;
+    auto off = [&](int e) __attribute__((always_inline)) {
+      return (int64_t)(e >> a.bs_shift) * a.kv_stride + head + (int64_t)(e & ((1 << a.bs_shift) - 1)) * (kBS * D);
+    };
     [&]<int... R>(std::integer_sequence<int, R...>) __attribute__((always_inline)) {
-      ((t.template load_part<BPU, R>(kc + (int64_t)__builtin_amdgcn_readlane(btw[R], (int)(ldi - wbase)) * a.kv_stride + head,
-                                     vc + (int64_t)__builtin_amdgcn_readlane(btw[R], (int)(ldi - wbase)) * a.kv_stride + head,
-                                     kk, vv)), ...);
+      ((t.template load_part<BPU, R>(kc + off(__builtin_amdgcn_readlane(btw[R], (int)(ldi - wbase))),
+                                     vc + off(__builtin_amdgcn_readlane(btw[R], (int)(ldi - wbase))), kk, vv)),
+       ...);
     }(std::make_integer_sequence<int, BPU>{});
   };
 
@@ -1039,7 +1053,7 @@ __global__ __launch_bounds__(64 * G) void decode_stream_merge_kernel(StreamArgs 
                                                                     const int32_t* __restrict__ context_lens) {
   using S = typename elem<T>::storage;
   constexpr int PER = D / 64;  // dims per lane
-  static_assert(PER == 1 || PER == 2, "head_dim 64 or 128");
+  static_assert(PER == 1 || PER == 2 || PER == 4, "head_dim 64, 128 or 256");
   const int kvh = blockIdx.x;
   const int s = blockIdx.y;
   const int h = threadIdx.x >> 6;
@@ -1067,7 +1081,13 @@ __global__ __launch_bounds__(64 * G) void decode_stream_merge_kernel(StreamArgs 
     const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + pi * (2 * G) + 2 * h);
     const float* pa = a.part_acc + pi * (G * D) + h * D + lane * PER;
     float v[PER];
-    if constexpr (PER == 2) {
+    if constexpr (PER == 4) {
+      const float4 t = *reinterpret_cast<const float4*>(pa);
+      v[0] = t.x;
+      v[1] = t.y;
+      v[2] = t.z;
+      v[3] = t.w;
+    } else if constexpr (PER == 2) {
       const float2 t = *reinterpret_cast<const float2*>(pa);
       v[0] = t.x;
       v[1] = t.y;
@@ -1225,7 +1245,12 @@ bool launch_mfma_g(const DecodeArgs& a, int G, dim3 grid, hipStream_t s) {
     case 2: launch_mfma<T, D, 2>(a, grid, s); return true;
     case 4: launch_mfma<T, D, 4>(a, grid, s); return true;
     case 8: launch_mfma<T, D, 8>(a, grid, s); return true;
-    case 16: launch_mfma<T, D, 16>(a, grid, s); return true;
+    case 16:
+      if constexpr (D < 256) {
+        launch_mfma<T, D, 16>(a, grid, s);
+        return true;
+      }
+      return false;
     default: return false;
   }
 }
@@ -1233,19 +1258,26 @@ bool launch_mfma_g(const DecodeArgs& a, int G, dim3 grid, hipStream_t s) {
 bool mfma_applies(const DecodeArgs& a, int32_t dtype) {
   const int G = a.num_heads / a.num_kv_heads;
   const int eb = dtype_bytes(dtype);
-  return (dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && a.block_size == kBS &&
-         (a.head_dim == 64 || a.head_dim == 128) &&
+  return (dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && a.bs_shift >= 0 &&
+         (a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256) &&
          (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && a.partition_size % kBS == 0 &&
          aligned16(a.q) && aligned16(a.k_cache) && aligned16(a.v_cache) &&
          (a.kv_stride * eb) % 16 == 0 &&
          (a.out == nullptr || (reinterpret_cast<uintptr_t>(a.out) & 3u) == 0);
 }
 
-// The stream-K decode: the MFMA shapes in bf16 / f16, and the same shapes in fp32.
+// The grid kernel: the MFMA shapes but head_dim 256 with 16 q-heads per kv-head (whose
+// accumulators and two K/V blocks in flight exceed the registers of a wave).
+bool grid_mfma_applies(const DecodeArgs& a, int32_t dtype) {
+  return mfma_applies(a, dtype) && !(a.head_dim == 256 && a.num_heads / a.num_kv_heads == 16);
+}
+
+// The stream-K decode: the MFMA shapes in bf16 / f16, and the same shapes in fp32 (head_dim 64
+// or 128).
 bool stream_applies(const DecodeArgs& a, int32_t dtype) {
   if (dtype != RG_DTYPE_F32) return mfma_applies(a, dtype);
   const int G = a.num_heads / a.num_kv_heads;
-  return a.block_size == kBS && (a.head_dim == 64 || a.head_dim == 128) &&
+  return a.bs_shift >= 0 && (a.head_dim == 64 || a.head_dim == 128) &&
          (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && aligned16(a.q) && aligned16(a.k_cache) &&
          aligned16(a.v_cache) && (a.kv_stride * 4) % 16 == 0 && (a.out == nullptr || (reinterpret_cast<uintptr_t>(a.out) & 3u) == 0);
 }
@@ -1254,14 +1286,16 @@ bool stream_applies(const DecodeArgs& a, int32_t dtype) {
 int run_partition(const char* op, const DecodeArgs& a, int32_t dtype, int32_t batch,
                   int32_t grid_parts, hipStream_t s) {
   if (batch == 0 || grid_parts == 0) return ok();
-  if (mfma_applies(a, dtype)) {
+  if (grid_mfma_applies(a, dtype)) {
     const int G = a.num_heads / a.num_kv_heads;
     const dim3 grid(grid_parts, a.num_kv_heads, batch);
     if (dtype == RG_DTYPE_BF16) {
-      if (a.head_dim == 128) launch_mfma_g<bf16_t, 128>(a, G, grid, s);
+      if (a.head_dim == 256) launch_mfma_g<bf16_t, 256>(a, G, grid, s);
+      else if (a.head_dim == 128) launch_mfma_g<bf16_t, 128>(a, G, grid, s);
       else launch_mfma_g<bf16_t, 64>(a, G, grid, s);
     } else {
-      if (a.head_dim == 128) launch_mfma_g<f16_t, 128>(a, G, grid, s);
+      if (a.head_dim == 256) launch_mfma_g<f16_t, 256>(a, G, grid, s);
+      else if (a.head_dim == 128) launch_mfma_g<f16_t, 128>(a, G, grid, s);
       else launch_mfma_g<f16_t, 64>(a, G, grid, s);
     }
     return check_launch(op);
@@ -1305,6 +1339,9 @@ DecodeArgs make_args(const void* q, const void* kc, const void* vc, const int32_
   a.partition_size = P;
   a.kv_stride = kv_stride ? kv_stride : (int64_t)sh.Hkv * sh.bs * sh.D;
   a.mode = mode;
+  a.bs_shift = -1;
+  for (int j = 0; j <= 4; ++j)
+    if (sh.bs == (kBS << j)) a.bs_shift = j;
   return a;
 }
 
@@ -1341,7 +1378,7 @@ int32_t v1_num_partitions(const Shape& sh) {
 
 int32_t stream_workers(const Shape& sh) {
   const int64_t want = (int64_t)device_cu_count() * RG_SK_WAVES_PER_CU;
-  const int64_t units_max = (int64_t)sh.B * sh.Hkv * std::max(sh.MB, 1);
+  const int64_t units_max = (int64_t)sh.B * sh.Hkv * std::max(sh.MB, 1) * std::max(sh.bs / kBS, 1);
   return (int32_t)std::max<int64_t>(1, std::min(want, units_max));
 }
 
@@ -1402,16 +1439,20 @@ int run_stream(const char* op, const DecodeArgs& a, int32_t dtype, const Shape& 
   sa.scale_log2 = a.scale_log2;
   sa.num_heads = sh.H;
   sa.num_kv_heads = sh.Hkv;
-  sa.max_blocks = sh.MB;
+  sa.max_blocks = sh.MB << a.bs_shift;
   sa.batch = sh.B;
   sa.num_workers = workers;
   sa.kv_stride = a.kv_stride;
+  sa.table_stride = sh.MB;
+  sa.bs_shift = a.bs_shift;
   const int G = sh.H / sh.Hkv;
   if (dtype == RG_DTYPE_BF16) {
-    if (sh.D == 128) launch_stream_g<bf16_t, 128>(sa, a, G, s);
+    if (sh.D == 256) launch_stream_g<bf16_t, 256>(sa, a, G, s);
+    else if (sh.D == 128) launch_stream_g<bf16_t, 128>(sa, a, G, s);
     else launch_stream_g<bf16_t, 64>(sa, a, G, s);
   } else if (dtype == RG_DTYPE_F16) {
-    if (sh.D == 128) launch_stream_g<f16_t, 128>(sa, a, G, s);
+    if (sh.D == 256) launch_stream_g<f16_t, 256>(sa, a, G, s);
+    else if (sh.D == 128) launch_stream_g<f16_t, 128>(sa, a, G, s);
     else launch_stream_g<f16_t, 64>(sa, a, G, s);
   } else {
     if (sh.D == 128) launch_stream_g<f32_t, 128>(sa, a, G, s);

@@ -148,16 +148,16 @@ def _stream_units(ctx, hkv: int, blocks_per_unit: int) -> int:
     return int(((blocks + blocks_per_unit - 1) // blocks_per_unit).sum()) * hkv
 
 
-def _big_decode_inputs(device, ctx, dt, H, Hkv, D, seed, mb):
+def _big_decode_inputs(device, ctx, dt, H, Hkv, D, seed, mb, bs=16):
     rng = np.random.default_rng(seed)
     ctx = np.asarray(ctx, np.int32)
-    need = int(((ctx.astype(np.int64) + 15) // 16).sum())
+    need = int(((ctx.astype(np.int64) + bs - 1) // bs).sum())
     nb = need + 64
-    bt = wl.assign_blocks(ctx, 16, nb, mb, rng)
-    dkc, kc = _device_normal((nb, Hkv, 16, D), dt, seed + 1, device)
-    dvc, vc = _device_normal((nb, Hkv, 16, D), dt, seed + 2, device)
+    bt = wl.assign_blocks(ctx, bs, nb, mb, rng)
+    dkc, kc = _device_normal((nb, Hkv, bs, D), dt, seed + 1, device)
+    dvc, vc = _device_normal((nb, Hkv, bs, D), dt, seed + 2, device)
     dq, q = _device_normal((len(ctx), H, D), dt, seed + 3, device)
-    return dict(ctx=ctx, bt=bt, q=q, kc=kc, vc=vc, H=H, Hkv=Hkv, D=D, bs=16, mb=mb, dt=dt, scale=1.0 / math.sqrt(D),
+    return dict(ctx=ctx, bt=bt, q=q, kc=kc, vc=vc, H=H, Hkv=Hkv, D=D, bs=bs, mb=mb, dt=dt, scale=1.0 / math.sqrt(D),
                 dq=dq, dkc=dkc, dvc=dvc, dbt=i32(bt, device), dctx=i32(ctx, device))
 
 
@@ -233,15 +233,74 @@ def test_workspace_reused_across_calls(device, kernels):
         assert_close(dev_f32(out), wants[i], "bf16", f"shape {i}")
 
 
-@pytest.mark.parametrize("dt,D,bs,G", [("f32", 128, 16, 4), ("bf16", 96, 16, 4), ("bf16", 256, 16, 2),
-                                       ("f16", 32, 8, 3), ("bf16", 128, 32, 4), ("f32", 256, 8, 1)])
+@pytest.mark.parametrize("dt,D,bs,G", [("f32", 128, 16, 4), ("bf16", 96, 16, 4), ("bf16", 256, 24, 2),
+                                       ("f16", 32, 8, 3), ("bf16", 128, 24, 4), ("f32", 256, 8, 1),
+                                       ("bf16", 128, 8, 4)])
 def test_generic_path_shapes(device, kernels, dt, D, bs, G):
-    """Shapes outside the MFMA kernel (fp32, head_dim 32/96/256, block 8/32, GQA 3)."""
+    """Shapes outside the MFMA kernels (fp32 without a workspace, head_dim 32/96/256, block 8 / 24,
+    GQA 3)."""
     inp = make_inputs(device, [1, 7, 40, 129, 0], dt, H=2 * G, Hkv=2, D=D, bs=bs, seed=D + bs + G)
     want = oracle_v1_plus(inp)
     for ws in (False, True):
         assert_close(gpu_v1(kernels, inp, ws), want, dt, f"ws={ws}")
     assert_close(gpu_v2(kernels, inp, 2 * bs), want, dt, "v2")
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("dt,D,G", [("bf16", 128, 4), ("f16", 64, 8), ("f32", 128, 4), ("bf16", 64, 1)])
+def test_mfma_path_block_sizes(device, kernels, dt, D, G, bs):
+    """Block sizes 16 << j on the MFMA grid and stream-K kernels, which work in 16-token
+    sub-blocks of each block: ragged contexts (0, 1, sub-block and block boundaries), v1
+    without a workspace (grid kernel; generic for fp32), with one (stream-K), v2 with P = 2 bs,
+    and the fused pool layout."""
+    Hkv = 2
+    for fused in (False, True):
+        inp = make_inputs(device, CTX_RAGGED + [bs - 1, bs, bs + 1, 3 * bs + 16], dt, H=Hkv * G, Hkv=Hkv, D=D,
+                          bs=bs, seed=bs + D + G, fused=fused)
+        want = oracle_v1_plus(inp)
+        for ws in (False, True):
+            assert_close(gpu_v1(kernels, inp, ws), want, dt, f"fused={fused} ws={ws}")
+        assert_close(gpu_v2(kernels, inp, 2 * bs), want, dt, f"fused={fused} v2")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
+def test_mfma_head_dim256(device, kernels, dt, G):
+    """head_dim 256 on the MFMA kernels (grid without a workspace, except G = 16, which the
+    generic kernel serves; stream-K with one; v2) over ragged contexts, 16- and 32-token blocks."""
+    Hkv = 2
+    for bs in (16, 32):
+        inp = make_inputs(device, CTX_RAGGED, dt, H=Hkv * G, Hkv=Hkv, D=256, bs=bs, seed=256 + G + bs)
+        want = oracle_v1_plus(inp)
+        for ws in (False, True):
+            assert_close(gpu_v1(kernels, inp, ws), want, dt, f"bs={bs} ws={ws}")
+        assert_close(gpu_v2(kernels, inp, 64), want, dt, f"bs={bs} v2")
+
+
+def test_stream_head_dim256_many_units(device, kernels):
+    """head_dim 256, 16 / 4 heads (Gemma-like grouping), 96 sequences with contexts U[64, 4096],
+    bf16: tens of one-block units per worker, window refills, segments crossed mid range."""
+    rng = np.random.default_rng(901)
+    ctx = rng.integers(64, 4096, 96, endpoint=True).astype(np.int32)
+    inp = _big_decode_inputs(device, ctx, "bf16", 16, 4, 256, seed=901, mb=256)
+    assert _stream_units(ctx, 4, 1) > 16 * _stream_workers(device)
+    want = orc.cpu_attention_gathered(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"], "bf16",
+                                      nthreads=_threads())
+    assert_close(gpu_v1(kernels, inp, True), want, "bf16", "D=256")
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+def test_stream_block_sizes_many_units(device, kernels, bs):
+    """Stream-K with 32- and 64-token blocks at a config-5-like load (128 sequences, contexts
+    U[64, 8192], 32 / 8 heads, head_dim 64, bf16): many units per worker, segments crossed mid
+    range, block-table window refills, each window entry a (block, sub-block) pair."""
+    rng = np.random.default_rng(700 + bs)
+    ctx = rng.integers(64, 8192, 128, endpoint=True).astype(np.int32)
+    inp = _big_decode_inputs(device, ctx, "bf16", 32, 8, 64, seed=700 + bs, mb=8192 // bs, bs=bs)
+    assert _stream_units(ctx, 8, 4) > 64 * _stream_workers(device)
+    want = orc.cpu_attention_gathered(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"], "bf16",
+                                      nthreads=_threads())
+    assert_close(gpu_v1(kernels, inp, True), want, "bf16", f"bs={bs}")
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
@@ -274,26 +333,29 @@ def test_tail_rows_never_leak(device, kernels, dt):
     assert np.isfinite(gpu_v2(kernels, inp, 32)).all()
 
 
-def test_v2_partition_contract(device, kernels):
-    """tmp_out / exp_sums / max_logits of v2_partition (fp32, P=256) against the oracle's."""
-    inp = make_inputs(device, [100, 256, 257, 700, 0], "f32", H=8, Hkv=2, D=64, seed=5)
+@pytest.mark.parametrize("dt,bs", [("f32", 16), ("bf16", 32)])
+def test_v2_partition_contract(device, kernels, dt, bs):
+    """tmp_out / exp_sums / max_logits of v2_partition (P=256) against the oracle's: fp32 (the
+    generic kernel) and bf16 with 32-token blocks (the MFMA grid kernel in partial mode)."""
+    inp = make_inputs(device, [100, 256, 257, 700, 0], dt, H=8, Hkv=2, D=64, bs=bs, seed=5)
     P, NP = 256, 3
     B = len(inp["ctx"])
     tmp, es, ml = orc.paged_attention_v2_partition(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"],
-                                                   inp["scale"], "f32", NP, P)
+                                                   inp["scale"], dt, NP, P)
     d_tmp = torch.zeros((B, 8, NP, 64), dtype=torch.float32, device=device)
     d_es = torch.zeros((B, 8, NP), dtype=torch.float32, device=device)
     d_ml = torch.zeros((B, 8, NP), dtype=torch.float32, device=device)
     kernels.launch_v2_partition(inp["dq"], inp["dkc"], inp["dvc"], inp["dbt"], inp["dctx"], d_tmp, d_es, d_ml,
-                                None, inp["scale"], 8, 2, 64, 16, inp["mb"], NP, B, P)
+                                None, inp["scale"], 8, 2, 64, bs, inp["mb"], NP, B, P)
     torch.cuda.synchronize()
-    np.testing.assert_allclose(dev_f32(d_ml), ml, atol=1e-5, rtol=1e-5)
-    np.testing.assert_allclose(dev_f32(d_es), es, atol=1e-4, rtol=1e-4)
-    np.testing.assert_allclose(dev_f32(d_tmp), tmp, atol=1e-4, rtol=1e-4)
-    out = torch.zeros((B, 8, 64), dtype=torch.float32, device=device)
+    tol = 1e-4 if dt == "f32" else 2e-2
+    np.testing.assert_allclose(dev_f32(d_ml), ml, atol=tol / 10, rtol=tol / 10)
+    np.testing.assert_allclose(dev_f32(d_es), es, atol=tol, rtol=tol)
+    np.testing.assert_allclose(dev_f32(d_tmp), tmp, atol=tol, rtol=tol)
+    out = torch.zeros((B, 8, 64), dtype=TORCH_DT[dt], device=device)
     kernels.launch_v2_reduce(out, d_es, d_ml, d_tmp, inp["dctx"], None, 8, 64, NP, B, P)
     torch.cuda.synchronize()
-    assert_close(dev_f32(out), oracle_v1_plus(inp), "f32")
+    assert_close(dev_f32(out), oracle_v1_plus(inp), dt)
 
 
 def _config_pool(w, device, seed_offset=0):
