@@ -31,7 +31,8 @@ BF16_MFMA_PEAK_TFLOPS = 2516.6
 
 def measured_traffic(key: str):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (copy-calibrated) for
-    this workload, as committed in profiles/traffic.json; None if absent."""
+    this workload, as committed in profiles/traffic.json (key "commit": the commit they were
+    measured at); None if absent."""
     try:
         with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
             return json.load(f).get(key)
@@ -478,7 +479,8 @@ def main() -> int:
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("paged_attention_v1_config2"),
-                     "traffic_source": "profiles/hbm_traffic_counters.txt (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE)",
+                     "traffic_source": "profiles/hbm_traffic_counters.txt (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE, "
+                                       f"measured at commit {measured_traffic('commit')})",
                      "algorithmic_bytes": w.decode_bytes(), "us_per_launch": round(ms_v1 * 1e3, 2)},
     }
     if args.only == "decode":
