@@ -92,6 +92,14 @@ extern "C" {
     ) -> c_int;
     /// Split-K workspace of rg_linear for this shape (0: runs unsplit).
     pub fn rg_linear_workspace_bytes(num_rows: i32, out_features: i32, in_features: i32) -> usize;
+    /// New: opt-in check of the block tables and context lengths (synchronises the stream).
+    pub fn rg_validate_block_tables(
+        block_table: *const i32, context_lens: *const i32, batch_size: i32, max_blocks_per_seq: i32,
+        block_size: i32, num_blocks: i32, stream: *mut c_void,
+    ) -> c_int;
+    /// New: opt-in check of a slot mapping (synchronises the stream).
+    pub fn rg_validate_slot_mapping(slot_mapping: *const i32, num_tokens: i32, num_slots: i64, stream: *mut c_void)
+        -> c_int;
     /// Replaces launch_v1 (mod.rs:305-348).
     pub fn rg_paged_attention_v1(
         query: *const c_void, key_cache: *const c_void, value_cache: *const c_void, block_table: *const i32,

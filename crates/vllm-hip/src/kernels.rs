@@ -451,6 +451,28 @@ impl PagedAttentionKernels {
                                 T::DTYPE, self.stream))
     }
 
+    /// Opt-in check (no counterpart in mod.rs): every context length within its table row and
+    /// every block number the contexts use within the pool; synchronises the stream and names
+    /// the first bad entry in the error.
+    pub unsafe fn validate_block_tables(
+        &self,
+        block_table: &HipSlice<i32>,
+        context_lens: &HipSlice<i32>,
+        batch_size: i32,
+        max_blocks_per_seq: i32,
+        block_size: i32,
+        num_blocks: i32,
+    ) -> CoreResult<()> {
+        status(ffi::rg_validate_block_tables(block_table.as_ptr(), context_lens.as_ptr(), batch_size,
+                                             max_blocks_per_seq, block_size, num_blocks, self.stream))
+    }
+
+    /// Opt-in check of a slot mapping against a pool of `num_slots` slots (negative slots are padding).
+    pub unsafe fn validate_slot_mapping(&self, slot_mapping: &HipSlice<i32>, num_tokens: i32, num_slots: i64)
+        -> CoreResult<()> {
+        status(ffi::rg_validate_slot_mapping(slot_mapping.as_ptr(), num_tokens, num_slots, self.stream))
+    }
+
     /// Split-K workspace bytes of launch_linear for this shape on the current device.
     pub fn linear_workspace_bytes(&self, num_rows: i32, out_features: i32, in_features: i32) -> usize {
         // SAFETY: a pure size computation.

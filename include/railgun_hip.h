@@ -218,6 +218,19 @@ int rg_linear(const void* x, const void* weight, void* out, int32_t num_rows,
  * shape runs unsplit, or is not supported). */
 size_t rg_linear_workspace_bytes(int32_t num_rows, int32_t out_features, int32_t in_features);
 
+/* Opt-in index checks (new entries, no counterpart: the reference's launchers pass indices to the
+ * kernels unchecked, crates/vllm-cuda/src/kernels/mod.rs:196-508, as do this library's kernel
+ * entries).  Each scans on the device, synchronises `stream` and returns RG_ERR_INVALID_ARGUMENT
+ * naming the first bad entry, RG_OK otherwise; a debugging aid, not for graph capture.
+ * rg_validate_block_tables: context_lens[s] in [0, max_blocks_per_seq * block_size] and the
+ * table entries those contexts use in [0, num_blocks).  rg_validate_slot_mapping: every slot
+ * below num_slots (= num_blocks * block_size; negative slots are padding). */
+int rg_validate_block_tables(const int32_t* block_table, const int32_t* context_lens,
+                             int32_t batch_size, int32_t max_blocks_per_seq, int32_t block_size,
+                             int32_t num_blocks, void* stream);
+int rg_validate_slot_mapping(const int32_t* slot_mapping, int32_t num_tokens, int64_t num_slots,
+                             void* stream);
+
 /* ------------------------------------------------------- decode, v1 -------- */
 
 /* Bytes of workspace rg_paged_attention_v1 / _v1_plus use for the given shape on the

@@ -23,7 +23,7 @@ BUILD_DIR = os.path.join(ROOT, "_build")
 LIB_OUT = os.path.join(PKG, "librailgun_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HIP_SOURCES = ["rg_status.hip", "cache_ops.hip", "decode.hip", "prefill.hip", "model_ops.hip", "gemm.hip"]
+HIP_SOURCES = ["rg_status.hip", "cache_ops.hip", "decode.hip", "prefill.hip", "model_ops.hip", "gemm.hip", "validate.hip"]
 # -packed-fp32-ops: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++20", f"-I{ROOT}/include",

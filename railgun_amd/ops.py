@@ -111,6 +111,21 @@ class PagedAttentionKernels:
         check(self.lib.rg_rope(x.data_ptr(), cos_sin.data_ptr(), positions.data_ptr(), num_heads, head_dim,
                                num_tokens, dtype_code(x), _stream(x)))
 
+    # Opt-in index checks (no counterpart in mod.rs): synchronous, raise RailgunError naming the
+    # first bad entry.
+    def validate_block_tables(self, block_table, context_lens, block_size: int, num_blocks: int) -> None:
+        _require_cuda(block_table, context_lens)
+        _require_i32(block_table, context_lens)
+        batch, max_blocks = int(block_table.shape[0]), int(block_table.shape[1])
+        check(self.lib.rg_validate_block_tables(block_table.data_ptr(), context_lens.data_ptr(), batch, max_blocks,
+                                                block_size, num_blocks, _stream(block_table)))
+
+    def validate_slot_mapping(self, slot_mapping, num_slots: int) -> None:
+        _require_cuda(slot_mapping)
+        _require_i32(slot_mapping)
+        check(self.lib.rg_validate_slot_mapping(slot_mapping.data_ptr(), int(slot_mapping.numel()), num_slots,
+                                                _stream(slot_mapping)))
+
     # mod.rs:227-262
     def launch_reshape_and_cache(self, k, v, k_cache, v_cache, slot_mapping, num_kv_heads: int,
                                  head_dim: int, block_size: int, batch_size: int) -> None:
