@@ -92,6 +92,12 @@ extern "C" {
     ) -> c_int;
     /// Split-K workspace of rg_linear for this shape (0: runs unsplit).
     pub fn rg_linear_workspace_bytes(num_rows: i32, out_features: i32, in_features: i32) -> usize;
+    /// New: the gate/up projection and SiLU·mul in one pass (interleaved gate/up weight).
+    pub fn rg_linear_silu_mul(
+        x: *const c_void, weight_gate_up: *const c_void, out: *mut c_void, num_rows: i32, intermediate_size: i32,
+        in_features: i32, x_row_stride: i64, weight_row_stride: i64, out_row_stride: i64, dtype: i32,
+        stream: *mut c_void,
+    ) -> c_int;
     /// New: opt-in check of the block tables and context lengths (synchronises the stream).
     pub fn rg_validate_block_tables(
         block_table: *const i32, context_lens: *const i32, batch_size: i32, max_blocks_per_seq: i32,

@@ -473,6 +473,25 @@ impl PagedAttentionKernels {
         status(ffi::rg_validate_slot_mapping(slot_mapping.as_ptr(), num_tokens, num_slots, self.stream))
     }
 
+    /// out [num_rows, intermediate_size] = silu(x . gate^T) * (x . up^T) with the gate and up rows of
+    /// `weight_gate_up` interleaved in blocks of 16 (see the header), decode batches only.
+    pub unsafe fn launch_linear_silu_mul<T: KvElement>(
+        &self,
+        x: &HipSlice<T>,
+        weight_gate_up: &HipSlice<T>,
+        out: &mut HipSlice<T>,
+        num_rows: i32,
+        intermediate_size: i32,
+        in_features: i32,
+        x_row_stride: i64,
+        weight_row_stride: i64,
+        out_row_stride: i64,
+    ) -> CoreResult<()> {
+        status(ffi::rg_linear_silu_mul(x.as_ptr(), weight_gate_up.as_ptr(), out.as_mut_ptr(), num_rows,
+                                       intermediate_size, in_features, x_row_stride, weight_row_stride,
+                                       out_row_stride, T::DTYPE, self.stream))
+    }
+
     /// Split-K workspace bytes of launch_linear for this shape on the current device.
     pub fn linear_workspace_bytes(&self, num_rows: i32, out_features: i32, in_features: i32) -> usize {
         // SAFETY: a pure size computation.

@@ -218,6 +218,16 @@ int rg_linear(const void* x, const void* weight, void* out, int32_t num_rows,
  * shape runs unsplit, or is not supported). */
 size_t rg_linear_workspace_bytes(int32_t num_rows, int32_t out_features, int32_t in_features);
 
+/* The gate/up projection and SiLU·mul in one pass (LlamaMLP, architecture.rs:80-84):
+ *   out[m, i] = round(round(silu(g)) * u),  g = round(x[m] . gate[i]), u = round(x[m] . up[i]),
+ * the arithmetic of rg_linear followed by rg_silu_and_mul.  weight_gate_up is [2 I, K] with the
+ * gate and up rows interleaved in blocks of 16 (rows 32j .. 32j+15: gate rows 16j .., rows
+ * 32j+16 .. 32j+31: up rows 16j ..); out is [num_rows, I].  The constraints of rg_linear, and
+ * I a multiple of 16.  New entry (the reference runs two GEMMs and the element-wise product). */
+int rg_linear_silu_mul(const void* x, const void* weight_gate_up, void* out, int32_t num_rows,
+                       int32_t intermediate_size, int32_t in_features, int64_t x_row_stride,
+                       int64_t weight_row_stride, int64_t out_row_stride, int32_t dtype, void* stream);
+
 /* Opt-in index checks (new entries, no counterpart: the reference's launchers pass indices to the
  * kernels unchecked, crates/vllm-cuda/src/kernels/mod.rs:196-508, as do this library's kernel
  * entries).  Each scans on the device, synchronises `stream` and returns RG_ERR_INVALID_ARGUMENT

@@ -104,8 +104,17 @@ struct GemmRing {
 // below (16 rows at one piece) touch every bank once.  The 4 waves take one k-step of 32
 // each from every chunk, so the workgroup reads each operand byte once, and each X fragment
 // feeds NB MFMAs.  The quarters are summed through LDS in a fixed order.
-template <typename T, int NB, int MB>
+//
+// EPI = kEpiSiluMul: W holds the gate and up projections interleaved in 16-row blocks (rows
+// 32j .. 32j + 15 are gate rows 16j .., rows 32j + 16 .. 32j + 31 up rows 16j ..), so n-blocks
+// 2j and 2j + 1 of a tile are the gate and up columns of the same 16 outputs; the wave owning
+// both writes a.c[m][16j + ..] = round(round(silu(g)) * u) from the rounded g and u (what
+// silu_mul_kernel computes from a gate/up GEMM's output), a.c being [M, N / 2].
+constexpr int kEpiPlain = 0;
+constexpr int kEpiSiluMul = 1;
+template <typename T, int NB, int MB, int EPI>
 __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
+  static_assert(EPI == kEpiPlain || NB % 2 == 0, "gate/up pairs need an even number of n-blocks");
   using MF = gemm_mfma<T>;
   using RG = GemmRing<NB, MB>;
   constexpr int KS = kGemmWaves;
@@ -194,14 +203,46 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
   // it at [f][(w - owner - 1) mod KS][lane].  Every copy has landed (the last wait was for 0).
   tile_barrier();
   gf32x4_t* red = reinterpret_cast<gf32x4_t*>(lds);
+  // The wave that finishes fragment (i, mb) (with EPI, the pair of gate / up blocks i / 2).
+  auto owner = [](int i, int mb) { return ((EPI == kEpiSiluMul ? i / 2 : i) * MB + mb) % KS; };
 #pragma unroll
   for (int i = 0; i < NB; ++i)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const int f = i * MB + mb, own = f % KS;
+      const int f = i * MB + mb, own = owner(i, mb);
       if (w != own) red[(f * (KS - 1) + (w - own - 1 + KS) % KS) * 64 + lane] = acc[i][mb];
     }
   __syncthreads();
+
+  if constexpr (EPI == kEpiSiluMul) {
+    using E = elem<T>;
+#pragma unroll
+    for (int jp = 0; jp < NB / 2; ++jp)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        if (w != owner(2 * jp, mb)) continue;
+        const int fg = 2 * jp * MB + mb, fu = (2 * jp + 1) * MB + mb;
+        gf32x4_t vg = acc[2 * jp][mb], vu = acc[2 * jp + 1][mb];
+#pragma unroll
+        for (int j = 0; j < KS - 1; ++j) {
+          vg += red[(fg * (KS - 1) + j) * 64 + lane];
+          vu += red[(fu * (KS - 1) + j) * 64 + lane];
+        }
+        if (16 * mb + r >= mrows) continue;
+        uint16_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float gv = E::to_f32(E::from_f32(vg[e]));
+          const float uv = E::to_f32(E::from_f32(vu[e]));
+          const float act = E::to_f32(E::from_f32(gv / (1.f + expf(-gv))));
+          o[e] = E::from_f32(act * uv);
+        }
+        const int n = (n0 / 32 + jp) * 16 + 4 * g;
+        *reinterpret_cast<uint2*>(a.c + (int64_t)(m0 + 16 * mb + r) * a.ldc + n) =
+            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+      }
+    return;
+  }
 
   // Lane (r, g) holds C[m0 + 16 mb + r][n0 + 16 i + 4g .. +3].
 #pragma unroll
@@ -210,7 +251,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
     for (int mb = 0; mb < MB; ++mb) {
       const int f = i * MB + mb;
       const int m = m0 + 16 * mb + r;
-      if (w != f % KS) continue;
+      if (w != owner(i, mb)) continue;
       gf32x4_t v = acc[i][mb];
 #pragma unroll
       for (int j = 0; j < KS - 1; ++j) v += red[(f * (KS - 1) + j) * 64 + lane];
@@ -239,16 +280,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a, int S) {
   *reinterpret_cast<uint2*>(a.c + (int64_t)m * a.ldc + n) = make_uint2(lo, hi);
 }
 
-template <typename T, int NB>
+template <typename T, int NB, int EPI = kEpiPlain>
 void launch_gemm_mb(const GemmArgs& a, int mb, int splits, hipStream_t s) {
   const dim3 grid((unsigned)(a.N / (16 * NB) * a.mtiles), (unsigned)splits);
   switch (mb) {
-    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 1>), grid, dim3(kGemmThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 2>), grid, dim3(kGemmThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 4>), grid, dim3(kGemmThreads), 0, s, a); break;
-    default: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 8>), grid, dim3(kGemmThreads), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 1, EPI>), grid, dim3(kGemmThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 2, EPI>), grid, dim3(kGemmThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 4, EPI>), grid, dim3(kGemmThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 8, EPI>), grid, dim3(kGemmThreads), 0, s, a); break;
   }
-  if (splits > 1) {
+  if (EPI == kEpiPlain && splits > 1) {
     const int64_t quads = (int64_t)a.M * a.N / 4;
     hipLaunchKernelGGL(splitk_reduce_kernel<T>, dim3((unsigned)ceil_div(quads, 256)), dim3(256), 0, s, a, splits);
   }
@@ -259,6 +300,12 @@ void launch_gemm(const GemmArgs& a, int nb, int mb, int splits, hipStream_t s) {
   if (nb == 4) launch_gemm_mb<T, 4>(a, mb, splits, s);
   else if (nb == 2) launch_gemm_mb<T, 2>(a, mb, splits, s);
   else launch_gemm_mb<T, 1>(a, mb, splits, s);
+}
+
+template <typename T>
+void launch_gemm_silu_mul(const GemmArgs& a, int nb, int mb, hipStream_t s) {
+  if (nb == 4) launch_gemm_mb<T, 4, kEpiSiluMul>(a, mb, 1, s);
+  else launch_gemm_mb<T, 2, kEpiSiluMul>(a, mb, 1, s);
 }
 
 // LDS bytes of a workgroup of the (NB, MB) instantiation (GemmRing<NB, MB>::BYTES).
@@ -283,7 +330,7 @@ int ring_bytes(int nb, int mb) {
 // Each workgroup streams its rows of X and its columns of W once per K range; small row tiles
 // cut the X bytes of narrow layers, and the XCD-aware order keeps their re-reads of W in L2.
 struct GemmPlan { int nb, mb, mtiles, splits, xcd; };
-GemmPlan gemm_plan(int M, int N, int K, int cus) {
+GemmPlan gemm_plan(int M, int N, int K, int cus, bool pairs = false) {
   const int nblk = N / 16, chunks = K / kChunkK;
   GemmPlan best{1, 1, M, 1, 0};
   double best_t = 1e30;
@@ -291,10 +338,10 @@ GemmPlan gemm_plan(int M, int N, int K, int cus) {
     if (mb > 1 && 16 * (mb / 2) >= M) continue;  // a smaller row tile already holds every row
     const int mtiles = (M + 16 * mb - 1) / (16 * mb);
     for (int nb : {4, 2, 1}) {
-      if (nblk % nb != 0) continue;
+      if (nblk % nb != 0 || (pairs && nb == 1)) continue;
       const int resident = std::max(1, std::min(4, kLdsBytes / ring_bytes(nb, mb)));
       for (int splits : {1, 2, 4}) {
-        if (splits > 1 && chunks / splits < 8) continue;
+        if (splits > 1 && (pairs || chunks / splits < 8)) continue;
         const int64_t wgs = (int64_t)mtiles * (nblk / nb) * splits;
         const double stream = 3.0 * (double)ceil_div(wgs, (int64_t)cus * resident) +
                               0.047 * (double)ceil_div(wgs, cus) * (mb + nb) * (chunks / splits);
@@ -327,36 +374,56 @@ extern "C" size_t rg_linear_workspace_bytes(int32_t num_rows, int32_t out_featur
   return p.splits > 1 ? (size_t)p.splits * num_rows * out_features * sizeof(float) : 0;
 }
 
-extern "C" int rg_linear(const void* x, const void* weight, void* out, int32_t num_rows, int32_t out_features,
-                         int32_t in_features, int64_t x_row_stride, int64_t weight_row_stride,
-                         int64_t out_row_stride, void* workspace, size_t workspace_bytes, int32_t dtype,
-                         void* stream) {
-  const char* op = "linear";
-  const int32_t M = num_rows, N = out_features, K = in_features;
+namespace rg {
+namespace {
+// Checks shared by the rg_linear entries (N: weight rows, out_cols: output row length).
+// Returns RG_OK, or a failure status; `empty` is set for a call with nothing to do.
+int check_linear(const char* op, const void* x, const void* weight, const void* out, int32_t M, int32_t N,
+                 int32_t K, int32_t out_cols, int64_t ldx, int64_t ldw, int64_t ldo, int32_t dtype, bool& empty) {
+  empty = false;
   if (dtype != RG_DTYPE_BF16 && dtype != RG_DTYPE_F16) {
     return fail(RG_ERR_NOT_SUPPORTED, "%s: bf16 or f16 operands only, got dtype %d", op, dtype);
   }
   if (M < 0 || N < 0 || K < 0) return fail(RG_ERR_INVALID_ARGUMENT, "%s: negative size", op);
-  if (M == 0 || N == 0) return ok();
+  if (M == 0 || N == 0) {
+    empty = true;
+    return ok();
+  }
   if (M > kGemmMaxRows || N % 16 != 0 || K % kChunkK != 0 || K == 0) {
     return fail(RG_ERR_NOT_SUPPORTED,
                 "%s: needs num_rows <= %d, out_features a multiple of 16 and in_features a positive "
                 "multiple of %d (got %d, %d, %d)", op, kGemmMaxRows, kChunkK, M, N, K);
   }
   if (!x || !weight || !out) return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
-  if (x_row_stride < K || weight_row_stride < K || out_row_stride < N) {
+  if (ldx < K || ldw < K || ldo < out_cols) {
     return fail(RG_ERR_INVALID_ARGUMENT, "%s: a row stride is shorter than its row", op);
   }
-  if (!aligned16(x) || !aligned16(weight) || x_row_stride % 8 != 0 || weight_row_stride % 8 != 0 ||
-      (reinterpret_cast<uintptr_t>(out) & 7u) != 0 || out_row_stride % 4 != 0) {
+  if (!aligned16(x) || !aligned16(weight) || ldx % 8 != 0 || ldw % 8 != 0 ||
+      (reinterpret_cast<uintptr_t>(out) & 7u) != 0 || ldo % 4 != 0) {
     return fail(RG_ERR_NOT_SUPPORTED,
                 "%s: operands and row strides must be 16-byte aligned (output 8-byte aligned)", op);
   }
   // The copies address a row as a 32-bit byte offset from X (from the workgroup's first W row).
-  if ((int64_t)(M - 1) * x_row_stride * 2 + 2 * (int64_t)K > INT32_MAX ||
-      (int64_t)63 * weight_row_stride * 2 + 2 * (int64_t)K > INT32_MAX) {
+  if ((int64_t)(M - 1) * ldx * 2 + 2 * (int64_t)K > INT32_MAX || (int64_t)63 * ldw * 2 + 2 * (int64_t)K > INT32_MAX) {
     return fail(RG_ERR_NOT_SUPPORTED, "%s: row strides too large for 32-bit copy offsets", op);
   }
+  return RG_OK;
+}
+}  // namespace
+}  // namespace rg
+
+extern "C" int rg_linear(const void* x, const void* weight, void* out, int32_t num_rows, int32_t out_features,
+                         int32_t in_features, int64_t x_row_stride, int64_t weight_row_stride,
+                         int64_t out_row_stride, void* workspace, size_t workspace_bytes, int32_t dtype,
+                         void* stream) {
+  const char* op = "linear";
+  const int32_t M = num_rows, N = out_features, K = in_features;
+  bool empty = false;
+  if (int st = check_linear(op, x, weight, out, M, N, K, N, x_row_stride, weight_row_stride, out_row_stride, dtype,
+                            empty)) {
+    return st;
+  }
+  if (empty) return ok();
   GemmPlan plan = gemm_plan(M, N, K, device_cu_count());
   const size_t need = plan.splits > 1 ? (size_t)plan.splits * M * N * sizeof(float) : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))) {
@@ -368,5 +435,29 @@ extern "C" int rg_linear(const void* x, const void* weight, void* out, int32_t n
   hipStream_t s = as_stream(stream);
   if (dtype == RG_DTYPE_BF16) launch_gemm<bf16_t>(a, plan.nb, plan.mb, plan.splits, s);
   else launch_gemm<f16_t>(a, plan.nb, plan.mb, plan.splits, s);
+  return check_launch(op);
+}
+
+extern "C" int rg_linear_silu_mul(const void* x, const void* weight_gate_up, void* out, int32_t num_rows,
+                                  int32_t intermediate_size, int32_t in_features, int64_t x_row_stride,
+                                  int64_t weight_row_stride, int64_t out_row_stride, int32_t dtype, void* stream) {
+  const char* op = "linear_silu_mul";
+  const int32_t M = num_rows, I = intermediate_size, K = in_features;
+  if (I < 0 || I % 16 != 0) {
+    return fail(RG_ERR_NOT_SUPPORTED, "%s: intermediate_size must be a multiple of 16 (got %d)", op, I);
+  }
+  bool empty = false;
+  if (int st = check_linear(op, x, weight_gate_up, out, M, 2 * I, K, I, x_row_stride, weight_row_stride,
+                            out_row_stride, dtype, empty)) {
+    return st;
+  }
+  if (empty) return ok();
+  const GemmPlan plan = gemm_plan(M, 2 * I, K, device_cu_count(), true);
+  GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight_gate_up),
+             static_cast<uint16_t*>(out), nullptr, M, 2 * I, K, x_row_stride, weight_row_stride, out_row_stride,
+             plan.mtiles, plan.xcd};
+  hipStream_t s = as_stream(stream);
+  if (dtype == RG_DTYPE_BF16) launch_gemm_silu_mul<bf16_t>(a, plan.nb, plan.mb, s);
+  else launch_gemm_silu_mul<f16_t>(a, plan.nb, plan.mb, s);
   return check_launch(op);
 }

@@ -18,7 +18,9 @@ then decode slots, :mod:`railgun_amd.batch`) runs as:
   MFMA GEMM, unless hipBLASLt (``F.linear``) measured more than 5 % faster for that shape on
   this device: each (rows, out, in) shape is timed when an eager step first meets it (three
   interleaved graph-replay trials of each, medians compared).  Larger (prefill) steps use
-  hipBLASLt.
+  hipBLASLt.  The MLP's gate/up projection and SiLU·mul run as one ``rg_linear_silu_mul`` (over
+  a copy of the gate/up weight with the rows interleaved in blocks of 16) when that measured
+  faster than the projection followed by ``rg_silu_and_mul``.
 
 Every layer owns a KV pool in Railgun's fused layout ``[NB, 2, H_kv, bs, D]``
 (crates/vllm-paged-attention/src/block.rs:70,89-95); the reference shares one pool across
@@ -37,8 +39,8 @@ import torch.nn.functional as F
 
 from .batch import StepBatch
 from .kv_pool import GpuBlockPool
-from .ops import (LINEAR_MAX_ROWS, PagedAttentionKernels, linear, linear_workspace_bytes, rms_norm,
-                  rope_cos_sin_table, silu_and_mul)
+from .ops import (LINEAR_MAX_ROWS, PagedAttentionKernels, interleave_gate_up, linear, linear_silu_mul,
+                  linear_workspace_bytes, rms_norm, rope_cos_sin_table, silu_and_mul)
 
 
 def graph_us(fn, calls: int = 10, replays: int = 3) -> float:
@@ -197,6 +199,9 @@ class RailgunLlama:
         self._ws = torch.empty(0, dtype=torch.uint8, device=self.device)
         # (rows, out_features, in_features) -> True for rg_linear, False for hipBLASLt
         self.linear_choice: dict = {}
+        # rows -> True for rg_linear_silu_mul, False for the projection + rg_silu_and_mul
+        self.mlp_choice: dict = {}
+        self._w_gate_up_il: dict = {}  # layer -> interleaved gate/up weight
         # Hook for measurements: called as attention_hook("begin"/"end", layer) around each
         # layer's attention kernels (None in normal use).
         self.attention_hook = None
@@ -254,6 +259,34 @@ class RailgunLlama:
             return F.linear(x, weight)
         return linear(x, weight, workspace=self._workspace(ws_bytes) if ws_bytes else None)
 
+    def _mlp_act(self, layer: int, h: torch.Tensor, act: torch.Tensor) -> None:
+        """act = silu(h @ gate^T) * (h @ up^T), fused or as the projection + rg_silu_and_mul."""
+        L = self.w.layers[layer]
+        inter = int(act.shape[1])
+        rows = int(h.shape[0])
+        if not (self._rg_linear_fits(h, L.w_gate_up) and inter % 16 == 0):
+            silu_and_mul(self._linear(h, L.w_gate_up), act)
+            return
+        w_il = self._w_gate_up_il.get(layer)
+        if w_il is None:
+            w_il = self._w_gate_up_il[layer] = interleave_gate_up(L.w_gate_up)
+        fused = self.mlp_choice.get(rows)
+        if fused is None:
+            if torch.cuda.is_current_stream_capturing():
+                fused = True
+            else:
+                self._linear(h, L.w_gate_up)  # settles the projection's own choice outside the timing
+                t_f, t_s = [], []
+                for _ in range(3):
+                    t_f.append(graph_us(lambda: linear_silu_mul(h, w_il, act), calls=20))
+                    t_s.append(graph_us(lambda: silu_and_mul(self._linear(h, L.w_gate_up), act), calls=20))
+                fused = not sorted(t_s)[1] < 0.95 * sorted(t_f)[1]
+            self.mlp_choice[rows] = fused
+        if fused:
+            linear_silu_mul(h, w_il, act)
+        else:
+            silu_and_mul(self._linear(h, L.w_gate_up), act)
+
     def check_step(self, b: StepBatch) -> None:
         """The kernels trust their indices (as the reference's do): check them on the host."""
         if b.num_tokens and int(b.positions.max()) >= self.cos_sin.shape[0]:
@@ -291,7 +324,7 @@ class RailgunLlama:
             delta = self._linear(attn.view(T, H * D), L.wo)
             # residual add + post_attention_layernorm, architecture.rs:53-57
             rms_norm(delta, L.post_norm, h, eps, residual=x)
-            silu_and_mul(self._linear(h, L.w_gate_up), act)     # LlamaMLP, architecture.rs:80-84
+            self._mlp_act(i, h, act)                            # LlamaMLP, architecture.rs:80-84
             delta = self._linear(act, L.w_down)
         rms_norm(delta, w.norm, h, eps, residual=x)            # last residual add + model.norm
         return self._linear(h.index_select(0, st.last_rows), w.lm_head)

@@ -460,6 +460,37 @@ def linear(x: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tensor] = 
     return out
 
 
+def interleave_gate_up(w_gate_up: torch.Tensor) -> torch.Tensor:
+    """[2 I, K] gate/up weight (gate rows, then up rows) -> the layout rg_linear_silu_mul takes:
+    gate and up rows interleaved in blocks of 16 (a copy)."""
+    two_i, k = (int(d) for d in w_gate_up.shape)
+    if two_i % 32 != 0:
+        raise RailgunError(_lib.RG_ERR_NOT_SUPPORTED, "interleave_gate_up: intermediate size must be a multiple of 16")
+    return w_gate_up.view(2, two_i // 32, 16, k).transpose(0, 1).contiguous().view(two_i, k)
+
+
+def linear_silu_mul(x: torch.Tensor, weight_il: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out [rows, I] = silu(x @ gate^T) * (x @ up^T), each step rounded as rg_linear followed by
+    rg_silu_and_mul round it; weight_il from interleave_gate_up."""
+    _require_cuda(x, weight_il, out)
+    if x.dim() != 2 or weight_il.dim() != 2 or x.stride(1) != 1 or not weight_il.is_contiguous() or \
+            x.dtype != weight_il.dtype:
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "linear_silu_mul: x [rows, K] with unit column stride and a "
+                                                         "contiguous interleaved weight [2 I, K] of the same dtype")
+    rows, k = (int(d) for d in x.shape)
+    inter = int(weight_il.shape[0]) // 2
+    if int(weight_il.shape[1]) != k:
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, f"linear_silu_mul: x has {k} features, weight "
+                                                         f"{int(weight_il.shape[1])}")
+    if out is None:
+        out = torch.empty((rows, inter), dtype=x.dtype, device=x.device)
+    elif tuple(out.shape) != (rows, inter) or out.stride(1) != 1 or out.dtype != x.dtype:
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "linear_silu_mul: out must be [rows, I] with unit column stride")
+    check(load_library().rg_linear_silu_mul(x.data_ptr(), weight_il.data_ptr(), out.data_ptr(), rows, inter, k,
+                                            x.stride(0), weight_il.stride(0), out.stride(0), dtype_code(x), _stream(x)))
+    return out
+
+
 __all__ = ["LINEAR_MAX_ROWS", "PagedAttentionKernels", "PagedAttentionOp", "RailgunError", "cache_geometry",
-           "dtype_code", "linear", "linear_workspace_bytes", "rms_norm", "rope_cos_sin_table", "silu_and_mul", "V1_MAX_CONTEXT",
+           "dtype_code", "interleave_gate_up", "linear", "linear_silu_mul", "linear_workspace_bytes", "rms_norm", "rope_cos_sin_table", "silu_and_mul", "V1_MAX_CONTEXT",
            "V2_PARTITION_SIZE"]

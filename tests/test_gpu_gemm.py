@@ -94,3 +94,34 @@ def test_linear_split_k(device, M, N, K):
     _check(split, x, w, f"split {M}x{N}x{K}")
     _check(unsplit, x, w, f"unsplit {M}x{N}x{K}")
     assert torch.equal(again.view(torch.int16), split.view(torch.int16)), "split K not deterministic"
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("M,I,K", [(128, 8192, 2048), (1, 8192, 2048), (37, 512, 256), (100, 1040, 1024)])
+def test_linear_silu_mul(device, M, I, K, dt):
+    """The gate/up projection with SiLU·mul in the epilogue against the fp32 products rounded the
+    way rg_linear + rg_silu_and_mul round them: g, u to the activation dtype, silu(g) rounded,
+    then the product."""
+    from railgun_amd.ops import interleave_gate_up, linear_silu_mul
+    g = torch.Generator().manual_seed(M + I + K)
+    x = torch.randn(M, K, generator=g).to(TORCH[dt]).to(device)
+    w = (0.05 * torch.randn(2 * I, K, generator=g)).to(TORCH[dt]).to(device)
+    got = linear_silu_mul(x, interleave_gate_up(w))
+    again = linear_silu_mul(x, interleave_gate_up(w))
+    torch.cuda.synchronize()
+    t = TORCH[dt]
+    xf, wf = x.float().cpu(), w.float().cpu()
+    gv = (xf @ wf[:I].T).to(t).float()
+    uv = (xf @ wf[I:].T).to(t).float()
+    act = (gv / (1 + torch.exp(-gv))).to(t).float()
+    ref = (act * uv).to(t).float()
+    err = (got.float().cpu() - ref).abs()
+    # First-order propagation of one ulp in g and in u (the GEMM's fp32 sums taken in another
+    # order can round either way) and of the roundings of silu(g) and of the product:
+    # |d out| <= eps (|u| |silu'(g)| |g| + 2 |silu(g)| |u| + |out|), eps one ulp relative.
+    eps = 2 ** -7 if dt == "bf16" else 2 ** -10
+    sig = torch.sigmoid(gv)
+    dsilu = (sig * (1 + gv * (1 - sig))).abs()
+    bound = eps * (uv.abs() * dsilu * gv.abs() + 2 * act.abs() * uv.abs() + ref.abs()) + 1e-3 * ref.abs().mean() + 1e-6
+    assert bool((err <= bound).all()), f"max excess {float((err - bound).max()):.3g}"
+    assert torch.equal(again.view(torch.int16), got.view(torch.int16)), "not deterministic"

@@ -209,3 +209,16 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stdout
+
+
+def test_interleave_gate_up_layout():
+    """interleave_gate_up puts gate rows 16j.. at rows 32j.. and up rows 16j.. at rows 32j + 16.."""
+    import torch
+
+    from railgun_amd.ops import interleave_gate_up
+    inter, k = 48, 8
+    w = torch.arange(2 * inter * k, dtype=torch.float32).view(2 * inter, k)
+    il = interleave_gate_up(w)
+    for j in range(inter // 16):
+        assert torch.equal(il[32 * j:32 * j + 16], w[16 * j:16 * j + 16])
+        assert torch.equal(il[32 * j + 16:32 * j + 32], w[inter + 16 * j:inter + 16 * j + 16])
