@@ -347,6 +347,8 @@ def side_model(device, steps: int) -> dict:
     step_bytes = weights.nbytes() + kv
     gemm = {f"{n}x{k}": "rg_linear" if v else "hipblaslt" for (_, n, k), v in model.linear_choice.items()}
     gemm["mlp"] = "fused gate/up + SiLU·mul" if model.mlp_choice.get(w.batch) else "gate/up + rg_silu_and_mul"
+    gemm["qkv"] = ("fused qkv + RoPE + cache write" if model.qkv_choice.get(w.batch)
+                   else "qkv + rg_qkv_rope_reshape_and_cache")
     del model, pool, weights, graph
     torch.cuda.empty_cache()
     return {"workload": w.name, "model": "llama-3.2-1b (random init, bf16)", "batch": w.batch,

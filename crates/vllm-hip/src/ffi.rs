@@ -63,6 +63,14 @@ extern "C" {
         num_heads: i32, num_kv_heads: i32, head_dim: i32, block_size: i32, num_tokens: i32, dtype: i32,
         kv_block_stride: i64, stream: *mut c_void,
     ) -> c_int;
+    /// New: the fused q/k/v projection and rg_qkv_rope_reshape_and_cache in one pass (decode batches).
+    pub fn rg_linear_qkv_rope_reshape_and_cache(
+        x: *const c_void, weight_qkv: *const c_void, q_out: *mut c_void, k_cache: *mut c_void,
+        v_cache: *mut c_void, cos_sin: *const f32, positions: *const i32, slot_mapping: *const i32,
+        num_tokens: i32, num_heads: i32, num_kv_heads: i32, head_dim: i32, block_size: i32, in_features: i32,
+        x_row_stride: i64, weight_row_stride: i64, q_out_token_stride: i64, kv_block_stride: i64, dtype: i32,
+        stream: *mut c_void,
+    ) -> c_int;
     /// New: the physical copies behind swap_out / swap_in / fork (allocator.rs:102-153).
     pub fn rg_copy_blocks(
         src_pool: *const c_void, dst_pool: *mut c_void, block_mapping: *const i32, num_pairs: i32,

@@ -387,6 +387,33 @@ impl PagedAttentionKernels {
             num_heads, num_kv_heads, head_dim, block_size, num_tokens, T::DTYPE, self.kv_block_stride, self.stream))
     }
 
+    /// The fused q/k/v projection and launch_qkv_rope_reshape_and_cache in one pass for decode
+    /// batches (num_tokens <= 128, head_dim 32 or 64); q_out rows of num_heads * head_dim.
+    pub unsafe fn launch_linear_qkv_rope_reshape_and_cache<T: KvElement>(
+        &self,
+        x: &HipSlice<T>,
+        weight_qkv: &HipSlice<T>,
+        q_out: &mut HipSlice<T>,
+        k_cache: &mut HipSlice<T>,
+        v_cache: &mut HipSlice<T>,
+        cos_sin: &HipSlice<f32>,
+        positions: &HipSlice<i32>,
+        slot_mapping: &HipSlice<i32>,
+        num_tokens: i32,
+        num_heads: i32,
+        num_kv_heads: i32,
+        head_dim: i32,
+        block_size: i32,
+        in_features: i32,
+        x_row_stride: i64,
+    ) -> CoreResult<()> {
+        status(ffi::rg_linear_qkv_rope_reshape_and_cache(
+            x.as_ptr(), weight_qkv.as_ptr(), q_out.as_mut_ptr(), k_cache.as_mut_ptr(), v_cache.as_mut_ptr(),
+            cos_sin.as_ptr() as *const f32, positions.as_ptr() as *const i32, slot_mapping.as_ptr() as *const i32,
+            num_tokens, num_heads, num_kv_heads, head_dim, block_size, in_features, x_row_stride,
+            in_features as i64, (num_heads * head_dim) as i64, self.kv_block_stride, T::DTYPE, self.stream))
+    }
+
     /// Packed causal prefill of `num_seqs` sequences (rows `cu_seqlens[s] .. cu_seqlens[s+1]`)
     /// over the paged cache.
     pub unsafe fn launch_prefill_packed<T: KvElement>(

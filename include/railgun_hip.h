@@ -228,6 +228,25 @@ int rg_linear_silu_mul(const void* x, const void* weight_gate_up, void* out, int
                        int32_t intermediate_size, int32_t in_features, int64_t x_row_stride,
                        int64_t weight_row_stride, int64_t out_row_stride, int32_t dtype, void* stream);
 
+/* The fused q/k/v projection and rg_qkv_rope_reshape_and_cache in one pass, for decode batches
+ * (the constraints of rg_linear): x [num_tokens, in_features] . weight_qkv^T, weight_qkv
+ * [(H + 2 H_kv) head_dim, in_features] (q, k, v heads in that order); each head's columns are
+ * rounded as the projection's output, q and k heads rotated by cos_sin[positions[t]] and
+ * rounded, q written to q_out [num_tokens, H, head_dim] (q_out_token_stride elements between
+ * tokens), k and v written into the paged caches at slot_mapping[t] (negative: padding, not
+ * written) — the arithmetic of rg_linear followed by rg_qkv_rope_reshape_and_cache.  head_dim 32
+ * or 64 (a workgroup's column tile is one head); cos_sin, the caches and kv_block_stride 16-byte
+ * aligned.  New entry (the reference projects q, k and v separately and applies no RoPE,
+ * attention.rs:104-125). */
+int rg_linear_qkv_rope_reshape_and_cache(const void* x, const void* weight_qkv, void* q_out,
+                                         void* k_cache, void* v_cache, const float* cos_sin,
+                                         const int32_t* positions, const int32_t* slot_mapping,
+                                         int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t block_size, int32_t in_features,
+                                         int64_t x_row_stride, int64_t weight_row_stride,
+                                         int64_t q_out_token_stride, int64_t kv_block_stride,
+                                         int32_t dtype, void* stream);
+
 /* Opt-in index checks (new entries, no counterpart: the reference's launchers pass indices to the
  * kernels unchecked, crates/vllm-cuda/src/kernels/mod.rs:196-508, as do this library's kernel
  * entries).  Each scans on the device, synchronises `stream` and returns RG_ERR_INVALID_ARGUMENT

@@ -81,6 +81,7 @@ SIGNATURES = {
     "rg_linear_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "rg_linear_silu_mul": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64,
                                    c_int32, c_void_p]),
+    "rg_linear_qkv_rope_reshape_and_cache": (c_int, [c_void_p] * 8 + [c_int32] * 6 + [c_int64] * 4 + [c_int32, c_void_p]),
     "rg_validate_block_tables": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p]),
     "rg_validate_slot_mapping": (c_int, [c_void_p, c_int32, c_int64, c_void_p]),
     "rg_paged_attention_v1_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),

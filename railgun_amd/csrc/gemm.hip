@@ -62,6 +62,14 @@ struct GemmArgs {
   int64_t ldx, ldw, ldc;  // elements between consecutive rows
   int32_t mtiles;         // row tiles of 16 MB rows (1: one tile holds every row)
   int32_t xcd_map;        // 1: the row tiles of a column tile run on one XCD (see the kernel)
+  // kEpiRope: the q / k / v heads of a fused qkv projection (one head per column tile).
+  const float* cos_sin;     // [positions, D]: cos at [i], sin at [D / 2 + i]
+  const int32_t* positions; // [M]
+  const int32_t* slots;     // [M]; negative: a padding token, not cached
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t kv_stride;        // elements between cache blocks
+  int32_t num_heads, num_kv_heads, block_size;
 };
 
 template <int N>
@@ -110,11 +118,30 @@ struct GemmRing {
 // 2j and 2j + 1 of a tile are the gate and up columns of the same 16 outputs; the wave owning
 // both writes a.c[m][16j + ..] = round(round(silu(g)) * u) from the rounded g and u (what
 // silu_mul_kernel computes from a gate/up GEMM's output), a.c being [M, N / 2].
+//
+// EPI = kEpiRope: W is a fused q / k / v projection whose column tiles are whole heads (16 NB =
+// head_dim), so n-blocks i and i + NB / 2 hold the rotation pairs (d, d + D / 2).  The wave
+// owning both rounds them as the projection's output is rounded, rotates q and k heads by
+// cos_sin[position] (RoPE in rotate_half form, the arithmetic of rope_cache_kernel), and writes
+// q heads to a.c ([M, H, D]: a.ldc between tokens) and k / v heads into the paged caches at
+// the token's slot.
 constexpr int kEpiPlain = 0;
 constexpr int kEpiSiluMul = 1;
+constexpr int kEpiRope = 2;
+
+// out = (lo c - hi s, hi c + lo s), unfused (the rotation of rope_cache_kernel).
+__device__ __forceinline__ void rope_rotate(float lo, float hi, float c, float s, float& out_lo, float& out_hi) {
+#pragma clang fp contract(off)
+  const float a = lo * c;
+  const float b = hi * s;
+  const float e = hi * c;
+  const float f = lo * s;
+  out_lo = a - b;
+  out_hi = e + f;
+}
 template <typename T, int NB, int MB, int EPI>
 __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
-  static_assert(EPI == kEpiPlain || NB % 2 == 0, "gate/up pairs need an even number of n-blocks");
+  static_assert(EPI == kEpiPlain || NB % 2 == 0, "gate/up and rotation pairs need an even number of n-blocks");
   using MF = gemm_mfma<T>;
   using RG = GemmRing<NB, MB>;
   constexpr int KS = kGemmWaves;
@@ -203,8 +230,12 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
   // it at [f][(w - owner - 1) mod KS][lane].  Every copy has landed (the last wait was for 0).
   tile_barrier();
   gf32x4_t* red = reinterpret_cast<gf32x4_t*>(lds);
-  // The wave that finishes fragment (i, mb) (with EPI, the pair of gate / up blocks i / 2).
-  auto owner = [](int i, int mb) { return ((EPI == kEpiSiluMul ? i / 2 : i) * MB + mb) % KS; };
+  // The wave that finishes fragment (i, mb): with kEpiSiluMul the pair of gate / up blocks i / 2,
+  // with kEpiRope the rotation pair i % (NB / 2).
+  auto owner = [](int i, int mb) {
+    const int pair = EPI == kEpiSiluMul ? i / 2 : EPI == kEpiRope ? i % (NB / 2) : i;
+    return (pair * MB + mb) % KS;
+  };
 #pragma unroll
   for (int i = 0; i < NB; ++i)
 #pragma unroll
@@ -213,6 +244,61 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
       if (w != own) red[(f * (KS - 1) + (w - own - 1 + KS) % KS) * 64 + lane] = acc[i][mb];
     }
   __syncthreads();
+
+  if constexpr (EPI == kEpiRope) {
+    using E = elem<T>;
+    constexpr int HD = 8 * NB;  // half the head
+    const int hg = n0 / (16 * NB);  // head among the H q, H_kv k and H_kv v heads
+    const bool is_q = hg < a.num_heads, is_v = hg >= a.num_heads + a.num_kv_heads;
+#pragma unroll
+    for (int p = 0; p < NB / 2; ++p)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        if (w != owner(p, mb)) continue;
+        const int fl = p * MB + mb, fh = (p + NB / 2) * MB + mb;
+        gf32x4_t vl = acc[p][mb], vh = acc[p + NB / 2][mb];
+#pragma unroll
+        for (int j = 0; j < KS - 1; ++j) {
+          vl += red[(fl * (KS - 1) + j) * 64 + lane];
+          vh += red[(fh * (KS - 1) + j) * 64 + lane];
+        }
+        if (16 * mb + r >= mrows) continue;
+        const int m = m0 + 16 * mb + r;
+        const int d = 16 * p + 4 * g;  // this lane's columns d .. d + 3 and HD + d ..
+        uint16_t ol[4], oh[4];
+        if (is_v) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ol[e] = E::from_f32(vl[e]), oh[e] = E::from_f32(vh[e]);
+        } else {
+          const float* cs = a.cos_sin + (int64_t)a.positions[m] * (2 * HD);
+          const float4 c4 = *reinterpret_cast<const float4*>(cs + d);
+          const float4 s4 = *reinterpret_cast<const float4*>(cs + HD + d);
+          const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float rl, rh;
+            rope_rotate(E::to_f32(E::from_f32(vl[e])), E::to_f32(E::from_f32(vh[e])), c[e], sn[e], rl, rh);
+            ol[e] = E::from_f32(rl);
+            oh[e] = E::from_f32(rh);
+          }
+        }
+        uint16_t* dst;
+        if (is_q) {
+          dst = a.c + (int64_t)m * a.ldc + (int64_t)hg * (2 * HD);
+        } else {
+          const int32_t slot = a.slots[m];
+          if (slot < 0) continue;  // padding token
+          const int kvh = is_v ? hg - a.num_heads - a.num_kv_heads : hg - a.num_heads;
+          dst = (is_v ? a.v_cache : a.k_cache) + (int64_t)(slot / a.block_size) * a.kv_stride +
+                ((int64_t)kvh * a.block_size + slot % a.block_size) * (2 * HD);
+        }
+        *reinterpret_cast<uint2*>(dst + d) = make_uint2((uint32_t)ol[0] | ((uint32_t)ol[1] << 16),
+                                                        (uint32_t)ol[2] | ((uint32_t)ol[3] << 16));
+        *reinterpret_cast<uint2*>(dst + HD + d) = make_uint2((uint32_t)oh[0] | ((uint32_t)oh[1] << 16),
+                                                             (uint32_t)oh[2] | ((uint32_t)oh[3] << 16));
+      }
+    return;
+  }
 
   if constexpr (EPI == kEpiSiluMul) {
     using E = elem<T>;
@@ -308,6 +394,12 @@ void launch_gemm_silu_mul(const GemmArgs& a, int nb, int mb, hipStream_t s) {
   else launch_gemm_mb<T, 2, kEpiSiluMul>(a, mb, 1, s);
 }
 
+template <typename T>
+void launch_gemm_rope(const GemmArgs& a, int nb, int mb, hipStream_t s) {
+  if (nb == 4) launch_gemm_mb<T, 4, kEpiRope>(a, mb, 1, s);
+  else launch_gemm_mb<T, 2, kEpiRope>(a, mb, 1, s);
+}
+
 // LDS bytes of a workgroup of the (NB, MB) instantiation (GemmRing<NB, MB>::BYTES).
 int ring_bytes(int nb, int mb) {
   const int slot = 16 * (mb + nb) * kChunkBytes;
@@ -330,7 +422,7 @@ int ring_bytes(int nb, int mb) {
 // Each workgroup streams its rows of X and its columns of W once per K range; small row tiles
 // cut the X bytes of narrow layers, and the XCD-aware order keeps their re-reads of W in L2.
 struct GemmPlan { int nb, mb, mtiles, splits, xcd; };
-GemmPlan gemm_plan(int M, int N, int K, int cus, bool pairs = false) {
+GemmPlan gemm_plan(int M, int N, int K, int cus, bool pairs = false, int only_nb = 0) {
   const int nblk = N / 16, chunks = K / kChunkK;
   GemmPlan best{1, 1, M, 1, 0};
   double best_t = 1e30;
@@ -338,7 +430,7 @@ GemmPlan gemm_plan(int M, int N, int K, int cus, bool pairs = false) {
     if (mb > 1 && 16 * (mb / 2) >= M) continue;  // a smaller row tile already holds every row
     const int mtiles = (M + 16 * mb - 1) / (16 * mb);
     for (int nb : {4, 2, 1}) {
-      if (nblk % nb != 0 || (pairs && nb == 1)) continue;
+      if (nblk % nb != 0 || (pairs && nb == 1) || (only_nb && nb != only_nb)) continue;
       const int resident = std::max(1, std::min(4, kLdsBytes / ring_bytes(nb, mb)));
       for (int splits : {1, 2, 4}) {
         if (splits > 1 && (pairs || chunks / splits < 8)) continue;
@@ -459,5 +551,49 @@ extern "C" int rg_linear_silu_mul(const void* x, const void* weight_gate_up, voi
   hipStream_t s = as_stream(stream);
   if (dtype == RG_DTYPE_BF16) launch_gemm_silu_mul<bf16_t>(a, plan.nb, plan.mb, s);
   else launch_gemm_silu_mul<f16_t>(a, plan.nb, plan.mb, s);
+  return check_launch(op);
+}
+
+extern "C" int rg_linear_qkv_rope_reshape_and_cache(const void* x, const void* weight_qkv, void* q_out,
+                                                    void* k_cache, void* v_cache, const float* cos_sin,
+                                                    const int32_t* positions, const int32_t* slot_mapping,
+                                                    int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                                                    int32_t head_dim, int32_t block_size, int32_t in_features,
+                                                    int64_t x_row_stride, int64_t weight_row_stride,
+                                                    int64_t q_out_token_stride, int64_t kv_block_stride,
+                                                    int32_t dtype, void* stream) {
+  const char* op = "linear_qkv_rope_reshape_and_cache";
+  const int32_t M = num_tokens, D = head_dim, K = in_features;
+  if (num_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 || num_heads % num_kv_heads != 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: need positive heads (H a multiple of H_kv) and block_size", op);
+  }
+  if (D != 32 && D != 64) {
+    return fail(RG_ERR_NOT_SUPPORTED, "%s: head_dim 32 or 64 (one head per column tile), got %d", op, D);
+  }
+  const int32_t N = (num_heads + 2 * num_kv_heads) * D;
+  bool empty = false;
+  if (int st = check_linear(op, x, weight_qkv, q_out, M, N, K, num_heads * D, x_row_stride, weight_row_stride,
+                            q_out_token_stride, dtype, empty)) {
+    return st;
+  }
+  if (empty) return ok();
+  if (!k_cache || !v_cache || !cos_sin || !positions || !slot_mapping) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
+  }
+  const int64_t kv_stride = kv_block_stride ? kv_block_stride : (int64_t)num_kv_heads * block_size * D;
+  if (kv_stride < (int64_t)num_kv_heads * block_size * D || !aligned16(k_cache) || !aligned16(v_cache) ||
+      kv_stride % 8 != 0 || (reinterpret_cast<uintptr_t>(cos_sin) & 15u) != 0) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: cache block stride shorter than a block, or caches / cos_sin not "
+                "16-byte aligned", op);
+  }
+  const int nb = D / 16;
+  const GemmPlan plan = gemm_plan(M, N, K, device_cu_count(), true, nb);
+  GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight_qkv), static_cast<uint16_t*>(q_out),
+             nullptr, M, N, K, x_row_stride, weight_row_stride, q_out_token_stride, plan.mtiles, plan.xcd,
+             cos_sin, positions, slot_mapping, static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
+             kv_stride, num_heads, num_kv_heads, block_size};
+  hipStream_t s = as_stream(stream);
+  if (dtype == RG_DTYPE_BF16) launch_gemm_rope<bf16_t>(a, nb, plan.mb, s);
+  else launch_gemm_rope<f16_t>(a, nb, plan.mb, s);
   return check_launch(op);
 }

@@ -202,6 +202,9 @@ class RailgunLlama:
         # rows -> True for rg_linear_silu_mul, False for the projection + rg_silu_and_mul
         self.mlp_choice: dict = {}
         self._w_gate_up_il: dict = {}  # layer -> interleaved gate/up weight
+        # rows -> True for rg_linear_qkv_rope_reshape_and_cache, False for the projection +
+        # rg_qkv_rope_reshape_and_cache
+        self.qkv_choice: dict = {}
         # Hook for measurements: called as attention_hook("begin"/"end", layer) around each
         # layer's attention kernels (None in normal use).
         self.attention_hook = None
@@ -287,6 +290,41 @@ class RailgunLlama:
         else:
             silu_and_mul(self._linear(h, L.w_gate_up), act)
 
+    def _qkv_rope_cache(self, layer: int, h: torch.Tensor, q: torch.Tensor, st: DeviceStep) -> None:
+        """q/k/v = h @ wqkv^T, RoPE on q and k, k and v into the paged cache: fused in the
+        projection's epilogue or as the projection + rg_qkv_rope_reshape_and_cache."""
+        cfg, L = self.cfg, self.w.layers[layer]
+        H, Hkv, D, bs = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, self.pool.block_size
+        kc, vc = self.pool.k_cache(layer), self.pool.v_cache(layer)
+        rows = int(h.shape[0])
+
+        def unfused():
+            self.kernels.launch_qkv_rope_reshape_and_cache(self._linear(h, L.wqkv), q, kc, vc, self.cos_sin,
+                                                          st.positions, st.slot_mapping, H, Hkv, D, bs, rows)
+
+        def fused():
+            self.kernels.launch_linear_qkv_rope_reshape_and_cache(h, L.wqkv, q, kc, vc, self.cos_sin, st.positions,
+                                                                  st.slot_mapping, H, Hkv, D, bs)
+
+        if not (self._rg_linear_fits(h, L.wqkv) and D in (32, 64) and q.is_contiguous()):
+            unfused()
+            return
+        use_fused = self.qkv_choice.get(rows)
+        if use_fused is None:
+            if torch.cuda.is_current_stream_capturing():
+                use_fused = True
+            else:
+                # Both candidates write the same k / v to the step's own slots, so timing them in
+                # place leaves the cache as the step would.
+                self._linear(h, L.wqkv)  # settles the projection's own choice outside the timing
+                t_f, t_u = [], []
+                for _ in range(3):
+                    t_f.append(graph_us(fused, calls=20))
+                    t_u.append(graph_us(unfused, calls=20))
+                use_fused = not sorted(t_u)[1] < 0.95 * sorted(t_f)[1]
+            self.qkv_choice[rows] = use_fused
+        (fused if use_fused else unfused)()
+
     def check_step(self, b: StepBatch) -> None:
         """The kernels trust their indices (as the reference's do): check them on the host."""
         if b.num_tokens and int(b.positions.max()) >= self.cos_sin.shape[0]:
@@ -312,10 +350,7 @@ class RailgunLlama:
         for i, L in enumerate(w.layers):
             # input_layernorm (with the previous MLP's residual add), architecture.rs:49-50
             rms_norm(delta if delta is not None else x, L.input_norm, h, eps, residual=x if delta is not None else None)
-            qkv = self._linear(h, L.wqkv)
-            self.kernels.launch_qkv_rope_reshape_and_cache(qkv, q, self.pool.k_cache(i), self.pool.v_cache(i),
-                                                          self.cos_sin, st.positions, st.slot_mapping, H, Hkv, D,
-                                                          self.pool.block_size, T)
+            self._qkv_rope_cache(i, h, q, st)                   # q/k/v, RoPE, cache write
             if self.attention_hook:
                 self.attention_hook("begin", i)
             self._attention(i, q, attn, st)

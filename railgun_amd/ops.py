@@ -258,6 +258,24 @@ class PagedAttentionKernels:
             cos_sin.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(), num_heads, num_kv_heads, head_dim,
             block_size, num_tokens, dtype_code(qkv), k_cache.stride(0), _stream(qkv)))
 
+    def launch_linear_qkv_rope_reshape_and_cache(self, x, weight_qkv, q_out, k_cache, v_cache, cos_sin, positions,
+                                                 slot_mapping, num_heads: int, num_kv_heads: int, head_dim: int,
+                                                 block_size: int) -> None:
+        """The fused q/k/v projection x @ weight_qkv^T and launch_qkv_rope_reshape_and_cache in one
+        pass (decode batches: x [T <= 128, K], head_dim 32 or 64); rotated q to q_out [T, H, D]."""
+        _require_cuda(x, weight_qkv, q_out, k_cache, v_cache, cos_sin, positions, slot_mapping)
+        _require_i32(positions, slot_mapping)
+        if x.dim() != 2 or x.stride(1) != 1 or not weight_qkv.is_contiguous() or not q_out.is_contiguous() or \
+                x.dtype != weight_qkv.dtype:
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "x must be [T, K] with unit column stride, weight_qkv "
+                                                             "and q_out contiguous, one dtype")
+        tokens, k = (int(d) for d in x.shape)
+        check(self.lib.rg_linear_qkv_rope_reshape_and_cache(
+            x.data_ptr(), weight_qkv.data_ptr(), q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+            cos_sin.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(), tokens, num_heads, num_kv_heads,
+            head_dim, block_size, k, x.stride(0), weight_qkv.stride(0), num_heads * head_dim, k_cache.stride(0),
+            dtype_code(x), _stream(x)))
+
     def launch_copy_blocks(self, src_pool: torch.Tensor, dst_pool: torch.Tensor, block_mapping: torch.Tensor,
                            layered: bool = False) -> None:
         """Whole-block copies (rg_copy_blocks): block ``m[i, 1]`` of ``dst_pool`` becomes block

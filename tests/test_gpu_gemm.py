@@ -125,3 +125,85 @@ def test_linear_silu_mul(device, M, I, K, dt):
     bound = eps * (uv.abs() * dsilu * gv.abs() + 2 * act.abs() * uv.abs() + ref.abs()) + 1e-3 * ref.abs().mean() + 1e-6
     assert bool((err <= bound).all()), f"max excess {float((err - bound).max()):.3g}"
     assert torch.equal(again.view(torch.int16), got.view(torch.int16)), "not deterministic"
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("T,H,Hkv,D,K,bs", [(128, 32, 8, 64, 2048, 16), (1, 32, 8, 64, 2048, 16),
+                                            (37, 8, 2, 32, 256, 32), (100, 4, 4, 64, 384, 16)])
+def test_linear_qkv_rope_reshape_and_cache(device, kernels, T, H, Hkv, D, K, bs, dt):
+    """The q/k/v projection with RoPE and the paged-cache write in its epilogue against the
+    unfused path (rg_linear without split, then rg_qkv_rope_reshape_and_cache on its output).
+    Both round q/k/v to the activation dtype before the rotation and rotate with the same
+    unfused arithmetic; they differ only where the fp32 sums, taken in another order, round
+    q/k/v to the other neighbour: one ulp of the pre-rotation value times |cos| + |sin|, plus
+    one ulp of the result.  Slots of padding tokens (-1) and every other slot stay untouched."""
+    from railgun_amd.ops import linear, rope_cos_sin_table
+    t = TORCH[dt]
+    g = torch.Generator().manual_seed(T * 31 + D + K)
+    x = torch.randn(T, K, generator=g).to(t).to(device)
+    w = (0.05 * torch.randn((H + 2 * Hkv) * D, K, generator=g)).to(t).to(device)
+    nb = max(8, 2 * T // bs + 2)
+    pos = torch.randint(0, 500, (T,), generator=g, dtype=torch.int32).to(device)
+    slots = torch.randperm(nb * bs, generator=g)[:T].to(torch.int32)
+    if T > 3:
+        slots[3] = -1
+    slots = slots.to(device)
+    cs = rope_cos_sin_table(512, D, 500000.0, device)
+    pool_a = torch.randn(nb, 2, Hkv, bs, D, generator=g).to(t).to(device)
+    pool_b = pool_a.clone()
+    q_a = torch.empty(T, H, D, dtype=t, device=device)
+    q_b = torch.empty(T, H, D, dtype=t, device=device)
+    kernels.launch_linear_qkv_rope_reshape_and_cache(x, w, q_a, pool_a[:, 0], pool_a[:, 1], cs, pos, slots,
+                                                     H, Hkv, D, bs)
+    qkv = linear(x, w, workspace=torch.empty(16, dtype=torch.uint8, device=device))
+    kernels.launch_qkv_rope_reshape_and_cache(qkv, q_b, pool_b[:, 0], pool_b[:, 1], cs, pos, slots, H, Hkv, D, bs, T)
+    again = torch.empty_like(q_a)
+    kernels.launch_linear_qkv_rope_reshape_and_cache(x, w, again, pool_a[:, 0], pool_a[:, 1], cs, pos, slots,
+                                                     H, Hkv, D, bs)
+    torch.cuda.synchronize()
+    assert torch.equal(again.view(torch.int16), q_a.view(torch.int16)), "not deterministic"
+
+    eps = 2 ** -7 if dt == "bf16" else 2 ** -10
+    half = D // 2
+    csc = cs.cpu()[pos.cpu().long()]                                     # [T, 2 half]: cos | sin
+    trig = (csc[:, :half].abs() + csc[:, half:].abs()).repeat(1, 2)      # |cos| + |sin| per column
+    pre = (x.float().cpu() @ w.float().cpu().T).view(T, H + 2 * Hkv, D)
+    pre_mag = torch.cat([pre[..., :half], pre[..., half:]], -1).abs()
+    pair = torch.maximum(pre_mag, torch.cat([pre_mag[..., half:], pre_mag[..., :half]], -1))
+
+    def bound(ref, heads, rotated, rows):
+        if rotated:
+            extra = pair[rows][:, heads] * trig[rows][:, None, :]
+        else:
+            extra = pre[rows][:, heads].abs()
+        return eps * (ref.abs() + extra) + 1e-6
+
+    every = torch.arange(T)
+    qa, qb = q_a.float().cpu(), q_b.float().cpu()
+    assert bool(((qa - qb).abs() <= bound(qb, slice(0, H), True, every)).all()), \
+        f"q: max diff {float((qa - qb).abs().max()):.3g}"
+    pa, pb = pool_a.float().cpu(), pool_b.float().cpu()
+    sl = slots.cpu().long()
+    written = torch.zeros(nb * bs, dtype=torch.bool)
+    written[sl[sl >= 0]] = True
+    flat_a = pa.permute(0, 3, 1, 2, 4).reshape(nb * bs, 2, Hkv, D)   # [slot, k/v, head, D]
+    flat_b = pb.permute(0, 3, 1, 2, 4).reshape(nb * bs, 2, Hkv, D)
+    assert torch.equal(flat_a[~written], flat_b[~written]), "wrote a slot outside the mapping"
+    tok = torch.nonzero(sl >= 0).squeeze(1)
+    for kv, heads, rot in ((0, slice(H, H + Hkv), True), (1, slice(H + Hkv, H + 2 * Hkv), False)):
+        got, ref = flat_a[sl[tok], kv], flat_b[sl[tok], kv]
+        assert bool(((got - ref).abs() <= bound(ref, heads, rot, tok)).all()), \
+            f"{'kv'[kv]} cache: max diff {float((got - ref).abs().max()):.3g}"
+
+
+def test_linear_qkv_rope_refuses_unsupported(device, kernels):
+    """Head dims other than 32 / 64 and more than 128 tokens are refused, not mis-computed."""
+    x = torch.zeros(4, 256, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(4 * 128, 256, dtype=torch.bfloat16, device=device)
+    q = torch.empty(4, 2, 128, dtype=torch.bfloat16, device=device)
+    pool = torch.zeros(4, 2, 1, 16, 128, dtype=torch.bfloat16, device=device)
+    cs = torch.zeros(16, 128, dtype=torch.float32, device=device)
+    i = torch.zeros(4, dtype=torch.int32, device=device)
+    with pytest.raises(RailgunError) as e:
+        kernels.launch_linear_qkv_rope_reshape_and_cache(x, w, q, pool[:, 0], pool[:, 1], cs, i, i, 2, 1, 128, 16)
+    assert e.value.code == _lib.RG_ERR_NOT_SUPPORTED

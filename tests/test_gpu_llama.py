@@ -153,8 +153,9 @@ class _AlwaysRgLinear(dict):
 def test_llama_prefill_decode_mixed(device, kernels, name, gemm):
     """Prefill, mixed and decode steps against the CPU model.  With gemm="rg_linear" every
     projection of the mixed (113 rows) and decode (4 rows) steps runs on rg_linear, the MLP's
-    gate/up with SiLU·mul fused (rg_linear_silu_mul); "measured" keeps the per-shape timing
-    choice of normal use."""
+    gate/up with SiLU·mul fused (rg_linear_silu_mul) and q/k/v with RoPE and the cache write
+    fused (rg_linear_qkv_rope_reshape_and_cache); "measured" keeps the per-shape timing choice
+    of normal use."""
     cfg = CONFIGS[name]
     bs, nb = 16, 96
     sd = _hf_state(cfg, 11)
@@ -164,6 +165,7 @@ def test_llama_prefill_decode_mixed(device, kernels, name, gemm):
     if gemm == "rg_linear":
         model.linear_choice = _AlwaysRgLinear()
         model.mlp_choice = _AlwaysRgLinear()
+        model.qkv_choice = _AlwaysRgLinear()
     ref32 = llama_ref.ReferenceLlama(cfg, sd, nb, bs)
     ref16 = llama_ref.ReferenceLlama(cfg, sd, nb, bs, act_dtype=torch.bfloat16)
     rng = np.random.default_rng(7)
