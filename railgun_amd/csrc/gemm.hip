@@ -95,9 +95,9 @@ struct GemmRing {
   static constexpr int SLOTS = FIT >= AHEAD + 2 ? AHEAD + 2 : AHEAD + 1;
   static constexpr bool TWO_BARRIERS = SLOTS == AHEAD + 1;
   static constexpr int PER = MB + NB;  // copies per wave per chunk (1 KB each: 4 rows x 256 B)
-  static constexpr int RED = NB * MB * (kGemmWaves - 1) * 1024;
+  static constexpr int RED = NB * MB * kGemmWaves * 1024;  // every wave's partial of every fragment
   static constexpr int BYTES = SLOTS * SLOT > RED ? SLOTS * SLOT : RED;
-  static_assert(AHEAD >= 1 && AHEAD * PER < 64, "ring does not fit");
+  static_assert(AHEAD >= 1 && AHEAD * PER < 64 && BYTES <= kLdsBytes, "ring does not fit");
 };
 
 // NB: 16-column n-blocks per workgroup, MB: 16-row blocks of X per row tile.  blockIdx.x is
@@ -226,131 +226,109 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
     if constexpr (RG::TWO_BARRIERS) tile_barrier();
   }
 
-  // Fragment f = i * MB + mb is finished by wave f % KS; the other waves leave their partials of
-  // it at [f][(w - owner - 1) mod KS][lane].  Every copy has landed (the last wait was for 0).
+  // Every wave leaves its partial of every fragment f = i * MB + mb at red[f][w]; then wave w
+  // finishes output items w, w + 4, ... (fragments, or the gate / up and rotation pairs of
+  // fragments for kEpiSiluMul and kEpiRope), summing the four partials in wave order.  A wave's
+  // items are independent, so the unrolled loop overlaps one item's LDS reads with another's
+  // arithmetic (the wave is alone on its SIMD here).  Every copy has landed (the last wait was
+  // for 0).
   tile_barrier();
   gf32x4_t* red = reinterpret_cast<gf32x4_t*>(lds);
-  // The wave that finishes fragment (i, mb): with kEpiSiluMul the pair of gate / up blocks i / 2,
-  // with kEpiRope the rotation pair i % (NB / 2).
-  auto owner = [](int i, int mb) {
-    const int pair = EPI == kEpiSiluMul ? i / 2 : EPI == kEpiRope ? i % (NB / 2) : i;
-    return (pair * MB + mb) % KS;
-  };
 #pragma unroll
   for (int i = 0; i < NB; ++i)
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int f = i * MB + mb, own = owner(i, mb);
-      if (w != own) red[(f * (KS - 1) + (w - own - 1 + KS) % KS) * 64 + lane] = acc[i][mb];
-    }
+    for (int mb = 0; mb < MB; ++mb) red[((i * MB + mb) * KS + w) * 64 + lane] = acc[i][mb];
   __syncthreads();
+  auto partial_sum = [&](int f) __attribute__((always_inline)) {
+    gf32x4_t v = red[(f * KS) * 64 + lane];
+#pragma unroll
+    for (int j = 1; j < KS; ++j) v += red[(f * KS + j) * 64 + lane];
+    return v;
+  };
+  auto round_to = [](float v) __attribute__((always_inline)) {
+    return std::is_same<T, bf16_t>::value ? (float)(__bf16)v : (float)(_Float16)v;
+  };
+  constexpr int ITEMS = EPI == kEpiPlain ? NB * MB : (NB / 2) * MB;
+  constexpr int PER_WAVE = (ITEMS + KS - 1) / KS;
 
   if constexpr (EPI == kEpiRope) {
-    using E = elem<T>;
     constexpr int HD = 8 * NB;  // half the head
     const int hg = n0 / (16 * NB);  // head among the H q, H_kv k and H_kv v heads
     const bool is_q = hg < a.num_heads, is_v = hg >= a.num_heads + a.num_kv_heads;
 #pragma unroll
-    for (int p = 0; p < NB / 2; ++p)
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int q = w + KS * j;
+      if (q >= ITEMS) break;
+      const int p = q / MB, mb = q % MB;
+      if (16 * mb + r >= mrows) continue;
+      const gf32x4_t vl = partial_sum(p * MB + mb), vh = partial_sum((p + NB / 2) * MB + mb);
+      const int m = m0 + 16 * mb + r;
+      const int d = 16 * p + 4 * g;  // this lane's columns d .. d + 3 and HD + d ..
+      float ol[4], oh[4];
+      if (is_v) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        if (w != owner(p, mb)) continue;
-        const int fl = p * MB + mb, fh = (p + NB / 2) * MB + mb;
-        gf32x4_t vl = acc[p][mb], vh = acc[p + NB / 2][mb];
+        for (int e = 0; e < 4; ++e) ol[e] = vl[e], oh[e] = vh[e];
+      } else {
+        const float* cs = a.cos_sin + (int64_t)a.positions[m] * (2 * HD);
+        const float4 c4 = *reinterpret_cast<const float4*>(cs + d);
+        const float4 s4 = *reinterpret_cast<const float4*>(cs + HD + d);
+        const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
-        for (int j = 0; j < KS - 1; ++j) {
-          vl += red[(fl * (KS - 1) + j) * 64 + lane];
-          vh += red[(fh * (KS - 1) + j) * 64 + lane];
-        }
-        if (16 * mb + r >= mrows) continue;
-        const int m = m0 + 16 * mb + r;
-        const int d = 16 * p + 4 * g;  // this lane's columns d .. d + 3 and HD + d ..
-        uint16_t ol[4], oh[4];
-        if (is_v) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) ol[e] = E::from_f32(vl[e]), oh[e] = E::from_f32(vh[e]);
-        } else {
-          const float* cs = a.cos_sin + (int64_t)a.positions[m] * (2 * HD);
-          const float4 c4 = *reinterpret_cast<const float4*>(cs + d);
-          const float4 s4 = *reinterpret_cast<const float4*>(cs + HD + d);
-          const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float rl, rh;
-            rope_rotate(E::to_f32(E::from_f32(vl[e])), E::to_f32(E::from_f32(vh[e])), c[e], sn[e], rl, rh);
-            ol[e] = E::from_f32(rl);
-            oh[e] = E::from_f32(rh);
-          }
-        }
-        uint16_t* dst;
-        if (is_q) {
-          dst = a.c + (int64_t)m * a.ldc + (int64_t)hg * (2 * HD);
-        } else {
-          const int32_t slot = a.slots[m];
-          if (slot < 0) continue;  // padding token
-          const int kvh = is_v ? hg - a.num_heads - a.num_kv_heads : hg - a.num_heads;
-          dst = (is_v ? a.v_cache : a.k_cache) + (int64_t)(slot / a.block_size) * a.kv_stride +
-                ((int64_t)kvh * a.block_size + slot % a.block_size) * (2 * HD);
-        }
-        *reinterpret_cast<uint2*>(dst + d) = make_uint2((uint32_t)ol[0] | ((uint32_t)ol[1] << 16),
-                                                        (uint32_t)ol[2] | ((uint32_t)ol[3] << 16));
-        *reinterpret_cast<uint2*>(dst + HD + d) = make_uint2((uint32_t)oh[0] | ((uint32_t)oh[1] << 16),
-                                                             (uint32_t)oh[2] | ((uint32_t)oh[3] << 16));
+        for (int e = 0; e < 4; ++e) rope_rotate(round_to(vl[e]), round_to(vh[e]), c[e], sn[e], ol[e], oh[e]);
       }
+      uint16_t* dst;
+      if (is_q) {
+        dst = a.c + (int64_t)m * a.ldc + (int64_t)hg * (2 * HD);
+      } else {
+        const int32_t slot = a.slots[m];
+        if (slot < 0) continue;  // padding token
+        const int kvh = is_v ? hg - a.num_heads - a.num_kv_heads : hg - a.num_heads;
+        dst = (is_v ? a.v_cache : a.k_cache) + (int64_t)(slot / a.block_size) * a.kv_stride +
+              ((int64_t)kvh * a.block_size + slot % a.block_size) * (2 * HD);
+      }
+      *reinterpret_cast<uint2*>(dst + d) = make_uint2(pack2<T>(ol[0], ol[1]), pack2<T>(ol[2], ol[3]));
+      *reinterpret_cast<uint2*>(dst + HD + d) = make_uint2(pack2<T>(oh[0], oh[1]), pack2<T>(oh[2], oh[3]));
+    }
     return;
   }
 
   if constexpr (EPI == kEpiSiluMul) {
-    using E = elem<T>;
 #pragma unroll
-    for (int jp = 0; jp < NB / 2; ++jp)
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int q = w + KS * j;
+      if (q >= ITEMS) break;
+      const int jp = q / MB, mb = q % MB;
+      if (16 * mb + r >= mrows) continue;
+      const gf32x4_t vg = partial_sum(2 * jp * MB + mb), vu = partial_sum((2 * jp + 1) * MB + mb);
+      float o[4];
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        if (w != owner(2 * jp, mb)) continue;
-        const int fg = 2 * jp * MB + mb, fu = (2 * jp + 1) * MB + mb;
-        gf32x4_t vg = acc[2 * jp][mb], vu = acc[2 * jp + 1][mb];
-#pragma unroll
-        for (int j = 0; j < KS - 1; ++j) {
-          vg += red[(fg * (KS - 1) + j) * 64 + lane];
-          vu += red[(fu * (KS - 1) + j) * 64 + lane];
-        }
-        if (16 * mb + r >= mrows) continue;
-        uint16_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float gv = E::to_f32(E::from_f32(vg[e]));
-          const float uv = E::to_f32(E::from_f32(vu[e]));
-          const float act = E::to_f32(E::from_f32(gv / (1.f + expf(-gv))));
-          o[e] = E::from_f32(act * uv);
-        }
-        const int n = (n0 / 32 + jp) * 16 + 4 * g;
-        *reinterpret_cast<uint2*>(a.c + (int64_t)(m0 + 16 * mb + r) * a.ldc + n) =
-            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+      for (int e = 0; e < 4; ++e) {
+        const float gv = round_to(vg[e]);
+        o[e] = round_to(gv / (1.f + expf(-gv))) * round_to(vu[e]);
       }
+      const int n = (n0 / 32 + jp) * 16 + 4 * g;
+      *reinterpret_cast<uint2*>(a.c + (int64_t)(m0 + 16 * mb + r) * a.ldc + n) =
+          make_uint2(pack2<T>(o[0], o[1]), pack2<T>(o[2], o[3]));
+    }
     return;
   }
 
   // Lane (r, g) holds C[m0 + 16 mb + r][n0 + 16 i + 4g .. +3].
 #pragma unroll
-  for (int i = 0; i < NB; ++i)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int f = i * MB + mb;
-      const int m = m0 + 16 * mb + r;
-      if (w != owner(i, mb)) continue;
-      gf32x4_t v = acc[i][mb];
-#pragma unroll
-      for (int j = 0; j < KS - 1; ++j) v += red[(f * (KS - 1) + j) * 64 + lane];
-      if (16 * mb + r >= mrows) continue;
-      const int n = n0 + 16 * i + 4 * g;
-      if (gridDim.y > 1) {
-        *reinterpret_cast<gf32x4_t*>(a.part + ((int64_t)blockIdx.y * a.M + m) * a.N + n) = v;
-      } else {
-        const uint32_t lo = (uint32_t)elem<T>::from_f32(v[0]) | ((uint32_t)elem<T>::from_f32(v[1]) << 16);
-        const uint32_t hi = (uint32_t)elem<T>::from_f32(v[2]) | ((uint32_t)elem<T>::from_f32(v[3]) << 16);
-        *reinterpret_cast<uint2*>(a.c + (int64_t)m * a.ldc + n) = make_uint2(lo, hi);
-      }
+  for (int j = 0; j < PER_WAVE; ++j) {
+    const int f = w + KS * j;
+    if (f >= ITEMS) break;
+    const int i = f / MB, mb = f % MB;
+    if (16 * mb + r >= mrows) continue;
+    const gf32x4_t v = partial_sum(f);
+    const int m = m0 + 16 * mb + r;
+    const int n = n0 + 16 * i + 4 * g;
+    if (gridDim.y > 1) {
+      *reinterpret_cast<gf32x4_t*>(a.part + ((int64_t)blockIdx.y * a.M + m) * a.N + n) = v;
+    } else {
+      *reinterpret_cast<uint2*>(a.c + (int64_t)m * a.ldc + n) = make_uint2(pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]));
     }
+  }
 }
 
 // out[m][n] = round(sum over the S splits, in split order, of part[s][m][n]): 4 columns per lane.
@@ -406,7 +384,7 @@ int ring_bytes(int nb, int mb) {
   const int fit = kLdsBytes / slot;
   const int ahead = fit >= RG_GEMM_AHEAD + 1 ? RG_GEMM_AHEAD : fit - 1;
   const int slots = fit >= ahead + 2 ? ahead + 2 : ahead + 1;
-  return std::max(slots * slot, nb * mb * (kGemmWaves - 1) * 1024);
+  return std::max(slots * slot, nb * mb * kGemmWaves * 1024);
 }
 
 // Workgroup shape: 16-column n-blocks (NB) and 16-row blocks (MB) per workgroup, row tiles

@@ -201,16 +201,6 @@ constexpr int kSchedSeqs = 256;
 
 constexpr float kSlack = 8.f;           // log2 headroom of the lazy softmax rescale
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-// Two probabilities as one packed operand word (v_cvt_pk_*_f32, round to nearest even).
-template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float hi);
-template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
-}
-template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)lo, (_Float16)hi});
-}
 // acc + lo + hi of a packed pair (v_dot2 with (1, 1), fp32 accumulation).
 template <typename T> __device__ __forceinline__ float pair_sum(uint32_t pair, float acc);
 template <> __device__ __forceinline__ float pair_sum<bf16_t>(uint32_t pair, float acc) {

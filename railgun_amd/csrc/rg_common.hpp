@@ -85,6 +85,18 @@ template <> struct elem<f16_t> {
   __device__ static __forceinline__ uint16_t from_f32(float v) { return f32_to_f16_bits(v); }
 };
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+// Two values rounded to nearest even and packed into one word, low half first
+// (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32).
+template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
+}
+template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)lo, (_Float16)hi});
+}
+
 inline int dtype_bytes(int32_t dtype) {
   switch (dtype) {
     case RG_DTYPE_F32: return 4;

@@ -236,8 +236,30 @@ class RailgunLlama:
                 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 and weight.is_contiguous()
                 and weight.data_ptr() % 16 == 0 and x.dtype in (torch.bfloat16, torch.float16))
 
-    def _linear(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-        """x @ weight^T on rg_linear or hipBLASLt, per the measured choice for the shape."""
+    def _peers(self, name: str) -> list:
+        """The weight `name` of every layer (the LM head alone for "lm_head")."""
+        if name == "lm_head":
+            return [self.w.lm_head]
+        return [getattr(L, name) for L in self.w.layers]
+
+    @staticmethod
+    def _time_pair(run_a, run_b, n: int) -> tuple:
+        """Device times of run_a(j) and run_b(j) for j = 0 .. n - 1 under graph replay, medians of
+        three interleaved trials (a clock or load change on the device hits both).  Each j is
+        another layer's weight, so the weights stream from HBM as they do in a step rather than
+        from the 256 MB last-level cache that a single weight timed in a loop would sit in."""
+        calls = max(1, 20 // n)
+        t_a, t_b = [], []
+        for _ in range(3):
+            t_a.append(graph_us(lambda: [run_a(j) for j in range(n)], calls=calls))
+            t_b.append(graph_us(lambda: [run_b(j) for j in range(n)], calls=calls))
+        return sorted(t_a)[1], sorted(t_b)[1]
+
+    def _linear(self, x: torch.Tensor, name: str, layer: int = 0) -> torch.Tensor:
+        """x @ weight^T for the weight `name` of `layer`, on rg_linear or hipBLASLt per the
+        measured choice for the shape."""
+        peers = self._peers(name)
+        weight = peers[layer]
         if not self._rg_linear_fits(x, weight):
             return F.linear(x, weight)
         rows, k, n = int(x.shape[0]), int(x.shape[1]), int(weight.shape[0])
@@ -250,13 +272,9 @@ class RailgunLlama:
             else:
                 out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
                 ws = self._workspace(ws_bytes)
-                # Three interleaved trials each (so that a clock or load change on the device hits
-                # both), compared by their medians.
-                t_rg, t_blas = [], []
-                for _ in range(3):
-                    t_rg.append(graph_us(lambda: linear(x, weight, out, ws), calls=20))
-                    t_blas.append(graph_us(lambda: F.linear(x, weight), calls=20))
-                use_rg = not sorted(t_blas)[1] < 0.95 * sorted(t_rg)[1]
+                t_rg, t_blas = self._time_pair(lambda j: linear(x, peers[j], out, ws),
+                                               lambda j: F.linear(x, peers[j]), len(peers))
+                use_rg = not t_blas < 0.95 * t_rg
             self.linear_choice[key] = use_rg
         if not use_rg:
             return F.linear(x, weight)
@@ -268,27 +286,31 @@ class RailgunLlama:
         inter = int(act.shape[1])
         rows = int(h.shape[0])
         if not (self._rg_linear_fits(h, L.w_gate_up) and inter % 16 == 0):
-            silu_and_mul(self._linear(h, L.w_gate_up), act)
+            silu_and_mul(self._linear(h, "w_gate_up", layer), act)
             return
-        w_il = self._w_gate_up_il.get(layer)
-        if w_il is None:
-            w_il = self._w_gate_up_il[layer] = interleave_gate_up(L.w_gate_up)
         fused = self.mlp_choice.get(rows)
         if fused is None:
             if torch.cuda.is_current_stream_capturing():
                 fused = True
             else:
-                self._linear(h, L.w_gate_up)  # settles the projection's own choice outside the timing
-                t_f, t_s = [], []
-                for _ in range(3):
-                    t_f.append(graph_us(lambda: linear_silu_mul(h, w_il, act), calls=20))
-                    t_s.append(graph_us(lambda: silu_and_mul(self._linear(h, L.w_gate_up), act), calls=20))
-                fused = not sorted(t_s)[1] < 0.95 * sorted(t_f)[1]
+                n = len(self.w.layers)
+                for j in range(n):
+                    if j not in self._w_gate_up_il:
+                        self._w_gate_up_il[j] = interleave_gate_up(self.w.layers[j].w_gate_up)
+                self._linear(h, "w_gate_up", layer)  # settles the projection's own choice outside the timing
+                t_f, t_s = self._time_pair(lambda j: linear_silu_mul(h, self._w_gate_up_il[j], act),
+                                           lambda j: silu_and_mul(self._linear(h, "w_gate_up", j), act), n)
+                fused = not t_s < 0.95 * t_f
+                if not fused and not any(self.mlp_choice.values()):
+                    self._w_gate_up_il.clear()
             self.mlp_choice[rows] = fused
         if fused:
+            w_il = self._w_gate_up_il.get(layer)
+            if w_il is None:
+                w_il = self._w_gate_up_il[layer] = interleave_gate_up(L.w_gate_up)
             linear_silu_mul(h, w_il, act)
         else:
-            silu_and_mul(self._linear(h, L.w_gate_up), act)
+            silu_and_mul(self._linear(h, "w_gate_up", layer), act)
 
     def _qkv_rope_cache(self, layer: int, h: torch.Tensor, q: torch.Tensor, st: DeviceStep) -> None:
         """q/k/v = h @ wqkv^T, RoPE on q and k, k and v into the paged cache: fused in the
@@ -297,33 +319,31 @@ class RailgunLlama:
         H, Hkv, D, bs = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, self.pool.block_size
         kc, vc = self.pool.k_cache(layer), self.pool.v_cache(layer)
         rows = int(h.shape[0])
+        peers = self._peers("wqkv")
 
-        def unfused():
-            self.kernels.launch_qkv_rope_reshape_and_cache(self._linear(h, L.wqkv), q, kc, vc, self.cos_sin,
+        # Both forms write into this layer's cache; timed with another layer's weight they leave
+        # other values at the step's slots, which the call below overwrites.
+        def unfused(j):
+            self.kernels.launch_qkv_rope_reshape_and_cache(self._linear(h, "wqkv", j), q, kc, vc, self.cos_sin,
                                                           st.positions, st.slot_mapping, H, Hkv, D, bs, rows)
 
-        def fused():
-            self.kernels.launch_linear_qkv_rope_reshape_and_cache(h, L.wqkv, q, kc, vc, self.cos_sin, st.positions,
+        def fused(j):
+            self.kernels.launch_linear_qkv_rope_reshape_and_cache(h, peers[j], q, kc, vc, self.cos_sin, st.positions,
                                                                   st.slot_mapping, H, Hkv, D, bs)
 
         if not (self._rg_linear_fits(h, L.wqkv) and D in (32, 64) and q.is_contiguous()):
-            unfused()
+            unfused(layer)
             return
         use_fused = self.qkv_choice.get(rows)
         if use_fused is None:
             if torch.cuda.is_current_stream_capturing():
                 use_fused = True
             else:
-                # Both candidates write the same k / v to the step's own slots, so timing them in
-                # place leaves the cache as the step would.
-                self._linear(h, L.wqkv)  # settles the projection's own choice outside the timing
-                t_f, t_u = [], []
-                for _ in range(3):
-                    t_f.append(graph_us(fused, calls=20))
-                    t_u.append(graph_us(unfused, calls=20))
-                use_fused = not sorted(t_u)[1] < 0.95 * sorted(t_f)[1]
+                self._linear(h, "wqkv", layer)  # settles the projection's own choice outside the timing
+                t_f, t_u = self._time_pair(fused, unfused, len(peers))
+                use_fused = not t_u < 0.95 * t_f
             self.qkv_choice[rows] = use_fused
-        (fused if use_fused else unfused)()
+        (fused if use_fused else unfused)(layer)
 
     def check_step(self, b: StepBatch) -> None:
         """The kernels trust their indices (as the reference's do): check them on the host."""
@@ -356,13 +376,13 @@ class RailgunLlama:
             self._attention(i, q, attn, st)
             if self.attention_hook:
                 self.attention_hook("end", i)
-            delta = self._linear(attn.view(T, H * D), L.wo)
+            delta = self._linear(attn.view(T, H * D), "wo", i)
             # residual add + post_attention_layernorm, architecture.rs:53-57
             rms_norm(delta, L.post_norm, h, eps, residual=x)
             self._mlp_act(i, h, act)                            # LlamaMLP, architecture.rs:80-84
-            delta = self._linear(act, L.w_down)
+            delta = self._linear(act, "w_down", i)
         rms_norm(delta, w.norm, h, eps, residual=x)            # last residual add + model.norm
-        return self._linear(h.index_select(0, st.last_rows), w.lm_head)
+        return self._linear(h.index_select(0, st.last_rows), "lm_head")
 
 
 __all__ = ["DeviceStep", "LLAMA_3_2_1B", "LayerWeights", "LlamaConfig", "LlamaWeights",
