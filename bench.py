@@ -349,6 +349,10 @@ def side_model(device, steps: int) -> dict:
     gemm["mlp"] = "fused gate/up + SiLU·mul" if model.mlp_choice.get(w.batch) else "gate/up + rg_silu_and_mul"
     gemm["qkv"] = ("fused qkv + RoPE + cache write" if model.qkv_choice.get(w.batch)
                    else "qkv + rg_qkv_rope_reshape_and_cache")
+    fold = model.norm_chain.get(w.batch, (False, False))
+    gemm["norms"] = {"input_norm": "folded into qkv (residual add in down_proj)" if fold[0] else "rg_rms_norm",
+                     "post_attention_norm": "folded into gate/up (residual add in o_proj)" if fold[1]
+                     else "rg_rms_norm"}
     del model, pool, weights, graph
     torch.cuda.empty_cache()
     return {"workload": w.name, "model": "llama-3.2-1b (random init, bf16)", "batch": w.batch,

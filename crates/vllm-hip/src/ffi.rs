@@ -100,6 +100,26 @@ extern "C" {
     ) -> c_int;
     /// Split-K workspace of rg_linear for this shape (0: runs unsplit).
     pub fn rg_linear_workspace_bytes(num_rows: i32, out_features: i32, in_features: i32) -> usize;
+    /// New: residual += x . weight^T (the o_proj / down_proj output and the residual add).
+    pub fn rg_linear_residual(
+        x: *const c_void, weight: *const c_void, residual: *mut c_void, num_rows: i32, out_features: i32,
+        in_features: i32, x_row_stride: i64, weight_row_stride: i64, residual_row_stride: i64,
+        workspace: *mut c_void, workspace_bytes: usize, dtype: i32, stream: *mut c_void,
+    ) -> c_int;
+    /// New: RmsNorm folded into the gate/up projection with SiLU·mul.
+    pub fn rg_rms_norm_linear_silu_mul(
+        x: *const c_void, norm_weight: *const c_void, eps: f32, weight_gate_up: *const c_void, out: *mut c_void,
+        num_rows: i32, intermediate_size: i32, in_features: i32, x_row_stride: i64, weight_row_stride: i64,
+        out_row_stride: i64, dtype: i32, stream: *mut c_void,
+    ) -> c_int;
+    /// New: RmsNorm folded into the q/k/v projection with RoPE and the cache write.
+    pub fn rg_rms_norm_linear_qkv_rope_reshape_and_cache(
+        x: *const c_void, norm_weight: *const c_void, eps: f32, weight_qkv: *const c_void, q_out: *mut c_void,
+        k_cache: *mut c_void, v_cache: *mut c_void, cos_sin: *const f32, positions: *const i32,
+        slot_mapping: *const i32, num_tokens: i32, num_heads: i32, num_kv_heads: i32, head_dim: i32,
+        block_size: i32, in_features: i32, x_row_stride: i64, weight_row_stride: i64, q_out_token_stride: i64,
+        kv_block_stride: i64, dtype: i32, stream: *mut c_void,
+    ) -> c_int;
     /// New: the gate/up projection and SiLU·mul in one pass (interleaved gate/up weight).
     pub fn rg_linear_silu_mul(
         x: *const c_void, weight_gate_up: *const c_void, out: *mut c_void, num_rows: i32, intermediate_size: i32,

@@ -546,6 +546,75 @@ impl PagedAttentionKernels {
                               x_row_stride, weight_row_stride, out_row_stride, ws, ws_len, T::DTYPE, self.stream))
     }
 
+    /// residual [num_rows, out_features] += x . weight^T, rounded as launch_linear followed by
+    /// the residual add of launch_rms_norm; the workspace as for launch_linear.
+    pub unsafe fn launch_linear_residual<T: KvElement>(
+        &self,
+        x: &HipSlice<T>,
+        weight: &HipSlice<T>,
+        residual: &mut HipSlice<T>,
+        num_rows: i32,
+        out_features: i32,
+        in_features: i32,
+        x_row_stride: i64,
+        weight_row_stride: i64,
+        residual_row_stride: i64,
+        workspace: Option<&mut HipSlice<u8>>,
+    ) -> CoreResult<()> {
+        let (ws, ws_len) = workspace.map_or((std::ptr::null_mut(), 0), |w| (w.as_mut_ptr(), w.len()));
+        status(ffi::rg_linear_residual(x.as_ptr(), weight.as_ptr(), residual.as_mut_ptr(), num_rows, out_features,
+                                       in_features, x_row_stride, weight_row_stride, residual_row_stride, ws, ws_len,
+                                       T::DTYPE, self.stream))
+    }
+
+    /// launch_linear_silu_mul on the RmsNorm of the residual stream x (norm weight [in_features]).
+    pub unsafe fn launch_rms_norm_linear_silu_mul<T: KvElement>(
+        &self,
+        x: &HipSlice<T>,
+        norm_weight: &HipSlice<T>,
+        eps: f32,
+        weight_gate_up: &HipSlice<T>,
+        out: &mut HipSlice<T>,
+        num_rows: i32,
+        intermediate_size: i32,
+        in_features: i32,
+        x_row_stride: i64,
+    ) -> CoreResult<()> {
+        status(ffi::rg_rms_norm_linear_silu_mul(x.as_ptr(), norm_weight.as_ptr(), eps, weight_gate_up.as_ptr(),
+                                                out.as_mut_ptr(), num_rows, intermediate_size, in_features,
+                                                x_row_stride, in_features as i64, intermediate_size as i64,
+                                                T::DTYPE, self.stream))
+    }
+
+    /// launch_linear_qkv_rope_reshape_and_cache on the RmsNorm of the residual stream x.
+    pub unsafe fn launch_rms_norm_linear_qkv_rope_reshape_and_cache<T: KvElement>(
+        &self,
+        x: &HipSlice<T>,
+        norm_weight: &HipSlice<T>,
+        eps: f32,
+        weight_qkv: &HipSlice<T>,
+        q_out: &mut HipSlice<T>,
+        k_cache: &mut HipSlice<T>,
+        v_cache: &mut HipSlice<T>,
+        cos_sin: &HipSlice<f32>,
+        positions: &HipSlice<i32>,
+        slot_mapping: &HipSlice<i32>,
+        num_tokens: i32,
+        num_heads: i32,
+        num_kv_heads: i32,
+        head_dim: i32,
+        block_size: i32,
+        in_features: i32,
+        x_row_stride: i64,
+    ) -> CoreResult<()> {
+        status(ffi::rg_rms_norm_linear_qkv_rope_reshape_and_cache(
+            x.as_ptr(), norm_weight.as_ptr(), eps, weight_qkv.as_ptr(), q_out.as_mut_ptr(), k_cache.as_mut_ptr(),
+            v_cache.as_mut_ptr(), cos_sin.as_ptr() as *const f32, positions.as_ptr() as *const i32,
+            slot_mapping.as_ptr() as *const i32, num_tokens, num_heads, num_kv_heads, head_dim, block_size,
+            in_features, x_row_stride, in_features as i64, (num_heads * head_dim) as i64, self.kv_block_stride,
+            T::DTYPE, self.stream))
+    }
+
     /// out = silu(gate) * up over the fused gate/up projection output.
     pub unsafe fn launch_silu_and_mul<T: KvElement>(
         &self,

@@ -247,6 +247,38 @@ int rg_linear_qkv_rope_reshape_and_cache(const void* x, const void* weight_qkv, 
                                          int64_t q_out_token_stride, int64_t kv_block_stride,
                                          int32_t dtype, void* stream);
 
+/* A decode-step projection added to the residual stream (the o_proj / down_proj output and the
+ * residual add of the next RmsNorm, architecture.rs:50-57):
+ *   residual[m, n] = round(residual[m, n] + round(x[m] . weight[n])),
+ * the arithmetic of rg_linear followed by the residual add of rg_rms_norm.  residual is
+ * [num_rows, out_features] (residual_row_stride elements between rows); the constraints and the
+ * optional split-K workspace of rg_linear (rg_linear_workspace_bytes).  New entry. */
+int rg_linear_residual(const void* x, const void* weight, void* residual, int32_t num_rows,
+                       int32_t out_features, int32_t in_features, int64_t x_row_stride,
+                       int64_t weight_row_stride, int64_t residual_row_stride, void* workspace,
+                       size_t workspace_bytes, int32_t dtype, void* stream);
+
+/* RmsNorm of the residual stream folded into the projection that follows it (architecture.rs:
+ * 49-50 with 104-125, and 56-57 with 80-84): with s_m = 1 / sqrt(mean_k(x[m, k]^2) + eps) over
+ * the fp32 values of row m, the projection of row m is s_m * sum_k x[m, k] W[n, k] norm_weight[k]
+ * with one of x[m, k] norm_weight[k] or W[n, k] norm_weight[k] rounded to the operand type, and
+ * rounded as the projection's output — in place of round(x s w) . W (rg_rms_norm, then the
+ * GEMM): the same values up to one rounding of each operand product.  Otherwise as
+ * rg_linear_silu_mul and rg_linear_qkv_rope_reshape_and_cache; in_features at most 8192,
+ * norm_weight [in_features], 16-byte aligned.  New entries. */
+int rg_rms_norm_linear_silu_mul(const void* x, const void* norm_weight, float eps, const void* weight_gate_up,
+                                void* out, int32_t num_rows, int32_t intermediate_size, int32_t in_features,
+                                int64_t x_row_stride, int64_t weight_row_stride, int64_t out_row_stride,
+                                int32_t dtype, void* stream);
+int rg_rms_norm_linear_qkv_rope_reshape_and_cache(const void* x, const void* norm_weight, float eps,
+                                                  const void* weight_qkv, void* q_out, void* k_cache,
+                                                  void* v_cache, const float* cos_sin, const int32_t* positions,
+                                                  const int32_t* slot_mapping, int32_t num_tokens,
+                                                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                                  int32_t block_size, int32_t in_features, int64_t x_row_stride,
+                                                  int64_t weight_row_stride, int64_t q_out_token_stride,
+                                                  int64_t kv_block_stride, int32_t dtype, void* stream);
+
 /* Opt-in index checks (new entries, no counterpart: the reference's launchers pass indices to the
  * kernels unchecked, crates/vllm-cuda/src/kernels/mod.rs:196-508, as do this library's kernel
  * entries).  Each scans on the device, synchronises `stream` and returns RG_ERR_INVALID_ARGUMENT

@@ -82,6 +82,11 @@ SIGNATURES = {
     "rg_linear_silu_mul": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64,
                                    c_int32, c_void_p]),
     "rg_linear_qkv_rope_reshape_and_cache": (c_int, [c_void_p] * 8 + [c_int32] * 6 + [c_int64] * 4 + [c_int32, c_void_p]),
+    "rg_linear_residual": (c_int, [c_void_p] * 3 + [c_int32] * 3 + [c_int64] * 3 + [c_void_p, c_size_t, c_int32, c_void_p]),
+    "rg_rms_norm_linear_silu_mul": (c_int, [c_void_p, c_void_p, c_float, c_void_p, c_void_p] + [c_int32] * 3
+                                    + [c_int64] * 3 + [c_int32, c_void_p]),
+    "rg_rms_norm_linear_qkv_rope_reshape_and_cache": (c_int, [c_void_p, c_void_p, c_float] + [c_void_p] * 7
+                                                      + [c_int32] * 6 + [c_int64] * 4 + [c_int32, c_void_p]),
     "rg_validate_block_tables": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p]),
     "rg_validate_slot_mapping": (c_int, [c_void_p, c_int32, c_int64, c_void_p]),
     "rg_paged_attention_v1_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),

@@ -70,6 +70,9 @@ struct GemmArgs {
   uint16_t* v_cache;
   int64_t kv_stride;        // elements between cache blocks
   int32_t num_heads, num_kv_heads, block_size;
+  // NORM kernels: X rows are RMS-normalised with this weight [K] (see the kernel).
+  const uint16_t* norm_w;
+  float norm_eps;
 };
 
 template <int N>
@@ -85,10 +88,10 @@ constexpr int kLdsBytes = 160 * 1024;
 constexpr int kGemmThreads = 64 * kGemmWaves;
 
 // LDS ring of one instantiation: a slot holds a chunk of X (16 MB rows) then of W (16 NB rows).
-template <int NB, int MB>
+template <int NB, int MB, int RESERVE = 0>
 struct GemmRing {
   static constexpr int SLOT = 16 * (MB + NB) * kChunkBytes;
-  static constexpr int FIT = kLdsBytes / SLOT;
+  static constexpr int FIT = (kLdsBytes - RESERVE) / SLOT;
   // AHEAD chunks in flight; with AHEAD + 2 slots the slot a wave refills was read two chunks ago,
   // so one barrier per chunk orders it; with AHEAD + 1 a second barrier follows the MFMAs.
   static constexpr int AHEAD = FIT >= RG_GEMM_AHEAD + 1 ? RG_GEMM_AHEAD : FIT - 1;
@@ -97,7 +100,7 @@ struct GemmRing {
   static constexpr int PER = MB + NB;  // copies per wave per chunk (1 KB each: 4 rows x 256 B)
   static constexpr int RED = NB * MB * kGemmWaves * 1024;  // every wave's partial of every fragment
   static constexpr int BYTES = SLOTS * SLOT > RED ? SLOTS * SLOT : RED;
-  static_assert(AHEAD >= 1 && AHEAD * PER < 64 && BYTES <= kLdsBytes, "ring does not fit");
+  static_assert(AHEAD >= 1 && AHEAD * PER < 64 && BYTES + RESERVE <= kLdsBytes, "ring does not fit");
 };
 
 // NB: 16-column n-blocks per workgroup, MB: 16-row blocks of X per row tile.  blockIdx.x is
@@ -128,6 +131,59 @@ struct GemmRing {
 constexpr int kEpiPlain = 0;
 constexpr int kEpiSiluMul = 1;
 constexpr int kEpiRope = 2;
+constexpr int kEpiResidual = 3;  // C[m][n] <- round(C[m][n] + round(X . W^T)): the residual add
+// Largest K of the NORM kernels (their norm weight is staged whole in LDS).
+constexpr int kNormMaxK = 8192;
+
+// The 8 values of a 16-byte fragment as floats.
+template <typename T>
+__device__ __forceinline__ void unpack8(uint4 u, float* f) {
+  const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = elem<T>::to_f32((uint16_t)(wd[i] & 0xffffu));
+    f[2 * i + 1] = elem<T>::to_f32((uint16_t)(wd[i] >> 16));
+  }
+}
+
+// round(v[e] * f[e]) for the 8 values of a fragment.
+template <typename T>
+__device__ __forceinline__ uint4 scale8(uint4 u, const float* f) {
+  float v[8];
+  unpack8<T>(u, v);
+  return make_uint4(pack2<T>(v[0] * f[0], v[1] * f[1]), pack2<T>(v[2] * f[2], v[3] * f[3]),
+                    pack2<T>(v[4] * f[4], v[5] * f[5]), pack2<T>(v[6] * f[6], v[7] * f[7]));
+}
+
+// acc + the sum of the squares of a fragment's 8 values (four dot2 steps, fp32 accumulation).
+template <typename T> __device__ __forceinline__ float sum_squares8(uint4 u, float acc);
+template <> __device__ __forceinline__ float sum_squares8<bf16_t>(uint4 u, float acc) {
+  const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wd[i]), __builtin_bit_cast(bf16x2_t, wd[i]),
+                                          acc, false);
+  }
+  return acc;
+}
+template <> __device__ __forceinline__ float sum_squares8<f16_t>(uint4 u, float acc) {
+  const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, wd[i]), __builtin_bit_cast(f16x2_t, wd[i]), acc, false);
+  }
+  return acc;
+}
+
+// Four stored values plus round(v): round(c + round(v)) per value (the residual add of
+// rms_norm_kernel on a rounded projection output).
+template <typename T>
+__device__ __forceinline__ uint2 add_rounded(uint2 c, gf32x4_t v) {
+  const float c0 = elem<T>::to_f32((uint16_t)(c.x & 0xffffu)), c1 = elem<T>::to_f32((uint16_t)(c.x >> 16));
+  const float c2 = elem<T>::to_f32((uint16_t)(c.y & 0xffffu)), c3 = elem<T>::to_f32((uint16_t)(c.y >> 16));
+  auto rnd = [](float x) { return std::is_same<T, bf16_t>::value ? (float)(__bf16)x : (float)(_Float16)x; };
+  return make_uint2(pack2<T>(c0 + rnd(v[0]), c1 + rnd(v[1])), pack2<T>(c2 + rnd(v[2]), c3 + rnd(v[3])));
+}
 
 // out = (lo c - hi s, hi c + lo s), unfused (the rotation of rope_cache_kernel).
 __device__ __forceinline__ void rope_rotate(float lo, float hi, float c, float s, float& out_lo, float& out_hi) {
@@ -139,14 +195,17 @@ __device__ __forceinline__ void rope_rotate(float lo, float hi, float c, float s
   out_lo = a - b;
   out_hi = e + f;
 }
-template <typename T, int NB, int MB, int EPI>
+template <typename T, int NB, int MB, int EPI, bool NORM = false>
 __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
-  static_assert(EPI == kEpiPlain || NB % 2 == 0, "gate/up and rotation pairs need an even number of n-blocks");
+  static_assert(EPI == kEpiPlain || EPI == kEpiResidual || NB % 2 == 0,
+                "gate/up and rotation pairs need an even number of n-blocks");
   using MF = gemm_mfma<T>;
-  using RG = GemmRing<NB, MB>;
+  constexpr int NORM_BYTES = NORM ? 2 * kNormMaxK : 0;
+  using RG = GemmRing<NB, MB, NORM_BYTES>;
   constexpr int KS = kGemmWaves;
   constexpr int D = RG::AHEAD;
-  __shared__ __attribute__((aligned(16))) char lds[RG::BYTES];
+  static_assert(RG::BYTES + NORM_BYTES <= kLdsBytes, "norm weight does not fit");
+  __shared__ __attribute__((aligned(16))) char lds[RG::BYTES + NORM_BYTES];
   const uint32_t lds_base = (uint32_t)(uintptr_t)((RG_LDS char*)lds);
 
   const int lane = threadIdx.x & 63;
@@ -200,6 +259,21 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[i][mb] = gf32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  // NORM: wave 0 copies the norm weight into LDS ahead of its first chunk, so the first chunk's
+  // wait covers it (copies complete in issue order for the counter).
+  if constexpr (NORM) {
+    if (w == 0) {
+      const uint32_t nbytes = (uint32_t)a.K * 2;
+      for (uint32_t q = 0; q * 1024 < nbytes; ++q) {
+        lds_dma16_s(reinterpret_cast<const char*>(a.norm_w), min(q * 1024 + (uint32_t)lane * 16, nbytes - 16),
+                    lds_base + (uint32_t)RG::BYTES + q * 1024);
+      }
+    }
+  }
+  float ss[MB];  // NORM: this lane's part of the sum of squares of row 16 mb + r
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) ss[mb] = 0.f;
+
   // Fragment reads: row R of the slot's X (or W) rows, piece 4w + g of the chunk.
   const int piece = ((4 * w + g) ^ r) << 4;
   for (int c = 0; c < D && c < chunks; ++c) issue(c);
@@ -217,9 +291,26 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
     for (int i = 0; i < NB; ++i) {
       wv[i] = *reinterpret_cast<const uint4*>(slot + (16 * MB + 16 * i + r) * kChunkBytes + piece);
     }
+    // NORM: the MFMA takes x and W with one of them scaled by the norm weight of its k and
+    // rounded — W when the tile has fewer W fragments than X fragments, else x — and the row
+    // scale 1 / rms(x) is applied to the sums at the end.
+    constexpr bool SCALE_W = NB < MB;
+    float nw[8];  // the norm weight of this lane's 8 k
+    if constexpr (NORM) {
+      const uint4 u = *reinterpret_cast<const uint4*>(lds + RG::BYTES + (cb + c) * kChunkBytes + (4 * w + g) * 16);
+      unpack8<T>(u, nw);
+      if constexpr (SCALE_W) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) wv[i] = scale8<T>(wv[i], nw);
+      }
+    }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const uint4 xv = *reinterpret_cast<const uint4*>(slot + (16 * mb + r) * kChunkBytes + piece);
+      uint4 xv = *reinterpret_cast<const uint4*>(slot + (16 * mb + r) * kChunkBytes + piece);
+      if constexpr (NORM) {
+        ss[mb] = sum_squares8<T>(xv, ss[mb]);
+        if constexpr (!SCALE_W) xv = scale8<T>(xv, nw);
+      }
 #pragma unroll
       for (int i = 0; i < NB; ++i) acc[i][mb] = MF::run(wv[i], xv, acc[i][mb]);
     }
@@ -238,17 +329,40 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
   for (int i = 0; i < NB; ++i)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) red[((i * MB + mb) * KS + w) * 64 + lane] = acc[i][mb];
+  // NORM: the row sums of squares, over the 4 lanes of a row (k pieces g), then over the waves
+  // (k-steps w) through the norm weight's LDS, which no wave reads any more.
+  float* sq = reinterpret_cast<float*>(lds + RG::BYTES);
+  if constexpr (NORM) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      ss[mb] += __shfl_xor(ss[mb], 16);
+      ss[mb] += __shfl_xor(ss[mb], 32);
+      if (g == 0) sq[(w * MB + mb) * 16 + r] = ss[mb];
+    }
+  }
   __syncthreads();
+  float rs[MB];  // NORM: 1 / rms of row 16 mb + r
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    rs[mb] = 1.f;
+    if constexpr (NORM) {
+      float t = sq[mb * 16 + r];
+#pragma unroll
+      for (int j = 1; j < KS; ++j) t += sq[(j * MB + mb) * 16 + r];
+      rs[mb] = rsqrtf(t / (float)a.K + a.norm_eps);
+    }
+  }
   auto partial_sum = [&](int f) __attribute__((always_inline)) {
     gf32x4_t v = red[(f * KS) * 64 + lane];
 #pragma unroll
     for (int j = 1; j < KS; ++j) v += red[(f * KS + j) * 64 + lane];
+    if constexpr (NORM) v *= rs[f % MB];
     return v;
   };
   auto round_to = [](float v) __attribute__((always_inline)) {
     return std::is_same<T, bf16_t>::value ? (float)(__bf16)v : (float)(_Float16)v;
   };
-  constexpr int ITEMS = EPI == kEpiPlain ? NB * MB : (NB / 2) * MB;
+  constexpr int ITEMS = EPI == kEpiPlain || EPI == kEpiResidual ? NB * MB : (NB / 2) * MB;
   constexpr int PER_WAVE = (ITEMS + KS - 1) / KS;
 
   if constexpr (EPI == kEpiRope) {
@@ -326,65 +440,70 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
     if (gridDim.y > 1) {
       *reinterpret_cast<gf32x4_t*>(a.part + ((int64_t)blockIdx.y * a.M + m) * a.N + n) = v;
     } else {
-      *reinterpret_cast<uint2*>(a.c + (int64_t)m * a.ldc + n) = make_uint2(pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]));
+      uint2* dst = reinterpret_cast<uint2*>(a.c + (int64_t)m * a.ldc + n);
+      if constexpr (EPI == kEpiResidual) *dst = add_rounded<T>(*dst, v);
+      else *dst = make_uint2(pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]));
     }
   }
 }
 
 // out[m][n] = round(sum over the S splits, in split order, of part[s][m][n]): 4 columns per lane.
-template <typename T>
+// RES: out[m][n] = round(out[m][n] + round(sum)), the residual add.
+template <typename T, bool RES>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a, int S) {
   const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (idx >= (int64_t)a.M * a.N) return;
   const int m = (int)(idx / a.N), n = (int)(idx % a.N);
   gf32x4_t v = *reinterpret_cast<const gf32x4_t*>(a.part + idx);
   for (int s = 1; s < S; ++s) v += *reinterpret_cast<const gf32x4_t*>(a.part + (int64_t)s * a.M * a.N + idx);
-  const uint32_t lo = (uint32_t)elem<T>::from_f32(v[0]) | ((uint32_t)elem<T>::from_f32(v[1]) << 16);
-  const uint32_t hi = (uint32_t)elem<T>::from_f32(v[2]) | ((uint32_t)elem<T>::from_f32(v[3]) << 16);
-  *reinterpret_cast<uint2*>(a.c + (int64_t)m * a.ldc + n) = make_uint2(lo, hi);
+  uint2* dst = reinterpret_cast<uint2*>(a.c + (int64_t)m * a.ldc + n);
+  if constexpr (RES) *dst = add_rounded<T>(*dst, v);
+  else *dst = make_uint2(pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]));
 }
 
-template <typename T, int NB, int EPI = kEpiPlain>
+template <typename T, int NB, int EPI = kEpiPlain, bool NORM = false>
 void launch_gemm_mb(const GemmArgs& a, int mb, int splits, hipStream_t s) {
   const dim3 grid((unsigned)(a.N / (16 * NB) * a.mtiles), (unsigned)splits);
   switch (mb) {
-    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 1, EPI>), grid, dim3(kGemmThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 2, EPI>), grid, dim3(kGemmThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 4, EPI>), grid, dim3(kGemmThreads), 0, s, a); break;
-    default: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 8, EPI>), grid, dim3(kGemmThreads), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 1, EPI, NORM>), grid, dim3(kGemmThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 2, EPI, NORM>), grid, dim3(kGemmThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 4, EPI, NORM>), grid, dim3(kGemmThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL((skinny_gemm_kernel<T, NB, 8, EPI, NORM>), grid, dim3(kGemmThreads), 0, s, a); break;
   }
-  if (EPI == kEpiPlain && splits > 1) {
+  if ((EPI == kEpiPlain || EPI == kEpiResidual) && splits > 1) {
     const int64_t quads = (int64_t)a.M * a.N / 4;
-    hipLaunchKernelGGL(splitk_reduce_kernel<T>, dim3((unsigned)ceil_div(quads, 256)), dim3(256), 0, s, a, splits);
+    hipLaunchKernelGGL((splitk_reduce_kernel<T, EPI == kEpiResidual>), dim3((unsigned)ceil_div(quads, 256)), dim3(256),
+                       0, s, a, splits);
   }
 }
 
-template <typename T>
+template <typename T, int EPI = kEpiPlain>
 void launch_gemm(const GemmArgs& a, int nb, int mb, int splits, hipStream_t s) {
-  if (nb == 4) launch_gemm_mb<T, 4>(a, mb, splits, s);
-  else if (nb == 2) launch_gemm_mb<T, 2>(a, mb, splits, s);
-  else launch_gemm_mb<T, 1>(a, mb, splits, s);
+  if (nb == 4) launch_gemm_mb<T, 4, EPI>(a, mb, splits, s);
+  else if (nb == 2) launch_gemm_mb<T, 2, EPI>(a, mb, splits, s);
+  else launch_gemm_mb<T, 1, EPI>(a, mb, splits, s);
 }
 
-template <typename T>
+template <typename T, bool NORM = false>
 void launch_gemm_silu_mul(const GemmArgs& a, int nb, int mb, hipStream_t s) {
-  if (nb == 4) launch_gemm_mb<T, 4, kEpiSiluMul>(a, mb, 1, s);
-  else launch_gemm_mb<T, 2, kEpiSiluMul>(a, mb, 1, s);
+  if (nb == 4) launch_gemm_mb<T, 4, kEpiSiluMul, NORM>(a, mb, 1, s);
+  else launch_gemm_mb<T, 2, kEpiSiluMul, NORM>(a, mb, 1, s);
 }
 
-template <typename T>
+template <typename T, bool NORM = false>
 void launch_gemm_rope(const GemmArgs& a, int nb, int mb, hipStream_t s) {
-  if (nb == 4) launch_gemm_mb<T, 4, kEpiRope>(a, mb, 1, s);
-  else launch_gemm_mb<T, 2, kEpiRope>(a, mb, 1, s);
+  if (nb == 4) launch_gemm_mb<T, 4, kEpiRope, NORM>(a, mb, 1, s);
+  else launch_gemm_mb<T, 2, kEpiRope, NORM>(a, mb, 1, s);
 }
 
-// LDS bytes of a workgroup of the (NB, MB) instantiation (GemmRing<NB, MB>::BYTES).
-int ring_bytes(int nb, int mb) {
+// LDS bytes of a workgroup of the (NB, MB) instantiation (GemmRing<NB, MB, reserve>::BYTES +
+// reserve, the norm weight's bytes of the NORM kernels).
+int ring_bytes(int nb, int mb, int reserve = 0) {
   const int slot = 16 * (mb + nb) * kChunkBytes;
-  const int fit = kLdsBytes / slot;
+  const int fit = (kLdsBytes - reserve) / slot;
   const int ahead = fit >= RG_GEMM_AHEAD + 1 ? RG_GEMM_AHEAD : fit - 1;
   const int slots = fit >= ahead + 2 ? ahead + 2 : ahead + 1;
-  return std::max(slots * slot, nb * mb * kGemmWaves * 1024);
+  return std::max(slots * slot, nb * mb * kGemmWaves * 1024) + reserve;
 }
 
 // Workgroup shape: 16-column n-blocks (NB) and 16-row blocks (MB) per workgroup, row tiles
@@ -400,7 +519,7 @@ int ring_bytes(int nb, int mb) {
 // Each workgroup streams its rows of X and its columns of W once per K range; small row tiles
 // cut the X bytes of narrow layers, and the XCD-aware order keeps their re-reads of W in L2.
 struct GemmPlan { int nb, mb, mtiles, splits, xcd; };
-GemmPlan gemm_plan(int M, int N, int K, int cus, bool pairs = false, int only_nb = 0) {
+GemmPlan gemm_plan(int M, int N, int K, int cus, bool pairs = false, int only_nb = 0, bool norm = false) {
   const int nblk = N / 16, chunks = K / kChunkK;
   GemmPlan best{1, 1, M, 1, 0};
   double best_t = 1e30;
@@ -409,9 +528,9 @@ GemmPlan gemm_plan(int M, int N, int K, int cus, bool pairs = false, int only_nb
     const int mtiles = (M + 16 * mb - 1) / (16 * mb);
     for (int nb : {4, 2, 1}) {
       if (nblk % nb != 0 || (pairs && nb == 1) || (only_nb && nb != only_nb)) continue;
-      const int resident = std::max(1, std::min(4, kLdsBytes / ring_bytes(nb, mb)));
+      const int resident = std::max(1, std::min(4, kLdsBytes / ring_bytes(nb, mb, norm ? 2 * kNormMaxK : 0)));
       for (int splits : {1, 2, 4}) {
-        if (splits > 1 && (pairs || chunks / splits < 8)) continue;
+        if (splits > 1 && (pairs || norm || chunks / splits < 8)) continue;
         const int64_t wgs = (int64_t)mtiles * (nblk / nb) * splits;
         const double stream = 3.0 * (double)ceil_div(wgs, (int64_t)cus * resident) +
                               0.047 * (double)ceil_div(wgs, cus) * (mb + nb) * (chunks / splits);
@@ -482,17 +601,15 @@ int check_linear(const char* op, const void* x, const void* weight, const void* 
 }  // namespace
 }  // namespace rg
 
-extern "C" int rg_linear(const void* x, const void* weight, void* out, int32_t num_rows, int32_t out_features,
-                         int32_t in_features, int64_t x_row_stride, int64_t weight_row_stride,
-                         int64_t out_row_stride, void* workspace, size_t workspace_bytes, int32_t dtype,
-                         void* stream) {
-  const char* op = "linear";
-  const int32_t M = num_rows, N = out_features, K = in_features;
+namespace rg {
+namespace {
+// rg_linear (EPI kEpiPlain) and rg_linear_residual (kEpiResidual: out is the residual stream).
+template <int EPI>
+int linear_entry(const char* op, const void* x, const void* weight, void* out, int32_t M, int32_t N, int32_t K,
+                 int64_t ldx, int64_t ldw, int64_t ldo, void* workspace, size_t workspace_bytes, int32_t dtype,
+                 void* stream) {
   bool empty = false;
-  if (int st = check_linear(op, x, weight, out, M, N, K, N, x_row_stride, weight_row_stride, out_row_stride, dtype,
-                            empty)) {
-    return st;
-  }
+  if (int st = check_linear(op, x, weight, out, M, N, K, N, ldx, ldw, ldo, dtype, empty)) return st;
   if (empty) return ok();
   GemmPlan plan = gemm_plan(M, N, K, device_cu_count());
   const size_t need = plan.splits > 1 ? (size_t)plan.splits * M * N * sizeof(float) : 0;
@@ -500,48 +617,54 @@ extern "C" int rg_linear(const void* x, const void* weight, void* out, int32_t n
     plan.splits = 1;  // no (or too small a) workspace: one pass over K
   }
   GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
-             static_cast<float*>(workspace), M, N, K, x_row_stride, weight_row_stride, out_row_stride,
-             plan.mtiles, plan.xcd};
+             static_cast<float*>(workspace), M, N, K, ldx, ldw, ldo, plan.mtiles, plan.xcd};
   hipStream_t s = as_stream(stream);
-  if (dtype == RG_DTYPE_BF16) launch_gemm<bf16_t>(a, plan.nb, plan.mb, plan.splits, s);
-  else launch_gemm<f16_t>(a, plan.nb, plan.mb, plan.splits, s);
+  if (dtype == RG_DTYPE_BF16) launch_gemm<bf16_t, EPI>(a, plan.nb, plan.mb, plan.splits, s);
+  else launch_gemm<f16_t, EPI>(a, plan.nb, plan.mb, plan.splits, s);
   return check_launch(op);
 }
 
-extern "C" int rg_linear_silu_mul(const void* x, const void* weight_gate_up, void* out, int32_t num_rows,
-                                  int32_t intermediate_size, int32_t in_features, int64_t x_row_stride,
-                                  int64_t weight_row_stride, int64_t out_row_stride, int32_t dtype, void* stream) {
-  const char* op = "linear_silu_mul";
-  const int32_t M = num_rows, I = intermediate_size, K = in_features;
+// The RMSNorm weight of the NORM kernels: present, 16-byte aligned, K within the LDS copy.
+int check_norm(const char* op, const void* norm_weight, int32_t K, float eps) {
+  if (!norm_weight || !aligned16(norm_weight)) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: norm_weight must be a 16-byte aligned [in_features] vector", op);
+  }
+  if (K > kNormMaxK) return fail(RG_ERR_NOT_SUPPORTED, "%s: in_features at most %d (got %d)", op, kNormMaxK, K);
+  if (!(eps >= 0.f)) return fail(RG_ERR_INVALID_ARGUMENT, "%s: eps must be non-negative", op);
+  return RG_OK;
+}
+
+int silu_mul_entry(const char* op, const void* x, const void* norm_weight, float eps, const void* weight_gate_up,
+                   void* out, int32_t M, int32_t I, int32_t K, int64_t ldx, int64_t ldw, int64_t ldo, int32_t dtype,
+                   void* stream) {
   if (I < 0 || I % 16 != 0) {
     return fail(RG_ERR_NOT_SUPPORTED, "%s: intermediate_size must be a multiple of 16 (got %d)", op, I);
   }
   bool empty = false;
-  if (int st = check_linear(op, x, weight_gate_up, out, M, 2 * I, K, I, x_row_stride, weight_row_stride,
-                            out_row_stride, dtype, empty)) {
-    return st;
-  }
+  if (int st = check_linear(op, x, weight_gate_up, out, M, 2 * I, K, I, ldx, ldw, ldo, dtype, empty)) return st;
   if (empty) return ok();
-  const GemmPlan plan = gemm_plan(M, 2 * I, K, device_cu_count(), true);
+  const bool norm = norm_weight != nullptr;
+  const GemmPlan plan = gemm_plan(M, 2 * I, K, device_cu_count(), true, 0, norm);
   GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight_gate_up),
-             static_cast<uint16_t*>(out), nullptr, M, 2 * I, K, x_row_stride, weight_row_stride, out_row_stride,
-             plan.mtiles, plan.xcd};
+             static_cast<uint16_t*>(out), nullptr, M, 2 * I, K, ldx, ldw, ldo, plan.mtiles, plan.xcd};
+  a.norm_w = static_cast<const uint16_t*>(norm_weight);
+  a.norm_eps = eps;
   hipStream_t s = as_stream(stream);
-  if (dtype == RG_DTYPE_BF16) launch_gemm_silu_mul<bf16_t>(a, plan.nb, plan.mb, s);
-  else launch_gemm_silu_mul<f16_t>(a, plan.nb, plan.mb, s);
+  if (norm) {
+    if (dtype == RG_DTYPE_BF16) launch_gemm_silu_mul<bf16_t, true>(a, plan.nb, plan.mb, s);
+    else launch_gemm_silu_mul<f16_t, true>(a, plan.nb, plan.mb, s);
+  } else {
+    if (dtype == RG_DTYPE_BF16) launch_gemm_silu_mul<bf16_t>(a, plan.nb, plan.mb, s);
+    else launch_gemm_silu_mul<f16_t>(a, plan.nb, plan.mb, s);
+  }
   return check_launch(op);
 }
 
-extern "C" int rg_linear_qkv_rope_reshape_and_cache(const void* x, const void* weight_qkv, void* q_out,
-                                                    void* k_cache, void* v_cache, const float* cos_sin,
-                                                    const int32_t* positions, const int32_t* slot_mapping,
-                                                    int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
-                                                    int32_t head_dim, int32_t block_size, int32_t in_features,
-                                                    int64_t x_row_stride, int64_t weight_row_stride,
-                                                    int64_t q_out_token_stride, int64_t kv_block_stride,
-                                                    int32_t dtype, void* stream) {
-  const char* op = "linear_qkv_rope_reshape_and_cache";
-  const int32_t M = num_tokens, D = head_dim, K = in_features;
+int qkv_rope_entry(const char* op, const void* x, const void* norm_weight, float eps, const void* weight_qkv,
+                   void* q_out, void* k_cache, void* v_cache, const float* cos_sin, const int32_t* positions,
+                   const int32_t* slot_mapping, int32_t M, int32_t num_heads, int32_t num_kv_heads, int32_t D,
+                   int32_t block_size, int32_t K, int64_t ldx, int64_t ldw, int64_t ldq, int64_t kv_block_stride,
+                   int32_t dtype, void* stream) {
   if (num_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 || num_heads % num_kv_heads != 0) {
     return fail(RG_ERR_INVALID_ARGUMENT, "%s: need positive heads (H a multiple of H_kv) and block_size", op);
   }
@@ -550,8 +673,7 @@ extern "C" int rg_linear_qkv_rope_reshape_and_cache(const void* x, const void* w
   }
   const int32_t N = (num_heads + 2 * num_kv_heads) * D;
   bool empty = false;
-  if (int st = check_linear(op, x, weight_qkv, q_out, M, N, K, num_heads * D, x_row_stride, weight_row_stride,
-                            q_out_token_stride, dtype, empty)) {
+  if (int st = check_linear(op, x, weight_qkv, q_out, M, N, K, num_heads * D, ldx, ldw, ldq, dtype, empty)) {
     return st;
   }
   if (empty) return ok();
@@ -565,13 +687,87 @@ extern "C" int rg_linear_qkv_rope_reshape_and_cache(const void* x, const void* w
                 "16-byte aligned", op);
   }
   const int nb = D / 16;
-  const GemmPlan plan = gemm_plan(M, N, K, device_cu_count(), true, nb);
+  const bool norm = norm_weight != nullptr;
+  const GemmPlan plan = gemm_plan(M, N, K, device_cu_count(), true, nb, norm);
   GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight_qkv), static_cast<uint16_t*>(q_out),
-             nullptr, M, N, K, x_row_stride, weight_row_stride, q_out_token_stride, plan.mtiles, plan.xcd,
+             nullptr, M, N, K, ldx, ldw, ldq, plan.mtiles, plan.xcd,
              cos_sin, positions, slot_mapping, static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
-             kv_stride, num_heads, num_kv_heads, block_size};
+             kv_stride, num_heads, num_kv_heads, block_size, static_cast<const uint16_t*>(norm_weight), eps};
   hipStream_t s = as_stream(stream);
-  if (dtype == RG_DTYPE_BF16) launch_gemm_rope<bf16_t>(a, nb, plan.mb, s);
-  else launch_gemm_rope<f16_t>(a, nb, plan.mb, s);
+  if (norm) {
+    if (dtype == RG_DTYPE_BF16) launch_gemm_rope<bf16_t, true>(a, nb, plan.mb, s);
+    else launch_gemm_rope<f16_t, true>(a, nb, plan.mb, s);
+  } else {
+    if (dtype == RG_DTYPE_BF16) launch_gemm_rope<bf16_t>(a, nb, plan.mb, s);
+    else launch_gemm_rope<f16_t>(a, nb, plan.mb, s);
+  }
   return check_launch(op);
+}
+}  // namespace
+}  // namespace rg
+
+extern "C" int rg_linear(const void* x, const void* weight, void* out, int32_t num_rows, int32_t out_features,
+                         int32_t in_features, int64_t x_row_stride, int64_t weight_row_stride,
+                         int64_t out_row_stride, void* workspace, size_t workspace_bytes, int32_t dtype,
+                         void* stream) {
+  return linear_entry<kEpiPlain>("linear", x, weight, out, num_rows, out_features, in_features, x_row_stride,
+                                 weight_row_stride, out_row_stride, workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" int rg_linear_residual(const void* x, const void* weight, void* residual, int32_t num_rows,
+                                  int32_t out_features, int32_t in_features, int64_t x_row_stride,
+                                  int64_t weight_row_stride, int64_t residual_row_stride, void* workspace,
+                                  size_t workspace_bytes, int32_t dtype, void* stream) {
+  return linear_entry<kEpiResidual>("linear_residual", x, weight, residual, num_rows, out_features, in_features,
+                                    x_row_stride, weight_row_stride, residual_row_stride, workspace, workspace_bytes,
+                                    dtype, stream);
+}
+
+extern "C" int rg_linear_silu_mul(const void* x, const void* weight_gate_up, void* out, int32_t num_rows,
+                                  int32_t intermediate_size, int32_t in_features, int64_t x_row_stride,
+                                  int64_t weight_row_stride, int64_t out_row_stride, int32_t dtype, void* stream) {
+  return silu_mul_entry("linear_silu_mul", x, nullptr, 0.f, weight_gate_up, out, num_rows, intermediate_size,
+                        in_features, x_row_stride, weight_row_stride, out_row_stride, dtype, stream);
+}
+
+extern "C" int rg_rms_norm_linear_silu_mul(const void* x, const void* norm_weight, float eps,
+                                           const void* weight_gate_up, void* out, int32_t num_rows,
+                                           int32_t intermediate_size, int32_t in_features, int64_t x_row_stride,
+                                           int64_t weight_row_stride, int64_t out_row_stride, int32_t dtype,
+                                           void* stream) {
+  const char* op = "rms_norm_linear_silu_mul";
+  if (num_rows > 0 && intermediate_size > 0) {
+    if (int st = check_norm(op, norm_weight, in_features, eps)) return st;
+  }
+  return silu_mul_entry(op, x, norm_weight, eps, weight_gate_up, out, num_rows, intermediate_size, in_features,
+                        x_row_stride, weight_row_stride, out_row_stride, dtype, stream);
+}
+
+extern "C" int rg_linear_qkv_rope_reshape_and_cache(const void* x, const void* weight_qkv, void* q_out,
+                                                    void* k_cache, void* v_cache, const float* cos_sin,
+                                                    const int32_t* positions, const int32_t* slot_mapping,
+                                                    int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                                                    int32_t head_dim, int32_t block_size, int32_t in_features,
+                                                    int64_t x_row_stride, int64_t weight_row_stride,
+                                                    int64_t q_out_token_stride, int64_t kv_block_stride,
+                                                    int32_t dtype, void* stream) {
+  return qkv_rope_entry("linear_qkv_rope_reshape_and_cache", x, nullptr, 0.f, weight_qkv, q_out, k_cache, v_cache,
+                        cos_sin, positions, slot_mapping, num_tokens, num_heads, num_kv_heads, head_dim, block_size,
+                        in_features, x_row_stride, weight_row_stride, q_out_token_stride, kv_block_stride, dtype,
+                        stream);
+}
+
+extern "C" int rg_rms_norm_linear_qkv_rope_reshape_and_cache(
+    const void* x, const void* norm_weight, float eps, const void* weight_qkv, void* q_out, void* k_cache,
+    void* v_cache, const float* cos_sin, const int32_t* positions, const int32_t* slot_mapping, int32_t num_tokens,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t in_features,
+    int64_t x_row_stride, int64_t weight_row_stride, int64_t q_out_token_stride, int64_t kv_block_stride,
+    int32_t dtype, void* stream) {
+  const char* op = "rms_norm_linear_qkv_rope_reshape_and_cache";
+  if (num_tokens > 0) {
+    if (int st = check_norm(op, norm_weight, in_features, eps)) return st;
+  }
+  return qkv_rope_entry(op, x, norm_weight, eps, weight_qkv, q_out, k_cache, v_cache, cos_sin, positions,
+                        slot_mapping, num_tokens, num_heads, num_kv_heads, head_dim, block_size, in_features,
+                        x_row_stride, weight_row_stride, q_out_token_stride, kv_block_stride, dtype, stream);
 }

@@ -39,8 +39,8 @@ import torch.nn.functional as F
 
 from .batch import StepBatch
 from .kv_pool import GpuBlockPool
-from .ops import (LINEAR_MAX_ROWS, PagedAttentionKernels, interleave_gate_up, linear, linear_silu_mul,
-                  linear_workspace_bytes, rms_norm, rope_cos_sin_table, silu_and_mul)
+from .ops import (LINEAR_MAX_ROWS, PagedAttentionKernels, interleave_gate_up, linear, linear_residual,
+                  linear_silu_mul, linear_workspace_bytes, rms_norm, rope_cos_sin_table, silu_and_mul)
 
 
 def graph_us(fn, calls: int = 10, replays: int = 3) -> float:
@@ -205,6 +205,11 @@ class RailgunLlama:
         # rows -> True for rg_linear_qkv_rope_reshape_and_cache, False for the projection +
         # rg_qkv_rope_reshape_and_cache
         self.qkv_choice: dict = {}
+        # rows -> (input norm, post-attention norm): True where the RmsNorm is folded into the
+        # projection after it (rg_rms_norm_linear_qkv_rope_reshape_and_cache with the residual add
+        # in down_proj, rg_rms_norm_linear_silu_mul with the residual add in o_proj:
+        # rg_linear_residual), False for rg_rms_norm + the projections above
+        self.norm_chain: dict = {}
         # Hook for measurements: called as attention_hook("begin"/"end", layer) around each
         # layer's attention kernels (None in normal use).
         self.attention_hook = None
@@ -354,6 +359,74 @@ class RailgunLlama:
         if b.num_tokens and int(b.slot_mapping.max()) >= self.pool.num_blocks * self.pool.block_size:
             raise ValueError("slot outside the pool")
 
+    def _norm_chain_fits(self, rows: int) -> bool:
+        cfg = self.cfg
+        return (0 < rows <= LINEAR_MAX_ROWS and cfg.head_dim in (32, 64) and cfg.hidden_size % 128 == 0
+                and cfg.hidden_size <= 8192 and cfg.intermediate_size % 128 == 0
+                and self.dtype in (torch.bfloat16, torch.float16))
+
+    def _gate_up_il(self, layer: int) -> torch.Tensor:
+        w_il = self._w_gate_up_il.get(layer)
+        if w_il is None:
+            w_il = self._w_gate_up_il[layer] = interleave_gate_up(self.w.layers[layer].w_gate_up)
+        return w_il
+
+    def _use_norm_chain(self, st: DeviceStep) -> tuple:
+        """Which RmsNorms of this step's layers are folded into the projection after them, as
+        (attention side, MLP side): the input norm into q/k/v (with the residual add of the MLP
+        output moved into down_proj) and the post-attention norm into gate/up (with the residual
+        add moved into o_proj).  Each side is measured once per row count against rg_rms_norm +
+        the projections, over every layer's weights with scratch activations, before the step's
+        first layer (so that the cache rows the timing writes are rewritten by the step itself)."""
+        cfg = self.cfg
+        rows = st.host.num_tokens
+        if not self._norm_chain_fits(rows):
+            return (False, False)
+        use = self.norm_chain.get(rows)
+        if use is not None:
+            return (use, use) if isinstance(use, bool) else use
+        if torch.cuda.is_current_stream_capturing():
+            use = (True, True)
+        else:
+            H, D, eps = cfg.num_attention_heads, cfg.head_dim, cfg.rms_norm_eps
+            Hkv, bs = cfg.num_key_value_heads, self.pool.block_size
+            g = torch.Generator(device=self.device).manual_seed(0)
+            x = torch.randn((rows, cfg.hidden_size), generator=g, device=self.device).to(self.dtype)
+            delta = x.clone()
+            h = torch.empty_like(x)
+            q = torch.empty((rows, H, D), device=self.device, dtype=self.dtype)
+            attn = torch.randn((rows, H * D), generator=g, device=self.device).to(self.dtype)
+            act = torch.randn((rows, cfg.intermediate_size), generator=g, device=self.device).to(self.dtype)
+            ws_o = self._workspace(max(linear_workspace_bytes(rows, cfg.hidden_size, H * D),
+                                       linear_workspace_bytes(rows, cfg.hidden_size, cfg.intermediate_size)))
+            layers = self.w.layers
+
+            def attn_folded(j):
+                self.kernels.launch_linear_qkv_rope_reshape_and_cache(
+                    x, layers[j].wqkv, q, self.pool.k_cache(j), self.pool.v_cache(j), self.cos_sin, st.positions,
+                    st.slot_mapping, H, Hkv, D, bs, norm_weight=layers[j].input_norm, eps=eps)
+                linear_residual(act, layers[j].w_down, x, ws_o)
+
+            def attn_unfolded(j):
+                rms_norm(delta, layers[j].input_norm, h, eps, residual=x)
+                self._qkv_rope_cache(j, h, q, st)
+                delta.copy_(self._linear(act, "w_down", j))
+
+            def mlp_folded(j):
+                linear_residual(attn, layers[j].wo, x, ws_o)
+                linear_silu_mul(x, self._gate_up_il(j), act, norm_weight=layers[j].post_norm, eps=eps)
+
+            def mlp_unfolded(j):
+                rms_norm(self._linear(attn, "wo", j), layers[j].post_norm, h, eps, residual=x)
+                self._mlp_act(j, h, act)
+
+            n = len(layers)
+            t_af, t_au = self._time_pair(attn_folded, attn_unfolded, n)
+            t_mf, t_mu = self._time_pair(mlp_folded, mlp_unfolded, n)
+            use = (not t_au < 0.95 * t_af, not t_mu < 0.95 * t_mf)
+        self.norm_chain[rows] = use
+        return use
+
     @torch.no_grad()
     def forward(self, st: DeviceStep) -> torch.Tensor:
         cfg, w = self.cfg, self.w
@@ -366,22 +439,44 @@ class RailgunLlama:
         q = torch.empty((T, H, D), device=self.device, dtype=self.dtype)
         attn = torch.empty_like(q)
         act = torch.empty((T, cfg.intermediate_size), device=self.device, dtype=self.dtype)
-        delta = None
+        delta = None                                            # projection output not yet added to x
+        fold_attn, fold_mlp = self._use_norm_chain(st)
+        ws_res = self._workspace(max(linear_workspace_bytes(T, cfg.hidden_size, H * D),
+                                     linear_workspace_bytes(T, cfg.hidden_size, cfg.intermediate_size))) \
+            if (fold_attn or fold_mlp) else None
         for i, L in enumerate(w.layers):
-            # input_layernorm (with the previous MLP's residual add), architecture.rs:49-50
-            rms_norm(delta if delta is not None else x, L.input_norm, h, eps, residual=x if delta is not None else None)
-            self._qkv_rope_cache(i, h, q, st)                   # q/k/v, RoPE, cache write
+            if fold_attn:
+                # input_layernorm folded into the q/k/v projection (+ RoPE, cache write); the
+                # previous down_proj already added its output to x
+                self.kernels.launch_linear_qkv_rope_reshape_and_cache(
+                    x, L.wqkv, q, self.pool.k_cache(i), self.pool.v_cache(i), self.cos_sin, st.positions,
+                    st.slot_mapping, H, Hkv, D, self.pool.block_size, norm_weight=L.input_norm, eps=eps)
+            else:
+                # input_layernorm (with the previous MLP's residual add), architecture.rs:49-50
+                rms_norm(delta if delta is not None else x, L.input_norm, h, eps,
+                         residual=x if delta is not None else None)
+                self._qkv_rope_cache(i, h, q, st)               # q/k/v, RoPE, cache write
             if self.attention_hook:
                 self.attention_hook("begin", i)
             self._attention(i, q, attn, st)
             if self.attention_hook:
                 self.attention_hook("end", i)
-            delta = self._linear(attn.view(T, H * D), "wo", i)
-            # residual add + post_attention_layernorm, architecture.rs:53-57
-            rms_norm(delta, L.post_norm, h, eps, residual=x)
-            self._mlp_act(i, h, act)                            # LlamaMLP, architecture.rs:80-84
-            delta = self._linear(act, "w_down", i)
-        rms_norm(delta, w.norm, h, eps, residual=x)            # last residual add + model.norm
+            if fold_mlp:
+                # o_proj + residual add, then post_attention_layernorm folded into gate/up + SiLU·mul
+                linear_residual(attn.view(T, H * D), L.wo, x, ws_res)
+                linear_silu_mul(x, self._gate_up_il(i), act, norm_weight=L.post_norm, eps=eps)
+            else:
+                delta = self._linear(attn.view(T, H * D), "wo", i)
+                # residual add + post_attention_layernorm, architecture.rs:53-57
+                rms_norm(delta, L.post_norm, h, eps, residual=x)
+                self._mlp_act(i, h, act)                        # LlamaMLP, architecture.rs:80-84
+            if fold_attn:
+                linear_residual(act, L.w_down, x, ws_res)       # down_proj + residual add
+                delta = None
+            else:
+                delta = self._linear(act, "w_down", i)
+        # last residual add (unless down_proj made it) + model.norm
+        rms_norm(delta if delta is not None else x, w.norm, h, eps, residual=x if delta is not None else None)
         return self._linear(h.index_select(0, st.last_rows), "lm_head")
 
 

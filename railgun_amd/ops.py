@@ -260,9 +260,11 @@ class PagedAttentionKernels:
 
     def launch_linear_qkv_rope_reshape_and_cache(self, x, weight_qkv, q_out, k_cache, v_cache, cos_sin, positions,
                                                  slot_mapping, num_heads: int, num_kv_heads: int, head_dim: int,
-                                                 block_size: int) -> None:
+                                                 block_size: int, norm_weight=None, eps: float = 0.0) -> None:
         """The fused q/k/v projection x @ weight_qkv^T and launch_qkv_rope_reshape_and_cache in one
-        pass (decode batches: x [T <= 128, K], head_dim 32 or 64); rotated q to q_out [T, H, D]."""
+        pass (decode batches: x [T <= 128, K], head_dim 32 or 64); rotated q to q_out [T, H, D].
+        With norm_weight, x is the residual stream and the RmsNorm in front of the attention is
+        folded in (rg_rms_norm_linear_qkv_rope_reshape_and_cache)."""
         _require_cuda(x, weight_qkv, q_out, k_cache, v_cache, cos_sin, positions, slot_mapping)
         _require_i32(positions, slot_mapping)
         if x.dim() != 2 or x.stride(1) != 1 or not weight_qkv.is_contiguous() or not q_out.is_contiguous() or \
@@ -270,6 +272,17 @@ class PagedAttentionKernels:
             raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "x must be [T, K] with unit column stride, weight_qkv "
                                                              "and q_out contiguous, one dtype")
         tokens, k = (int(d) for d in x.shape)
+        if norm_weight is not None:
+            _require_cuda(norm_weight)
+            if tuple(norm_weight.shape) != (k,) or not norm_weight.is_contiguous() or norm_weight.dtype != x.dtype:
+                raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "norm_weight must be a contiguous [K] vector of "
+                                                                 "x's dtype")
+            check(self.lib.rg_rms_norm_linear_qkv_rope_reshape_and_cache(
+                x.data_ptr(), norm_weight.data_ptr(), float(eps), weight_qkv.data_ptr(), q_out.data_ptr(),
+                k_cache.data_ptr(), v_cache.data_ptr(), cos_sin.data_ptr(), positions.data_ptr(),
+                slot_mapping.data_ptr(), tokens, num_heads, num_kv_heads, head_dim, block_size, k, x.stride(0),
+                weight_qkv.stride(0), num_heads * head_dim, k_cache.stride(0), dtype_code(x), _stream(x)))
+            return
         check(self.lib.rg_linear_qkv_rope_reshape_and_cache(
             x.data_ptr(), weight_qkv.data_ptr(), q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
             cos_sin.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(), tokens, num_heads, num_kv_heads,
@@ -487,9 +500,12 @@ def interleave_gate_up(w_gate_up: torch.Tensor) -> torch.Tensor:
     return w_gate_up.view(2, two_i // 32, 16, k).transpose(0, 1).contiguous().view(two_i, k)
 
 
-def linear_silu_mul(x: torch.Tensor, weight_il: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+def linear_silu_mul(x: torch.Tensor, weight_il: torch.Tensor, out: Optional[torch.Tensor] = None,
+                    norm_weight: Optional[torch.Tensor] = None, eps: float = 0.0) -> torch.Tensor:
     """out [rows, I] = silu(x @ gate^T) * (x @ up^T), each step rounded as rg_linear followed by
-    rg_silu_and_mul round it; weight_il from interleave_gate_up."""
+    rg_silu_and_mul round it; weight_il from interleave_gate_up.  With norm_weight, x is the
+    residual stream and the RmsNorm in front of the MLP is folded in
+    (rg_rms_norm_linear_silu_mul)."""
     _require_cuda(x, weight_il, out)
     if x.dim() != 2 or weight_il.dim() != 2 or x.stride(1) != 1 or not weight_il.is_contiguous() or \
             x.dtype != weight_il.dtype:
@@ -504,11 +520,46 @@ def linear_silu_mul(x: torch.Tensor, weight_il: torch.Tensor, out: Optional[torc
         out = torch.empty((rows, inter), dtype=x.dtype, device=x.device)
     elif tuple(out.shape) != (rows, inter) or out.stride(1) != 1 or out.dtype != x.dtype:
         raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "linear_silu_mul: out must be [rows, I] with unit column stride")
+    if norm_weight is not None:
+        _require_cuda(norm_weight)
+        if tuple(norm_weight.shape) != (k,) or not norm_weight.is_contiguous() or norm_weight.dtype != x.dtype:
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "linear_silu_mul: norm_weight must be a contiguous [K] "
+                                                             "vector of x's dtype")
+        check(load_library().rg_rms_norm_linear_silu_mul(
+            x.data_ptr(), norm_weight.data_ptr(), float(eps), weight_il.data_ptr(), out.data_ptr(), rows, inter, k,
+            x.stride(0), weight_il.stride(0), out.stride(0), dtype_code(x), _stream(x)))
+        return out
     check(load_library().rg_linear_silu_mul(x.data_ptr(), weight_il.data_ptr(), out.data_ptr(), rows, inter, k,
                                             x.stride(0), weight_il.stride(0), out.stride(0), dtype_code(x), _stream(x)))
     return out
 
 
+def linear_residual(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
+                    workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """residual += x @ weight^T in place, rounded as rg_linear followed by the residual add of
+    rg_rms_norm (rg_linear_residual); the split-K workspace as for linear."""
+    _require_cuda(x, weight, residual)
+    if x.dim() != 2 or weight.dim() != 2 or x.stride(1) != 1 or not weight.is_contiguous() or x.dtype != weight.dtype:
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "linear_residual: x [rows, K] with unit column stride and a "
+                                                         "contiguous weight [N, K] of the same dtype")
+    rows, k = (int(d) for d in x.shape)
+    n = int(weight.shape[0])
+    if int(weight.shape[1]) != k or tuple(residual.shape) != (rows, n) or residual.stride(1) != 1 or \
+            residual.dtype != x.dtype:
+        raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "linear_residual: weight [N, K] and residual [rows, N] with "
+                                                         "unit column stride")
+    if workspace is None:
+        ws_bytes = linear_workspace_bytes(rows, n, k)
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    ws_ptr, ws_len = (workspace.data_ptr(), workspace.numel() * workspace.element_size()) if workspace is not None \
+        else (None, 0)
+    check(load_library().rg_linear_residual(x.data_ptr(), weight.data_ptr(), residual.data_ptr(), rows, n, k,
+                                            x.stride(0), weight.stride(0), residual.stride(0), ws_ptr, ws_len,
+                                            dtype_code(x), _stream(x)))
+    return residual
+
+
 __all__ = ["LINEAR_MAX_ROWS", "PagedAttentionKernels", "PagedAttentionOp", "RailgunError", "cache_geometry",
-           "dtype_code", "interleave_gate_up", "linear", "linear_silu_mul", "linear_workspace_bytes", "rms_norm", "rope_cos_sin_table", "silu_and_mul", "V1_MAX_CONTEXT",
+           "dtype_code", "interleave_gate_up", "linear", "linear_residual", "linear_silu_mul", "linear_workspace_bytes",
+           "rms_norm", "rope_cos_sin_table", "silu_and_mul", "V1_MAX_CONTEXT",
            "V2_PARTITION_SIZE"]

@@ -207,3 +207,120 @@ def test_linear_qkv_rope_refuses_unsupported(device, kernels):
     with pytest.raises(RailgunError) as e:
         kernels.launch_linear_qkv_rope_reshape_and_cache(x, w, q, pool[:, 0], pool[:, 1], cs, i, i, 2, 1, 128, 16)
     assert e.value.code == _lib.RG_ERR_NOT_SUPPORTED
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 2048, 2048), (128, 2048, 8192), (37, 512, 256), (1, 2048, 8192)])
+def test_linear_residual(device, M, N, K):
+    """residual += x @ W^T equals rg_linear's rounded output added to the residual and rounded
+    (the residual add of rg_rms_norm) bit for bit, with and without a split of K."""
+    from railgun_amd.ops import linear_residual, linear_workspace_bytes
+    g = torch.Generator().manual_seed(M + N + 3 * K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(device)
+    w = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).to(device)
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(device)
+    ws = torch.empty(max(16, linear_workspace_bytes(M, N, K)), dtype=torch.uint8, device=device)
+    got = linear_residual(x, w, res.clone(), workspace=ws)
+    delta = linear(x, w, workspace=ws)
+    torch.cuda.synchronize()
+    want = (res.float() + delta.float()).to(torch.bfloat16)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def _norm_ref(x, nw, eps):
+    """fp32 RmsNorm of x (without rounding) and the row scales."""
+    xf = x.float().cpu()
+    rs = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return xf * rs * nw.float().cpu(), rs
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("M,I,K", [(128, 8192, 2048), (1, 8192, 2048), (37, 512, 256), (100, 1040, 1024)])
+def test_rms_norm_linear_silu_mul(device, M, I, K, dt):
+    """The MLP input RmsNorm folded into the gate/up projection with SiLU·mul, against the fp32
+    chain.  The kernel feeds round(x w_norm) to the MFMA and scales the sums by 1 / rms(x); the
+    bound carries one rounding of every operand product (|x w_norm| |W| summed, times the row
+    scale) and of g and u, then SiLU·mul to first order, and the two output roundings."""
+    from railgun_amd.ops import interleave_gate_up, linear_silu_mul
+    t = TORCH[dt]
+    g = torch.Generator().manual_seed(M + I + K + 1)
+    x = (3 * torch.randn(M, K, generator=g)).to(t).to(device)
+    nw = (1 + 0.2 * torch.randn(K, generator=g)).to(t).to(device)
+    w = (0.05 * torch.randn(2 * I, K, generator=g)).to(t).to(device)
+    eps = 1e-5
+    got = linear_silu_mul(x, interleave_gate_up(w), norm_weight=nw, eps=eps)
+    again = linear_silu_mul(x, interleave_gate_up(w), norm_weight=nw, eps=eps)
+    torch.cuda.synchronize()
+    h, rs = _norm_ref(x, nw, eps)
+    wf = w.float().cpu()
+    gv, uv = h @ wf[:I].T, h @ wf[I:].T
+    absx = (x.float().cpu() * nw.float().cpu()).abs()
+    e = 2 ** -8 if dt == "bf16" else 2 ** -11
+    dg = e * rs * (absx @ wf[:I].abs().T) + e * gv.abs()
+    du = e * rs * (absx @ wf[I:].abs().T) + e * uv.abs()
+    sig = torch.sigmoid(gv)
+    act = gv * sig
+    ref = act * uv
+    dsilu = (sig * (1 + gv * (1 - sig))).abs()
+    bound = 2 * (dsilu * dg * uv.abs() + act.abs() * du + 2 * e * ref.abs()) + 1e-3 * ref.abs().mean() + 1e-6
+    err = (got.float().cpu() - ref).abs()
+    assert bool((err <= bound).all()), f"max excess {float((err - bound).max()):.3g}"
+    assert torch.equal(again.view(torch.int16), got.view(torch.int16)), "not deterministic"
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("T,H,Hkv,D,K,bs", [(128, 32, 8, 64, 2048, 16), (1, 32, 8, 64, 2048, 16),
+                                            (37, 8, 2, 32, 256, 32)])
+def test_rms_norm_linear_qkv_rope_reshape_and_cache(device, kernels, T, H, Hkv, D, K, bs, dt):
+    """The attention input RmsNorm folded into the q/k/v projection with RoPE and the cache
+    write, against the fp32 chain (bound as in the MLP test: one rounding of every operand
+    product and of q/k/v, carried through the rotation by |cos| + |sin|, plus the output
+    rounding).  Slots outside the mapping stay untouched."""
+    from railgun_amd.ops import rope_cos_sin_table
+    tt = TORCH[dt]
+    g = torch.Generator().manual_seed(T * 13 + D + K)
+    x = (3 * torch.randn(T, K, generator=g)).to(tt).to(device)
+    nw = (1 + 0.2 * torch.randn(K, generator=g)).to(tt).to(device)
+    w = (0.05 * torch.randn((H + 2 * Hkv) * D, K, generator=g)).to(tt).to(device)
+    nb = max(8, 2 * T // bs + 2)
+    pos = torch.randint(0, 500, (T,), generator=g, dtype=torch.int32).to(device)
+    slots = torch.randperm(nb * bs, generator=g)[:T].to(torch.int32)
+    if T > 3:
+        slots[3] = -1
+    slots = slots.to(device)
+    cs = rope_cos_sin_table(512, D, 500000.0, device)
+    pool = torch.randn(nb, 2, Hkv, bs, D, generator=g).to(tt).to(device)
+    before = pool.clone()
+    q = torch.empty(T, H, D, dtype=tt, device=device)
+    eps = 1e-5
+    kernels.launch_linear_qkv_rope_reshape_and_cache(x, w, q, pool[:, 0], pool[:, 1], cs, pos, slots, H, Hkv, D, bs,
+                                                     norm_weight=nw, eps=eps)
+    torch.cuda.synchronize()
+    h, rs = _norm_ref(x, nw, eps)
+    wf = w.float().cpu()
+    pre = (h @ wf.T).view(T, H + 2 * Hkv, D)
+    absx = (x.float().cpu() * nw.float().cpu()).abs()
+    e = 2 ** -8 if dt == "bf16" else 2 ** -11
+    dpre = (e * rs * (absx @ wf.abs().T)).view(T, H + 2 * Hkv, D) + e * pre.abs()
+    half = D // 2
+    csc = cs.cpu()[pos.cpu().long()]
+    c, s = csc[:, :half][:, None, :], csc[:, half:][:, None, :]
+    lo, hi = pre[..., :half], pre[..., half:]
+    rot = torch.cat([lo * c - hi * s, hi * c + lo * s], -1)
+    dl, dh = dpre[..., :half], dpre[..., half:]
+    drot = torch.cat([dl * c.abs() + dh * s.abs(), dh * c.abs() + dl * s.abs()], -1)
+    bound = 2 * (drot + e * rot.abs()) + 1e-5
+    got_q = q.float().cpu()
+    assert bool(((got_q - rot[:, :H]).abs() <= bound[:, :H]).all()), \
+        f"q: max excess {float(((got_q - rot[:, :H]).abs() - bound[:, :H]).max()):.3g}"
+    sl = slots.cpu().long()
+    flat = pool.float().cpu().permute(0, 3, 1, 2, 4).reshape(nb * bs, 2, Hkv, D)
+    flat0 = before.float().cpu().permute(0, 3, 1, 2, 4).reshape(nb * bs, 2, Hkv, D)
+    written = torch.zeros(nb * bs, dtype=torch.bool)
+    written[sl[sl >= 0]] = True
+    assert torch.equal(flat[~written], flat0[~written]), "wrote a slot outside the mapping"
+    tok = torch.nonzero(sl >= 0).squeeze(1)
+    kref, kb = rot[tok, H:H + Hkv], bound[tok, H:H + Hkv]
+    vref = pre[tok, H + Hkv:]
+    vb = 2 * (dpre[tok, H + Hkv:] + e * vref.abs()) + 1e-5
+    assert bool(((flat[sl[tok], 0] - kref).abs() <= kb).all()), "k cache"
+    assert bool(((flat[sl[tok], 1] - vref).abs() <= vb).all()), "v cache"

@@ -148,24 +148,46 @@ class _AlwaysRgLinear(dict):
         return True
 
 
-@pytest.mark.parametrize("gemm", ["measured", "rg_linear"])
+class _Never(dict):
+    """A choice table that declines every eligible shape (the RmsNorm-folded chain)."""
+
+    def get(self, key, default=None):
+        return False
+
+
+class _Fixed(dict):
+    """A choice table that answers every eligible shape with the same value."""
+
+    def __init__(self, value):
+        super().__init__()
+        self.value = value
+
+    def get(self, key, default=None):
+        return self.value
+
+
+@pytest.mark.parametrize("gemm", ["measured", "rg_linear", "norm_chain", "fold_attn_only", "fold_mlp_only"])
 @pytest.mark.parametrize("name", list(CONFIGS))
 def test_llama_prefill_decode_mixed(device, kernels, name, gemm):
     """Prefill, mixed and decode steps against the CPU model.  With gemm="rg_linear" every
     projection of the mixed (113 rows) and decode (4 rows) steps runs on rg_linear, the MLP's
     gate/up with SiLU·mul fused (rg_linear_silu_mul) and q/k/v with RoPE and the cache write
-    fused (rg_linear_qkv_rope_reshape_and_cache); "measured" keeps the per-shape timing choice
-    of normal use."""
+    fused (rg_linear_qkv_rope_reshape_and_cache); "norm_chain" also folds the RmsNorms into those
+    projections and the residual adds into o_proj / down_proj (rg_rms_norm_linear_*,
+    rg_linear_residual), "fold_attn_only" / "fold_mlp_only" one side of it; "measured" keeps the
+    per-shape timing choice of normal use."""
     cfg = CONFIGS[name]
     bs, nb = 16, 96
     sd = _hf_state(cfg, 11)
     w = LlamaWeights.from_state_dict(cfg, sd, device)
     pool = GpuBlockPool.for_model(cfg, nb, bs, device)
     model = RailgunLlama(cfg, w, pool, kernels, max_position=4096)
-    if gemm == "rg_linear":
+    if gemm != "measured":
         model.linear_choice = _AlwaysRgLinear()
         model.mlp_choice = _AlwaysRgLinear()
         model.qkv_choice = _AlwaysRgLinear()
+        model.norm_chain = _Fixed({"rg_linear": (False, False), "norm_chain": (True, True),
+                                   "fold_attn_only": (True, False), "fold_mlp_only": (False, True)}[gemm])
     ref32 = llama_ref.ReferenceLlama(cfg, sd, nb, bs)
     ref16 = llama_ref.ReferenceLlama(cfg, sd, nb, bs, act_dtype=torch.bfloat16)
     rng = np.random.default_rng(7)
