@@ -368,33 +368,75 @@ def side_model(device, steps: int) -> dict:
 
 def side_gemm(device) -> dict:
     """The Llama-3.2-1B decode projections (qkv, o_proj, gate/up, down, LM head) at 1 row and at
-    config 5's 128 rows: rg_linear against hipBLASLt (torch F.linear), each the mean of 30 calls
-    over HIP-graph replays.  Weights bf16 ~ N(0, 0.02), activations N(0, 1)."""
+    config 5's 128 rows: rg_linear against hipBLASLt (torch F.linear), and at 128 rows the fused
+    forms the model step runs (gate/up + SiLU·mul, q/k/v + RoPE + cache write, each with and
+    without the folded RmsNorm; o_proj / down + residual add).  Each figure is the mean per call
+    over HIP-graph replays of one call per copy of the weight, the copies totalling >= 600 MB, so
+    that every call streams its weight from HBM as a decode step does (one weight timed in a loop
+    would sit in the 256 MB last-level cache).  Weights bf16 ~ N(0, 0.02), activations N(0, 1)."""
     import torch
     import torch.nn.functional as F
 
     from railgun_amd.llama import graph_us
-    from railgun_amd.ops import linear, linear_workspace_bytes
+    from railgun_amd.ops import (PagedAttentionKernels, interleave_gate_up, linear, linear_residual,
+                                 linear_silu_mul, linear_workspace_bytes, rope_cos_sin_table)
 
     shapes = {"qkv": (3072, 2048), "o_proj": (2048, 2048), "gate_up": (16384, 2048), "down": (2048, 8192),
               "lm_head": (128256, 2048)}
     g = torch.Generator(device=device)
     g.manual_seed(5)
+    bf = torch.bfloat16
+
+    def per_call(run, n):
+        return graph_us(lambda: [run(j) for j in range(n)], calls=1, replays=5) / n
+
+    def tb(n, k, us):
+        return round(n * k * 2 / (us * 1e-6) / 1e12, 3)
+
     out = {}
+    kern = PagedAttentionKernels(device)
     for rows in (1, 128):
         per = {}
         for name, (n, k) in shapes.items():
-            x = torch.randn((rows, k), device=device, generator=g).to(torch.bfloat16)
-            w = (0.02 * torch.randn((n, k), device=device, generator=g)).to(torch.bfloat16)
-            o = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
-            ws = torch.empty(max(16, linear_workspace_bytes(rows, n, k)), dtype=torch.uint8, device=device)
-            t_rg = graph_us(lambda: linear(x, w, o, ws))
-            t_blas = graph_us(lambda: F.linear(x, w))
-            per[name] = {"rg_linear_us": round(t_rg, 2), "hipblaslt_us": round(t_blas, 2),
-                         "rg_linear_weight_TB/s": round(n * k * 2 / (t_rg * 1e-6) / 1e12, 3)}
-            del x, w, o, ws
+            copies = max(2, -(-600_000_000 // (n * k * 2)))
+            x = torch.randn((rows, k), device=device, generator=g).to(bf)
+            ws_ = [(0.02 * torch.randn((n, k), device=device, generator=g)).to(bf) for _ in range(copies)]
+            o = torch.empty((rows, n), device=device, dtype=bf)
+            wsp = torch.empty(max(16, linear_workspace_bytes(rows, n, k)), dtype=torch.uint8, device=device)
+            t_rg = per_call(lambda j: linear(x, ws_[j], o, wsp), copies)
+            t_blas = per_call(lambda j: F.linear(x, ws_[j]), copies)
+            entry = {"rg_linear_us": round(t_rg, 2), "hipblaslt_us": round(t_blas, 2),
+                     "rg_linear_weight_TB/s": tb(n, k, t_rg), "weight_copies": copies}
+            if rows == 128 and name in ("o_proj", "down"):
+                res = torch.randn((rows, n), device=device, generator=g).to(bf)
+                t = per_call(lambda j: linear_residual(x, ws_[j], res, wsp), copies)
+                entry["rg_linear_residual_us"] = round(t, 2)
+            if rows == 128 and name == "gate_up":
+                il = [interleave_gate_up(w) for w in ws_]
+                nw = (1 + 0.1 * torch.randn((k,), device=device, generator=g)).to(bf)
+                act = torch.empty((rows, n // 2), device=device, dtype=bf)
+                entry["rg_linear_silu_mul_us"] = round(per_call(lambda j: linear_silu_mul(x, il[j], act), copies), 2)
+                entry["rg_rms_norm_linear_silu_mul_us"] = round(
+                    per_call(lambda j: linear_silu_mul(x, il[j], act, norm_weight=nw, eps=1e-5), copies), 2)
+                del il
+            if rows == 128 and name == "qkv":
+                H, Hkv, D, bs = 32, 8, 64, 16
+                q = torch.empty((rows, H, D), device=device, dtype=bf)
+                pool = torch.zeros((64, 2, Hkv, bs, D), device=device, dtype=bf)
+                cs = rope_cos_sin_table(4096, D, 500000.0, device)
+                pos = torch.arange(rows, device=device, dtype=torch.int32)
+                nw = (1 + 0.1 * torch.randn((k,), device=device, generator=g)).to(bf)
+
+                def qkv(j, norm):
+                    kern.launch_linear_qkv_rope_reshape_and_cache(x, ws_[j], q, pool[:, 0], pool[:, 1], cs, pos, pos,
+                                                                  H, Hkv, D, bs, norm_weight=norm, eps=1e-5)
+                entry["rg_linear_qkv_rope_reshape_and_cache_us"] = round(per_call(lambda j: qkv(j, None), copies), 2)
+                entry["rg_rms_norm_linear_qkv_rope_reshape_and_cache_us"] = round(
+                    per_call(lambda j: qkv(j, nw), copies), 2)
+            per[name] = entry
+            del x, ws_, o, wsp
+            torch.cuda.empty_cache()
         out[f"rows_{rows}"] = per
-    torch.cuda.empty_cache()
     return out
 
 
