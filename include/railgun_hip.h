@@ -251,8 +251,9 @@ int rg_linear_qkv_rope_reshape_and_cache(const void* x, const void* weight_qkv, 
  * residual add of the next RmsNorm, architecture.rs:50-57):
  *   residual[m, n] = round(residual[m, n] + round(x[m] . weight[n])),
  * the arithmetic of rg_linear followed by the residual add of rg_rms_norm.  residual is
- * [num_rows, out_features] (residual_row_stride elements between rows); the constraints and the
- * optional split-K workspace of rg_linear (rg_linear_workspace_bytes).  New entry. */
+ * [num_rows, out_features] (residual_row_stride elements between rows) and must not overlap x or
+ * weight; the constraints and the optional split-K workspace of rg_linear
+ * (rg_linear_workspace_bytes).  New entry. */
 int rg_linear_residual(const void* x, const void* weight, void* residual, int32_t num_rows,
                        int32_t out_features, int32_t in_features, int64_t x_row_stride,
                        int64_t weight_row_stride, int64_t residual_row_stride, void* workspace,

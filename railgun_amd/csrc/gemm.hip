@@ -205,6 +205,8 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int KS = kGemmWaves;
   constexpr int D = RG::AHEAD;
   static_assert(RG::BYTES + NORM_BYTES <= kLdsBytes, "norm weight does not fit");
+  // Wave 0 has up to 2 kNormMaxK / 1024 norm-weight copies in flight with its first chunks.
+  static_assert(!NORM || D * RG::PER + 2 * kNormMaxK / 1024 < 64, "vmcnt range");
   __shared__ __attribute__((aligned(16))) char lds[RG::BYTES + NORM_BYTES];
   const uint32_t lds_base = (uint32_t)(uintptr_t)((RG_LDS char*)lds);
 
