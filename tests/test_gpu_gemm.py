@@ -234,7 +234,8 @@ def _norm_ref(x, nw, eps):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-@pytest.mark.parametrize("M,I,K", [(128, 8192, 2048), (1, 8192, 2048), (37, 512, 256), (100, 1040, 1024)])
+@pytest.mark.parametrize("M,I,K", [(128, 8192, 2048), (1, 8192, 2048), (37, 512, 256), (100, 1040, 1024),
+                                   (5, 1024, 8192), (64, 2048, 4096)])
 def test_rms_norm_linear_silu_mul(device, M, I, K, dt):
     """The MLP input RmsNorm folded into the gate/up projection with SiLU·mul, against the fp32
     chain.  The kernel feeds round(x w_norm) to the MFMA and scales the sums by 1 / rms(x); the
@@ -269,7 +270,7 @@ def test_rms_norm_linear_silu_mul(device, M, I, K, dt):
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("T,H,Hkv,D,K,bs", [(128, 32, 8, 64, 2048, 16), (1, 32, 8, 64, 2048, 16),
-                                            (37, 8, 2, 32, 256, 32)])
+                                            (37, 8, 2, 32, 256, 32), (9, 16, 4, 64, 8192, 16)])
 def test_rms_norm_linear_qkv_rope_reshape_and_cache(device, kernels, T, H, Hkv, D, K, bs, dt):
     """The attention input RmsNorm folded into the q/k/v projection with RoPE and the cache
     write, against the fp32 chain (bound as in the MLP test: one rounding of every operand
@@ -324,3 +325,21 @@ def test_rms_norm_linear_qkv_rope_reshape_and_cache(device, kernels, T, H, Hkv, 
     vb = 2 * (dpre[tok, H + Hkv:] + e * vref.abs()) + 1e-5
     assert bool(((flat[sl[tok], 0] - kref).abs() <= kb).all()), "k cache"
     assert bool(((flat[sl[tok], 1] - vref).abs() <= vb).all()), "v cache"
+
+
+def test_rms_norm_linear_refuses_unsupported(device, kernels):
+    """in_features past the LDS copy of the norm weight, a misaligned norm weight and a
+    negative eps are refused."""
+    from railgun_amd.ops import linear_silu_mul
+    x = torch.zeros(4, 8192 + 128, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(64, 8192 + 128, dtype=torch.bfloat16, device=device)
+    with pytest.raises(RailgunError) as e:
+        linear_silu_mul(x, w, norm_weight=torch.ones(8192 + 128, dtype=torch.bfloat16, device=device), eps=1e-5)
+    assert e.value.code == _lib.RG_ERR_NOT_SUPPORTED
+    x = torch.zeros(4, 256, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(64, 256, dtype=torch.bfloat16, device=device)
+    nw = torch.ones(257, dtype=torch.bfloat16, device=device)[1:]       # 2 bytes past 16-byte alignment
+    with pytest.raises(RailgunError):
+        linear_silu_mul(x, w, norm_weight=nw, eps=1e-5)
+    with pytest.raises(RailgunError):
+        linear_silu_mul(x, w, norm_weight=torch.ones(256, dtype=torch.bfloat16, device=device), eps=-1.0)
