@@ -176,11 +176,23 @@ def test_llama_prefill_decode_mixed(device, kernels, name, gemm):
     projections and the residual adds into o_proj / down_proj (rg_rms_norm_linear_*,
     rg_linear_residual), "fold_attn_only" / "fold_mlp_only" one side of it; "measured" keeps the
     per-shape timing choice of normal use."""
-    cfg = CONFIGS[name]
+    _mixed_steps(device, kernels, CONFIGS[name], gemm, torch.bfloat16)
+
+
+@pytest.mark.parametrize("gemm", ["measured", "norm_chain"])
+def test_llama_f16_steps(device, kernels, gemm):
+    """The same prefill, mixed and decode steps with fp16 weights, activations and KV pool (the
+    oracle's weights rounded to fp16, its drift reference rounding to fp16)."""
+    _mixed_steps(device, kernels, CONFIGS["mfma_d64"], gemm, torch.float16)
+
+
+def _mixed_steps(device, kernels, cfg, gemm, dtype):
     bs, nb = 16, 96
     sd = _hf_state(cfg, 11)
-    w = LlamaWeights.from_state_dict(cfg, sd, device)
-    pool = GpuBlockPool.for_model(cfg, nb, bs, device)
+    if dtype != torch.bfloat16:
+        sd = {k: v.to(dtype).float() for k, v in sd.items()}
+    w = LlamaWeights.from_state_dict(cfg, sd, device, dtype=dtype)
+    pool = GpuBlockPool.for_model(cfg, nb, bs, device, dtype=dtype)
     model = RailgunLlama(cfg, w, pool, kernels, max_position=4096)
     if gemm != "measured":
         model.linear_choice = _AlwaysRgLinear()
@@ -189,7 +201,7 @@ def test_llama_prefill_decode_mixed(device, kernels, name, gemm):
         model.norm_chain = _Fixed({"rg_linear": (False, False), "norm_chain": (True, True),
                                    "fold_attn_only": (True, False), "fold_mlp_only": (False, True)}[gemm])
     ref32 = llama_ref.ReferenceLlama(cfg, sd, nb, bs)
-    ref16 = llama_ref.ReferenceLlama(cfg, sd, nb, bs, act_dtype=torch.bfloat16)
+    ref16 = llama_ref.ReferenceLlama(cfg, sd, nb, bs, act_dtype=dtype)
     rng = np.random.default_rng(7)
     lens = [40, 77, 130, 300]
     prompts = [rng.integers(0, cfg.vocab_size, n).tolist() for n in lens]
