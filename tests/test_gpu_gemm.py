@@ -209,21 +209,28 @@ def test_linear_qkv_rope_refuses_unsupported(device, kernels):
     assert e.value.code == _lib.RG_ERR_NOT_SUPPORTED
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("M,N,K", [(128, 2048, 2048), (128, 2048, 8192), (37, 512, 256), (1, 2048, 8192)])
-def test_linear_residual(device, M, N, K):
+def test_linear_residual(device, M, N, K, dt):
     """residual += x @ W^T equals rg_linear's rounded output added to the residual and rounded
-    (the residual add of rg_rms_norm) bit for bit, with and without a split of K."""
+    (the residual add of rg_rms_norm) bit for bit, with and without a split of K; the residual
+    a column slice of a wider buffer whose other columns stay untouched."""
     from railgun_amd.ops import linear_residual, linear_workspace_bytes
+    t = TORCH[dt]
     g = torch.Generator().manual_seed(M + N + 3 * K)
-    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(device)
-    w = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).to(device)
-    res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(device)
+    x = torch.randn(M, K, generator=g).to(t).to(device)
+    w = (0.02 * torch.randn(N, K, generator=g)).to(t).to(device)
+    buf = torch.randn(M, N + 24, generator=g).to(t).to(device)
+    res = buf[:, 8:8 + N]                               # row stride N + 24
+    before = buf.clone()
     ws = torch.empty(max(16, linear_workspace_bytes(M, N, K)), dtype=torch.uint8, device=device)
-    got = linear_residual(x, w, res.clone(), workspace=ws)
+    linear_residual(x, w, res, workspace=ws)
     delta = linear(x, w, workspace=ws)
     torch.cuda.synchronize()
-    want = (res.float() + delta.float()).to(torch.bfloat16)
-    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    want = (before[:, 8:8 + N].float() + delta.float()).to(t)
+    assert torch.equal(res.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(buf[:, :8].view(torch.int16), before[:, :8].view(torch.int16))
+    assert torch.equal(buf[:, 8 + N:].view(torch.int16), before[:, 8 + N:].view(torch.int16))
 
 
 def _norm_ref(x, nw, eps):
