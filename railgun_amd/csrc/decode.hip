@@ -1127,71 +1127,92 @@ struct MergeArgs {
   int32_t skip_single;  // 1: sequences with one partition were written by the partition kernel
 };
 
-// One wave per (seq, q-head).  The partition weights e^(m_p - M) are computed once per
-// partition into LDS, then every lane accumulates its dims over the partitions.
+// One workgroup of 256 threads per (seq, q-head).  The partition weights e^(m_p - M) go to LDS
+// once per partition; thread t accumulates the float4 column chunk c = t % C of the rows
+// p = g, g + R, ... of tmp_out (C = D / 4 chunks per row, g = t / C, R = 256 / C row groups),
+// so R rows are read at a time, and the R partial sums are added in group order through LDS
+// (a fixed order: the result does not depend on timing).
+constexpr int kMergeThreads = 256;
 template <typename T>
-__global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(MergeArgs a) {
   using E = elem<T>;
   using S = typename E::storage;
-  constexpr int kChunk = 64;
+  constexpr int kChunk = kMergeThreads;  // partitions whose weights sit in LDS at a time
+  constexpr int kWaves = kMergeThreads / 64;
   __shared__ float w_lds[kChunk];
+  __shared__ float red[2 * kWaves];
+  __shared__ float4 part[kMergeThreads];
   const int h = blockIdx.x;
   const int s = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
+  const int wv = tid >> 6;
   const int D = a.head_dim;
   const int ctx = max(0, a.context_lens[s]);
   const int np_s = min(num_parts_for(ctx, a.partition_size), a.num_partitions);
   if (a.skip_single && np_s <= 1) return;
   S* op = static_cast<S*>(a.out) + ((int64_t)s * a.num_heads + h) * D;
   if (np_s == 0) {
-    for (int d = lane; d < D; d += 64) E::store(op, d, 0.f);
+    for (int d = tid; d < D; d += kMergeThreads) E::store(op, d, 0.f);
     return;
   }
   const int64_t sh = ((int64_t)s * a.num_heads + h) * a.num_partitions;
   const float* ml = a.max_logits + sh;
   const float* es = a.exp_sums + sh;
   float M = -INFINITY;
-  for (int q = lane; q < np_s; q += 64) M = fmaxf(M, ml[q]);
+  for (int q = tid; q < np_s; q += kMergeThreads) M = fmaxf(M, ml[q]);
   M = wave_max(M);
+  if ((tid & 63) == 0) red[wv] = M;
+  __syncthreads();
+  M = red[0];
+#pragma unroll
+  for (int j = 1; j < kWaves; ++j) M = fmaxf(M, red[j]);
   float L = 0.f;
-  for (int q = lane; q < np_s; q += 64) L += expf(ml[q] - M) * es[q];
+  for (int q = tid; q < np_s; q += kMergeThreads) L += expf(ml[q] - M) * es[q];
   L = wave_sum(L);
+  if ((tid & 63) == 0) red[kWaves + wv] = L;
+  __syncthreads();
+  L = red[kWaves];
+#pragma unroll
+  for (int j = 1; j < kWaves; ++j) L += red[kWaves + j];
   const float inv = L != 0.f ? 1.f / L : 1.f;
   const float* tp = a.tmp_out + sh * D;
-  // Lane owns dims lane*4 + 256*i (head_dim <= 1024, checked on the host).
-  float4 acc[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int C = D / 4;                    // head_dim % 4 == 0 and <= 1024 (checked on the host)
+  const int R = kMergeThreads / C;
+  const int c = tid % C, g = tid / C;
+  const bool active = g < R;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int q0 = 0; q0 < np_s; q0 += kChunk) {
     const int n = min(kChunk, np_s - q0);
-    __syncthreads();  // previous chunk's weights are no longer read
-    if (lane < n) w_lds[lane] = expf(ml[q0 + lane] - M);
+    __syncthreads();  // the previous chunk's weights are no longer read
+    if (tid < n) w_lds[tid] = expf(ml[q0 + tid] - M);
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d0 = lane * 4 + 256 * i;
-      if (d0 < D) {
+    if (active) {
 #pragma unroll 4
-        for (int q = 0; q < n; ++q) {
-          const float r = w_lds[q];
-          const float4 v = *reinterpret_cast<const float4*>(tp + (int64_t)(q0 + q) * D + d0);
-          acc[i].x += r * v.x;
-          acc[i].y += r * v.y;
-          acc[i].z += r * v.z;
-          acc[i].w += r * v.w;
-        }
+      for (int q = g; q < n; q += R) {
+        const float r = w_lds[q];
+        const float4 v = *reinterpret_cast<const float4*>(tp + (int64_t)(q0 + q) * D + 4 * c);
+        acc.x += r * v.x;
+        acc.y += r * v.y;
+        acc.z += r * v.z;
+        acc.w += r * v.w;
       }
     }
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int d0 = lane * 4 + 256 * i;
-    if (d0 < D) {
-      E::store(op, d0 + 0, acc[i].x * inv);
-      E::store(op, d0 + 1, acc[i].y * inv);
-      E::store(op, d0 + 2, acc[i].z * inv);
-      E::store(op, d0 + 3, acc[i].w * inv);
+  if (active) part[g * C + c] = acc;
+  __syncthreads();
+  if (tid < C) {
+    float4 t = part[tid];
+    for (int j = 1; j < R; ++j) {
+      const float4 u = part[j * C + tid];
+      t.x += u.x;
+      t.y += u.y;
+      t.z += u.z;
+      t.w += u.w;
     }
+    E::store(op, 4 * tid + 0, t.x * inv);
+    E::store(op, 4 * tid + 1, t.y * inv);
+    E::store(op, 4 * tid + 2, t.z * inv);
+    E::store(op, 4 * tid + 3, t.w * inv);
   }
 }
 
@@ -1311,7 +1332,7 @@ int run_merge(const char* op, const MergeArgs& m, int32_t dtype, int32_t batch, 
   if (batch == 0) return ok();
   const dim3 grid(m.num_heads, batch);
   return dispatch_dtype(dtype, [&](auto tag) {
-    hipLaunchKernelGGL(decode_merge_kernel<decltype(tag)>, grid, dim3(64), 0, s, m);
+    hipLaunchKernelGGL(decode_merge_kernel<decltype(tag)>, grid, dim3(kMergeThreads), 0, s, m);
     return check_launch(op);
   });
 }
