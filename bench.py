@@ -27,6 +27,7 @@ if ROOT not in sys.path:
 METRIC = "paged decode achieved HBM GB/s (% of peak) + prefill MFMA util, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2516.6
+FP32_MFMA_PEAK_TFLOPS = 157.3
 
 
 def measured_traffic(key: str):
@@ -256,7 +257,9 @@ def side_fp32(device, gen, steps: int) -> dict:
             "bytes": w.decode_bytes()}
 
 
-def side_prefill(device, gen, steps: int) -> dict:
+def side_prefill(device, gen, steps: int, fp32: bool = False) -> dict:
+    """Config 4's packed causal prefill (bf16; with fp32 the same shapes in the reference's
+    element type, on the fp32 MFMA kernel, against the 157.3 TFLOP/s dense fp32 MFMA peak)."""
     import torch
 
     from railgun_amd import workloads as wl
@@ -267,10 +270,11 @@ def side_prefill(device, gen, steps: int) -> dict:
     op = PagedAttentionOp(w.scale, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size, kernels)
     T = w.num_tokens
     shape = (w.num_blocks, w.num_kv_heads, w.block_size, w.head_dim)
-    kc, vc = bf16_normal(shape, gen, device), bf16_normal(shape, gen, device)
-    q = bf16_normal((T, w.num_heads, w.head_dim), gen, device)
-    k = bf16_normal((T, w.num_kv_heads, w.head_dim), gen, device)
-    v = bf16_normal((T, w.num_kv_heads, w.head_dim), gen, device)
+    mk = (lambda sh: bf16_normal(sh, gen, device).float()) if fp32 else (lambda sh: bf16_normal(sh, gen, device))
+    kc, vc = mk(shape), mk(shape)
+    q = mk((T, w.num_heads, w.head_dim))
+    k = mk((T, w.num_kv_heads, w.head_dim))
+    v = mk((T, w.num_kv_heads, w.head_dim))
     cs = rope_cos_sin_table(int(w.context_lens.max()), w.head_dim, w.rope_theta, device)
     i32 = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
     pos, slots, bt, ctx, cu = (i32(a) for a in (w.positions, w.slot_mapping, w.block_table, w.context_lens,
@@ -285,6 +289,10 @@ def side_prefill(device, gen, steps: int) -> dict:
 
     ms = time_events(call, steps, 2)
     tflops = w.causal_flops() / (ms * 1e-3) / 1e12
+    if fp32:
+        return {"workload": "config4_shape_fp32_packed_prefill", "kernel": "prefill_f32_kernel "
+                "(v_mfma_f32_32x32x2_f32)", "tokens": T, "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 2),
+                "frac_fp32_mfma_peak": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4), "flops": w.causal_flops()}
     return {"workload": w.name, "tokens": T, "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 2),
             "frac_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops": w.causal_flops(),
             "traffic": measured_traffic("prefill_config4")}
@@ -471,7 +479,8 @@ def main() -> int:
         print(json.dumps(side_v2(device, gen, args.steps)), flush=True)
         return 0
     if args.only == "fp32":
-        print(json.dumps(side_fp32(device, gen, args.steps)), flush=True)
+        print(json.dumps({"decode": side_fp32(device, gen, args.steps),
+                          "prefill": side_prefill(device, gen, max(3, args.steps // 5), fp32=True)}), flush=True)
         return 0
     if args.only == "prefill":
         print(json.dumps(side_prefill(device, gen, args.steps)), flush=True)
@@ -542,6 +551,8 @@ def main() -> int:
         result["fp32_decode"] = side_fp32(device, gen, max(3, args.steps // 5))
         log("[bench] config4 prefill ...")
         result["prefill"] = side_prefill(device, gen, 10)
+        log("[bench] config4 prefill in fp32 ...")
+        result["fp32_prefill"] = side_prefill(device, gen, 3, fp32=True)
         log("[bench] config5 model step ...")
         result["model_step"] = side_model(device, 10)
         log("[bench] config5 projections ...")

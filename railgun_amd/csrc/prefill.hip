@@ -8,7 +8,8 @@
 // prefill_generic_kernel: one wave per (row, q-head), any dtype / head_dim /
 // block size; each lane owns 4 dims and the keys are visited in order with an
 // online softmax.  prefill_mfma_kernel (bf16/f16, head_dim 64/128, GQA 1, 2 or a multiple
-// of 4) is the MFMA tile kernel used whenever it applies.
+// of 4) is the MFMA tile kernel used whenever it applies; prefill_f32_kernel is its fp32
+// counterpart on v_mfma_f32_32x32x2_f32.
 #include <math.h>
 
 #include <algorithm>
@@ -803,6 +804,187 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   }  // units of this workgroup
 }
 
+// ------------------------------------------------------------ fp32 MFMA tile kernel --
+//
+// The reference's element type.  fp32 MFMA (v_mfma_f32_32x32x2_f32) is 16x slower per flop
+// than bf16 and the kernel is bound by it.  Units are tiles of UR query rows of one sequence
+// for GW heads of one kv-head (as in prefill_mfma_kernel: GW = min(G, 4) heads, 4 / GW
+// subtiles of 32 rows); workgroup (r, s, group) of the grid takes the units r, r + R, ... of
+// sequence s (R = gridDim.x).  The 32-key K and V tiles reach LDS by direct global -> LDS
+// copies into two buffers, tile kt + 1 in flight while tile kt computes.
+//
+//  * Scores transposed, S^T = K Q^T: lane (row l % 32, half h = l / 32) provides K[key l % 32]
+//    and Q[query l % 32] at the d of MFMA k-index h; inside a pair of steps the d order is
+//    permuted (k-index 0 <-> d = 4c + e, 1 <-> 4c + 2 + e), the same for both operands, so a
+//    lane reads its two K values of steps (c, 0) and (c, 1) as one 8-byte LDS read (K tile
+//    stored as [d / 4][key][4 floats]).  Q (scaled by scale * log2 e) stays in registers.
+//  * The output S^T[key][query] leaves lane l the query l % 32 and keys 8 j + 4 h + r, so the
+//    softmax statistics are per lane (the two halves of a query's 32 keys meet through one
+//    lane exchange).
+//  * O^T = V^T P^T: step (j, r) pairs keys 8 j + r (k-index 0) and 8 j + 4 + r (k-index 1),
+//    which are exactly the P values lane halves 0 and 1 hold in register (j, r); the V^T
+//    operand is 32 consecutive floats of a V row per half-wave (V tile row-major in LDS).
+//    Lane l accumulates O[query l % 32][d block b: 8 j + 4 h + r].
+template <int D, int GW>
+__global__ __launch_bounds__(kPThreads, 2) void prefill_f32_kernel(PrefillArgs a) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  constexpr int QS = kPWaves / GW;      // 32-row subtiles per unit
+  constexpr int UR = kPT * QS;          // rows per unit
+  constexpr int NC = D / 4;             // 16-byte pieces per row
+  constexpr int NDB = D / 32;           // d blocks of the output
+  constexpr int TILE = kPT * D;         // floats per K (or V) tile
+  constexpr int PER = TILE / 4 / kPThreads;  // copies per wave per operand and tile
+  static_assert(PER * 4 * kPThreads == TILE, "tile pieces per thread");
+  __shared__ __attribute__((aligned(16))) float k_lds[2][TILE];
+  __shared__ __attribute__((aligned(16))) float v_lds[2][TILE];
+  const uint32_t k_base = (uint32_t)(uintptr_t)((RG_LDS float*)&k_lds[0][0]);
+  const uint32_t v_base = (uint32_t)(uintptr_t)((RG_LDS float*)&v_lds[0][0]);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qi = lane & 31, h = lane >> 5;
+  const int s = blockIdx.y;
+  const int G = a.num_heads / a.num_kv_heads;
+  const int head = blockIdx.z * GW + (w % GW);
+  const int kvh = (blockIdx.z * GW) / G;
+  const int sub = w / GW;
+  const int row0 = a.cu_seqlens[s];
+  const int L = a.cu_seqlens[s + 1] - row0;
+  const int ctx = a.context_lens[s];
+  const int first = ctx - L;           // position of the sequence's first new row
+  const float* q = static_cast<const float*>(a.q);
+  const float* kc = static_cast<const float*>(a.k_cache);
+  const float* vc = static_cast<const float*>(a.v_cache);
+  float* out = static_cast<float*>(a.out);
+  const int32_t* bt = a.block_table + (int64_t)s * a.max_blocks;
+  int bs = a.block_size;
+  int key_cap = a.max_blocks * bs;  // positions the table row can address
+  int first_v = first;
+  // Per-lane arithmetic only: kept in VGPRs (the scalar registers are the tight budget here).
+  asm volatile("" : "+v"(bs), "+v"(key_cap), "+v"(first_v));
+
+  for (int unit = blockIdx.x; unit * UR < L; unit += gridDim.x) {
+    const int myrow = unit * UR + sub * kPT + qi;
+    const bool row_ok = myrow < L;
+    const int qpos = first_v + myrow;           // negative: a row without a position (zeros)
+    // Keys of the unit: positions 0 .. (position of its last row), within the context.
+    const int last_row = min(unit * UR + UR, L) - 1;
+    const int nkeys = __builtin_amdgcn_readfirstlane(max(0, min(min(ctx, key_cap), first_v + last_row + 1)));
+    const int ntiles = (nkeys + kPT - 1) / kPT;
+
+    // Copies of tile kt into buffer kt % 2: copy i of wave w moves LDS pieces
+    // 64 (w PER + i) + lane; keys past the unit's last read the last one (masked below).  The
+    // block-table reads come first, so that no wait for one of them falls between copies.
+    auto issue = [&](int kt) __attribute__((always_inline)) {
+      const uint32_t off = (uint32_t)((kt & 1) * TILE * 4);
+      int64_t ksrc[PER], vsrc[PER];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int pc = 64 * (w * PER + i) + lane;
+        const int kk = min(kt * kPT + pc % kPT, nkeys - 1);   // K image [d / 4][key][4]
+        ksrc[i] = (int64_t)bt[kk / bs] * a.kv_stride + ((int64_t)kvh * bs + kk % bs) * D + 4 * (pc / kPT);
+        const int vk = min(kt * kPT + pc / NC, nkeys - 1);     // V image row-major
+        vsrc[i] = (int64_t)bt[vk / bs] * a.kv_stride + ((int64_t)kvh * bs + vk % bs) * D + 4 * (pc % NC);
+      }
+      // Every address is formed (the compiler's waits for the table reads placed) before the
+      // first copy: a wait it placed after a copy would wait for that copy too.
+#pragma unroll
+      for (int i = 0; i < PER; ++i) asm volatile("" ::"v"(ksrc[i]), "v"(vsrc[i]));
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const uint32_t dst = off + (uint32_t)(64 * (w * PER + i)) * 16;
+        lds_dma16(kc + ksrc[i], k_base + dst);
+        lds_dma16(vc + vsrc[i], v_base + dst);
+      }
+    };
+
+    float qr[NC][2];
+    {
+      const int row = min(myrow, L - 1);
+      const float* qp = q + ((int64_t)(row0 + row) * a.num_heads + head) * D;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const float2 v = *reinterpret_cast<const float2*>(qp + 4 * c + 2 * h);
+        qr[c][0] = v.x * a.scale_log2;
+        qr[c][1] = v.y * a.scale_log2;
+      }
+    }
+    f32x16 o[NDB];
+#pragma unroll
+    for (int b = 0; b < NDB; ++b) o[b] = f32x16{};
+    float m = -INFINITY, lsum = 0.f;
+
+    if (ntiles > 0) issue(0);
+    for (int kt = 0; kt < ntiles; ++kt) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile kt
+      tile_barrier();                                   // ... and every wave's
+      if (kt + 1 < ntiles) issue(kt + 1);               // the buffer tile kt - 1 used
+      const float* kt_lds = k_lds[kt & 1];
+      const float* vt_lds = v_lds[kt & 1];
+
+      // S^T = K Q^T over d: steps (c, e).
+      f32x16 st = f32x16{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const float2 kv = *reinterpret_cast<const float2*>(kt_lds + (c * kPT + qi) * 4 + 2 * h);
+        st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qr[c][0], st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qr[c][1], st, 0, 0, 0);
+      }
+      // Mask, tile maximum, online softmax (log2 units).
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kt * kPT + 8 * j + 4 * h + r;
+          if (!row_ok || key > qpos || key >= nkeys) st[4 * j + r] = -INFINITY;
+          mx = fmaxf(mx, st[4 * j + r]);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mn = fmaxf(m, mx);
+      const float alpha = mn == -INFINITY ? 1.f : exp2f(m - mn);
+      float ps = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float pe = mn == -INFINITY ? 0.f : exp2f(st[e] - mn);
+        st[e] = pe;
+        ps += pe;
+      }
+      lsum = lsum * alpha + ps;
+      m = mn;
+#pragma unroll
+      for (int b = 0; b < NDB; ++b) o[b] *= alpha;
+      // O^T += V^T P^T over the tile's keys: steps (j, r).
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float* vrow = vt_lds + (8 * j + 4 * h + r) * D + qi;
+#pragma unroll
+          for (int b = 0; b < NDB; ++b) {
+            o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * b], st[4 * j + r], o[b], 0, 0, 0);
+          }
+        }
+    }
+    // The two halves of a query's row sum; rows without keys (or past the sequence) give 0.
+    const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    if (row_ok) {
+      float* op = out + ((int64_t)(row0 + myrow) * a.num_heads + head) * D;
+#pragma unroll
+      for (int b = 0; b < NDB; ++b)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = 32 * b + 8 * j + 4 * h;
+          *reinterpret_cast<float4*>(op + d) =
+              make_float4(o[b][4 * j] * inv, o[b][4 * j + 1] * inv, o[b][4 * j + 2] * inv, o[b][4 * j + 3] * inv);
+        }
+    }
+    __syncthreads();  // every wave is done with the LDS tiles before the next unit's copies
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -908,6 +1090,28 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
       if (head_dim == 128) go_gw(f16_t{}, D128{});
       else go_gw(f16_t{}, D64{});
     }
+    return check_launch(op);
+  }
+  // The fp32 MFMA tile kernel: head_dim 64 / 128, the GQA ratios of the 16-bit kernel, any
+  // block size, 16-byte aligned rows.
+  if (dtype == RG_DTYPE_F32 && (G == 1 || G == 2 || G % 4 == 0) && (head_dim == 64 || head_dim == 128) &&
+      max_blocks_per_seq > 0 && num_seqs <= 65535 && aligned16(query) && aligned16(key_cache) &&
+      aligned16(value_cache) && aligned16(output) && stride % 4 == 0) {
+    const int64_t UR = (int64_t)kPT * (kPWaves / GW);
+    const int64_t qmax = std::min<int64_t>(std::max<int32_t>(max_query_len, 1), num_tokens);
+    const dim3 grid((unsigned)((qmax + UR - 1) / UR), (unsigned)num_seqs, (unsigned)(num_heads / GW));
+    auto go = [&](auto dtag, auto gtag) {
+      constexpr int D = decltype(dtag)::value;
+      constexpr int W = decltype(gtag)::value;
+      hipLaunchKernelGGL((prefill_f32_kernel<D, W>), grid, dim3(kPThreads), 0, s, a);
+    };
+    auto go_gw = [&](auto dtag) {
+      if (GW == 4) go(dtag, std::integral_constant<int, 4>{});
+      else if (GW == 2) go(dtag, std::integral_constant<int, 2>{});
+      else go(dtag, std::integral_constant<int, 1>{});
+    };
+    if (head_dim == 128) go_gw(std::integral_constant<int, 128>{});
+    else go_gw(std::integral_constant<int, 64>{});
     return check_launch(op);
   }
   return dispatch_dtype(dtype, [&](auto tag) {

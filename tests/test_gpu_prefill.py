@@ -97,27 +97,47 @@ def test_prefill_config4(device, kernels):
     _run(device, kernels, w, seed=w.seed, row_sample=True)
 
 
-def _gqa_workload(G: int, D: int, lens, prior, seed: int, H: int = 32, mb: int = 0) -> wl.PrefillWorkload:
+def _gqa_workload(G: int, D: int, lens, prior, seed: int, H: int = 32, mb: int = 0, dt: str = "bf16",
+                  bs: int = 16) -> wl.PrefillWorkload:
     rng = np.random.default_rng(seed)
     lens, prior = np.asarray(lens, np.int32), np.asarray(prior, np.int32)
     hkv = H // G
-    need = int(((prior + lens + 15) // 16).sum())
-    mb = mb or int(((prior + lens + 15) // 16).max())
-    bt = wl.assign_blocks(prior + lens, 16, need + 4, mb, rng)
-    return wl.PrefillWorkload(f"gqa{G}_d{D}", "bf16", H, hkv, D, 16, need + 4, lens, bt, seed, prior=prior)
+    need = int(((prior + lens + bs - 1) // bs).sum())
+    mb = mb or int(((prior + lens + bs - 1) // bs).max())
+    bt = wl.assign_blocks(prior + lens, bs, need + 4, mb, rng)
+    return wl.PrefillWorkload(f"gqa{G}_d{D}", dt, H, hkv, D, bs, need + 4, lens, bt, seed, prior=prior)
 
 
-@pytest.mark.parametrize("G", [1, 2, 8, 16])
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
 @pytest.mark.parametrize("D", [64, 128])
-def test_prefill_mfma_gqa_ratios(device, kernels, G, D):
-    """The MFMA prefill beyond GQA 4: one head per workgroup on four 32-row subtiles (G 1), two
-    heads on two (G 2), two or four head groups of one kv-head (G 8, 16).  Ragged units (1 to 200
-    rows, lengths around the 32 / 64 / 128-row unit sizes), prior context, a sequence whose
-    rows end inside a unit's first subtile; every row against the oracle."""
+def test_prefill_mfma_gqa_ratios(device, kernels, G, D, dt):
+    """The MFMA prefill kernels (bf16 and fp32) beyond GQA 4: one head per workgroup on four
+    32-row subtiles (G 1), two heads on two (G 2), one or several head groups of one kv-head
+    (G 4, 8, 16).  Ragged units (1 to 200 rows, lengths around the 32 / 64 / 128-row unit
+    sizes), prior context, a sequence whose rows end inside a unit's first subtile; every row
+    against the oracle."""
     H = 16 if G == 1 else 32
     w = _gqa_workload(G, D, [1, 31, 33, 64, 65, 100, 129, 200, 7], [0, 0, 40, 0, 17, 300, 0, 64, 1000],
-                      seed=100 + G + D, H=H)
+                      seed=100 + G + D, H=H, dt=dt)
     _run(device, kernels, w, seed=200 + G + D, row_sample=True, row_stride=1)
+
+
+@pytest.mark.parametrize("bs", [16, 32, 8])
+def test_prefill_f32_long_and_block_sizes(device, kernels, bs):
+    """The fp32 MFMA prefill on longer sequences (up to 1,200 rows after up to 2,000 cached
+    positions, GQA 4, head_dim 128) and at block sizes 8 / 32 as well as 16 (its key tiles
+    address any block size); every sequence on a row sample against the oracle."""
+    w = _gqa_workload(4, 128, [1200, 700, 333, 64], [0, 2000, 5, 100], seed=500 + bs, dt="f32", bs=bs)
+    _run(device, kernels, w, seed=600 + bs, row_sample=True)
+
+
+@pytest.mark.parametrize("max_query_len", [None, 1])
+def test_prefill_f32_understated_max_query_len(device, kernels, max_query_len):
+    """fp32: with max_query_len = 1 one workgroup per sequence and head group walks every unit
+    of its sequence, which must give the same result as the full grid."""
+    w = _gqa_workload(4, 64, [33, 170, 5, 96], [300, 2100, 0, 40], seed=71, dt="f32", H=16)
+    _run(device, kernels, w, seed=72, max_query_len=max_query_len)
 
 
 @pytest.mark.parametrize("G", [1, 2, 8])
