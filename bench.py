@@ -8,6 +8,12 @@ HBM).  ``roofline`` is for the dominant call, paged attention v1 (partition + me
 kernels), timed with HIP events on the stream it is launched on.  Side figures: config 3
 (v2 split-K, 8 x 32k) and config 4 (packed causal prefill, bf16 MFMA roofline).
 
+Every timed region is preceded by ``SETTLE_MS`` of the same calls back to back (untimed, on
+top of the warmup calls): the GPU's clocks ramp over the first ~10-20 ms of load (measured:
+config 2's v1 call 114-115 us in its first 10 ms, 111-112 us after; config 4's prefill
+158-187 us in its first rounds, 144 us after), and a figure timed inside that ramp is not the
+steady state.
+
 ``cpu_baseline`` times the restated reference CPU path (gather -> q.K^T*scale -> softmax -> .V,
 oracle/oracle.c) on every host core this process may use, over the whole config-2 batch.
 """
@@ -28,6 +34,7 @@ METRIC = "paged decode achieved HBM GB/s (% of peak) + prefill MFMA util, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2516.6
 FP32_MFMA_PEAK_TFLOPS = 157.3
+SETTLE_MS = 100.0  # back-to-back calls before each timed region (clock ramp, see above)
 
 
 def measured_traffic(key: str):
@@ -64,14 +71,30 @@ def bf16_normal(shape, gen, device):
     return torch.randn(shape, generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
 
 
+def settle(fn, ms: float = SETTLE_MS) -> None:
+    """Runs fn() back to back (synchronising after each batch of calls) until `ms` of wall time
+    have passed, so that the GPU clocks have left their ramp before a timed region."""
+    import torch
+
+    t0 = time.perf_counter()
+    n = 1
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        n = min(2 * n, 64)
+
+
 def time_events(fn, steps: int, warmup: int):
-    """Average ms per call of fn() over `steps` back-to-back calls: one HIP event pair on the
-    current stream (the stream every launch goes to) brackets them all, so no event record
-    sits between two calls (a record between calls adds its own gap to the GPU timeline)."""
+    """Average ms per call of fn() over `steps` back-to-back calls, after `warmup` calls and the
+    settle phase: one HIP event pair on the current stream (the stream every launch goes to)
+    brackets them all, so no event record sits between two calls (a record between calls adds
+    its own gap to the GPU timeline)."""
     import torch
 
     for _ in range(warmup):
         fn()
+    settle(fn)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -504,6 +527,7 @@ def main() -> int:
 
     for _ in range(args.warmup):
         step()
+    settle(step)
     torch.cuda.synchronize()
     # Timed region: exactly K whole steps, back to back, between one pair of events.
     t_start = torch.cuda.Event(enable_timing=True)
@@ -526,7 +550,7 @@ def main() -> int:
 
     result = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "settle_ms": SETTLE_MS, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) q/k/v and pool, shuffled tables)",
         "config": {"workload": w.name, "batch": w.batch, "context": "U[512,4096]", "context_tokens":
                    int(w.context_lens.sum()), "heads": f"{w.num_heads}/{w.num_kv_heads}", "head_dim": w.head_dim,

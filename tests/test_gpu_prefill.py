@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close, dev_f32, i32, normal, to_dev
+from helpers import TORCH_DT, assert_close, dev_f32, i32, normal, to_dev
 from oracle import oracle as orc
 from railgun_amd import workloads as wl
 from railgun_amd.ops import rope_cos_sin_table
@@ -263,3 +263,43 @@ def test_prefill_rows_without_position(device, kernels, D):
     assert not np.isnan(got).any()
     assert_close(got, want, "bf16", "rows without a position")
     assert np.all(got[cu[2]:cu[3]] == 0)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_prefill_rising_scores(device, kernels, dt):
+    """Scores that climb along the keys (about 9 log2 units per 32-key tile on average, up to
+    33 where the oscillation on top rises), so that the running maximum keeps moving: the MFMA
+    kernel's lazy maximum, which moves only when a tile's maximum passes it by more than its
+    slack of 8 log2 units, moves on most tiles here and rescales the accumulated output each
+    time.  GQA 4, head_dim 128, prior context, every row against the oracle."""
+    rng = np.random.default_rng(57)
+    D, H, hkv, bs = 128, 32, 8, 16
+    lens = np.array([300, 150, 64, 1], np.int32)
+    prior = np.array([200, 0, 900, 700], np.int32)
+    ctx = prior + lens
+    need = int(((ctx + bs - 1) // bs).sum())
+    mb = int(((ctx + bs - 1) // bs).max())
+    bt = wl.assign_blocks(ctx, bs, need + 4, mb, rng)
+    nb = need + 4
+    u = rng.choice([-1.0, 1.0], size=(hkv, D)).astype(np.float32)
+    kc = (0.3 * rng.standard_normal((nb, hkv, bs, D))).astype(np.float32)
+    vc = rng.standard_normal((nb, hkv, bs, D)).astype(np.float32)
+    for s in range(len(lens)):
+        t = np.arange(int(ctx[s]))
+        g = 0.0077 * t + 0.9 * np.sin(t / 31.0)
+        blk, off = bt[s, t // bs], t % bs
+        kc[blk, :, off, :] += g[:, None, None] * u[None, :, :]
+    T = int(lens.sum())
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q = (2.0 * np.repeat(u, H // hkv, axis=0)[None] + 0.3 * rng.standard_normal((T, H, D))).astype(np.float32)
+    q, kc, vc = (orc.from_f32(x, dt) for x in (q, kc, vc))
+    scale = 1.0 / math.sqrt(D)
+    out = torch.full((T, H, D), float("nan"), dtype=TORCH_DT[dt], device=device)
+    kernels.launch_prefill_packed(to_dev(q, dt, device), to_dev(kc, dt, device), to_dev(vc, dt, device),
+                                  i32(bt, device), i32(ctx, device), i32(cu, device), out, scale, H, hkv, D, bs, mb,
+                                  len(lens), T, int(lens.max()))
+    torch.cuda.synchronize()
+    want = orc.prefill_packed(q, kc, vc, bt, ctx, cu, scale, dt)
+    got = dev_f32(out)
+    assert not np.isnan(got).any()
+    assert_close(got, want, dt, "rising scores")
