@@ -1060,14 +1060,17 @@ __global__ __launch_bounds__(64 * G) void decode_stream_merge_kernel(StreamArgs 
   const int lane = threadIdx.x & 63;
   const int hkv = a.num_kv_heads;
   S* out = static_cast<S*>(a.out) + ((int64_t)s * a.num_heads + (int64_t)kvh * G + h) * D + lane * PER;
-  const int nblk = seq_blocks(context_lens, s, a.max_blocks);
-  if (nblk == 0) {
+  // The segment's workers, as the first of them recorded (their partials: first + g .. ); the
+  // descriptor is loaded together with the context length (one memory round trip, not two)
+  // and used only when the segment has units (a segment without any keeps a stale entry).
+  const int2 dsc = a.seg_desc[(int64_t)s * hkv + kvh];
+  const int ctx = context_lens[s];
+  asm volatile("" ::"s"(dsc.x), "s"(dsc.y), "s"(ctx));  // both loads issued before either is waited for
+  if (min(ctx, a.max_blocks * kBS) <= 0) {  // no blocks (seq_blocks == 0)
 #pragma unroll
     for (int e = 0; e < PER; ++e) out[e] = 0;
     return;
   }
-  // The segment's workers, as the first of them recorded (their partials: first + g .. ).
-  const int2 dsc = a.seg_desc[(int64_t)s * hkv + kvh];
   const int64_t pbase = (int64_t)dsc.x + (int64_t)s * hkv + kvh;  // partial index of the first worker
   const int np = dsc.y;
 
