@@ -15,15 +15,17 @@ import pytest
 import torch
 
 from railgun_amd import _lib
-from railgun_amd.ops import RailgunError, linear
+from railgun_amd.ops import RailgunError, linear, linear_residual, linear_workspace_bytes
 
 pytestmark = pytest.mark.gpu
 
 TORCH = {"bf16": torch.bfloat16, "f16": torch.float16}
 
 
-def _check(out: torch.Tensor, x: torch.Tensor, w: torch.Tensor, what: str) -> None:
-    ref = x.float().cpu() @ w.float().cpu().T
+def _check(out: torch.Tensor, x: torch.Tensor, w: torch.Tensor, what: str, ref_on_device: bool = False) -> None:
+    # (the float32 product of the largest shapes runs on the device: torch's fp32 GEMM there is
+    # a plain fp32 product, no reduced-precision inputs)
+    ref = (x.float() @ w.float().T).cpu() if ref_on_device else x.float().cpu() @ w.float().cpu().T
     got = out.float().cpu()
     # one rounding of the output type (2^-8 relative for bf16, 2^-11 for f16), on a floor of the
     # typical magnitude for outputs near zero
@@ -48,6 +50,50 @@ def test_linear_matches_fp32(device, M, N, K, dt):
     again = linear(x, w)
     torch.cuda.synchronize()
     assert torch.equal(again.view(torch.int16), out.view(torch.int16)), "not deterministic"
+
+
+@pytest.mark.parametrize("M,N,K,dt", [(128, 128256, 2048, "bf16"), (100, 128256, 2048, "f16"), (17, 128256, 2048, "bf16"),
+                                      (37, 65536, 128, "bf16"), (90, 131072, 128, "f16"), (64, 128256, 256, "f16")])
+def test_linear_large_n(device, M, N, K, dt):
+    """Large N: the Llama LM head (N = 128,256) at 128, 100 and 17 rows (full, ragged and
+    two-block row tiles), N = 64 k / 128 k with K of one chunk, fp16; against the fp32 product
+    and repeatable bit for bit."""
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g).to(TORCH[dt]).to(device)
+    w = (0.02 * torch.randn(N, K, generator=g)).to(TORCH[dt]).to(device)
+    out = linear(x, w)
+    torch.cuda.synchronize()
+    _check(out, x, w, f"{M}x{N}x{K} {dt}", ref_on_device=True)
+    again = linear(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(again.view(torch.int16), out.view(torch.int16)), "not deterministic"
+
+
+def test_linear_large_n_strided_and_residual(device):
+    """Large N with x a column slice of a wider activation and out a column slice of a wider
+    buffer (untouched around it), and the residual epilogue at a large N: bit for bit the
+    rounded product added to the residual and rounded (the residual add of rg_rms_norm)."""
+    g = torch.Generator().manual_seed(11)
+    K, N, M = 1024, 32768, 128
+    act = torch.randn(M, K + 64, generator=g).to(torch.bfloat16).to(device)
+    x = act[:, 64:]
+    w = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).to(device)
+    buf = torch.full((M, N + 32), 7.0, dtype=torch.bfloat16, device=device)
+    out = buf[:, 16:16 + N]
+    linear(x, w, out)
+    torch.cuda.synchronize()
+    _check(out, x, w, "strided, large N", ref_on_device=True)
+    assert bool((buf[:, :16] == 7.0).all()) and bool((buf[:, 16 + N:] == 7.0).all())
+    M2, N2, K2 = 48, 65536, 640
+    x2 = torch.randn(M2, K2, generator=g).to(torch.bfloat16).to(device)
+    w2 = (0.02 * torch.randn(N2, K2, generator=g)).to(torch.bfloat16).to(device)
+    res = torch.randn(M2, N2, generator=g).to(torch.bfloat16).to(device)
+    prod = linear(x2, w2)  # the same tiles, rounded once
+    want = (res.float() + prod.float()).to(torch.bfloat16)
+    linear_residual(x2, w2, res)
+    torch.cuda.synchronize()
+    _check(prod, x2, w2, "large N", ref_on_device=True)
+    assert torch.equal(res.view(torch.int16), want.view(torch.int16)), "residual epilogue"
 
 
 def test_linear_strided_rows(device):
@@ -215,7 +261,6 @@ def test_linear_residual(device, M, N, K, dt):
     """residual += x @ W^T equals rg_linear's rounded output added to the residual and rounded
     (the residual add of rg_rms_norm) bit for bit, with and without a split of K; the residual
     a column slice of a wider buffer whose other columns stay untouched."""
-    from railgun_amd.ops import linear_residual, linear_workspace_bytes
     t = TORCH[dt]
     g = torch.Generator().manual_seed(M + N + 3 * K)
     x = torch.randn(M, K, generator=g).to(t).to(device)
