@@ -111,7 +111,7 @@ struct GemmRing {
 // tile to a.part[y] and splitk_reduce_kernel finishes.
 //
 // X and W reach LDS by direct copies of whole 256-byte row pieces (1 KB per wave instruction:
-// 4 rows); 16-byte piece p of row R sits at piece p ^ (R % 16), so the MFMA fragment reads
+// 4 rows; W's copies non-temporal: each weight byte is read once per call); 16-byte piece p of row R sits at piece p ^ (R % 16), so the MFMA fragment reads
 // below (16 rows at one piece) touch every bank once.  The 4 waves take one k-step of 32
 // each from every chunk, so the workgroup reads each operand byte once, and each X fragment
 // feeds NB MFMAs.  The quarters are summed through LDS in a fixed order.
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int q = 0; q < MB; ++q) lds_dma16_s(xbase + kb, xoff[q], slot + (w * MB + q) * 1024);
 #pragma unroll
-    for (int q = 0; q < NB; ++q) lds_dma16_s(wbase + kb, woff[q], slot + 16 * MB * kChunkBytes + (w * NB + q) * 1024);
+    for (int q = 0; q < NB; ++q) lds_dma16_s_nt(wbase + kb, woff[q], slot + 16 * MB * kChunkBytes + (w * NB + q) * 1024);
   };
 
   gf32x4_t acc[NB][MB];
