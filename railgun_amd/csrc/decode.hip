@@ -712,7 +712,9 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 // rescale decision, LDS exchange, cursor) is the same as at head_dim 128.  Units of four
 // blocks (16 KB) with two of them in flight measured fastest: 206.6 us per layer at the
 // Llama-3.2-1B step against 216.6 us for two-block units three deep and 236.5 us for
-// one-block units four deep (2 x 4, 2 x 5 and 3 x 3 were in between).
+// one-block units four deep (2 x 4, 2 x 5 and 3 x 3 were in between), with ordinary K/V
+// loads; with the non-temporal loads 4 x 2 stays ahead of 2 x 3 and 4 x 3 (194.7 against
+// 196.0 / 198.0 us per call), as one-block units three deep do at head_dim 128.
 #ifndef RG_SK_BPU_D64
 #define RG_SK_BPU_D64 4
 #endif
