@@ -545,11 +545,11 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   // test needs no multiply: raw maximum > m_thr  <=>  scaled maximum > m_run + kSlack.
   float m_thr = -INFINITY;
 
-  // The tile loop is software-pipelined: iteration kt turns the scores of tile kt into
-  // probabilities while the MFMA unit computes the scores of tile kt+1, then accumulates
-  // O^T += V^T P^T of tile kt while the VALU masks and reduces the scores of tile kt+1.
-  // Ring: tile kt+1's K and tile kt's V are read during iteration kt; copies of tiles
-  // kt+2 .. kt+kPStages-1 are in flight.
+  // The tile loop runs each tile in order (scores, maximum, probabilities, PV); the overlap
+  // of one wave's softmax with another's MFMAs comes from the three workgroups sharing each
+  // SIMD.  Ring: iteration kt reads tile kt's K and V from its stage; copies of tiles
+  // kt+1 .. kt+kPStages-1 are in flight (tile kt+kPStages-1 issued during kt's QK MFMAs into
+  // the stage tile kt-1 left).
   static_assert(kPStages >= 3 && kPStages <= 64, "ring depth");
   const char* vlds = lds + TL::KBYTES;
   const int grp = lane >> 4;
