@@ -12,7 +12,7 @@
 namespace rg {
 namespace {
 
-constexpr unsigned long long kNoError = 0x7F7F7F7F7F7F7F7FULL;  // the result cell's fill
+constexpr unsigned long long kNoError = 0x7F7F7F7F7F7F7F7FULL;  // the result cell before a scan
 
 // One workgroup per sequence: code s * (max_blocks + 1) for a context length outside
 // [0, max_blocks * block_size], s * (max_blocks + 1) + 1 + i for table entry i (one of the
@@ -43,6 +43,10 @@ __global__ __launch_bounds__(256) void check_slots_kernel(const int32_t* __restr
   }
 }
 
+// Sets the result cell to kNoError (a kernel rather than a memset, so the stream carries
+// kernels only).
+__global__ void fill_cell_kernel(unsigned long long* cell) { *cell = kNoError; }
+
 // The result cell of each device (allocated on first use, held until the process ends).
 std::mutex g_cell_mutex;
 std::vector<unsigned long long*> g_cells;
@@ -64,7 +68,8 @@ template <typename F>
 int run_check(const char* op, hipStream_t s, F&& launch, unsigned long long* found) {
   unsigned long long* cell = nullptr;
   if (int st = result_cell(op, &cell)) return st;
-  if (hipMemsetAsync(cell, 0x7F, sizeof(*cell), s) != hipSuccess) return fail(RG_ERR_HIP, "%s: memset failed", op);
+  hipLaunchKernelGGL(fill_cell_kernel, dim3(1), dim3(1), 0, s, cell);
+  if (int st = check_launch(op)) return st;
   launch(cell);
   if (int st = check_launch(op)) return st;
   if (hipMemcpyAsync(found, cell, sizeof(*found), hipMemcpyDeviceToHost, s) != hipSuccess ||
