@@ -18,6 +18,7 @@
 //! failure -> `Tensor(message)`.
 
 use std::os::raw::{c_int, c_void};
+use std::sync::{Arc, Mutex};
 
 use vllm_core::{CoreError, Device, Result as CoreResult};
 
@@ -48,6 +49,10 @@ pub struct PagedAttentionKernels {
     ordinal: usize,
     stream: *mut c_void,
     kv_block_stride: i64,
+    /// Grow-only device workspace of `PagedAttentionOp::execute`'s split-K forms, shared by
+    /// the clones of this object (one `Arc<PagedAttentionKernels>` serves every layer,
+    /// model.rs:127, while the op itself is built anew for each call, attention.rs:109-116).
+    workspace: Arc<Mutex<Option<HipSlice<u8>>>>,
 }
 
 // SAFETY: the stream handle may be used from any thread (HIP orders work per stream).
@@ -67,7 +72,7 @@ impl PagedAttentionKernels {
             });
         }
         match unsafe { ffi::rg_init(ordinal as c_int) } {
-            ffi::RG_OK => Ok(Self { ordinal, stream, kv_block_stride: 0 }),
+            ffi::RG_OK => Ok(Self { ordinal, stream, kv_block_stride: 0, workspace: Arc::new(Mutex::new(None)) }),
             _ => Err(CoreError::DeviceInit { device: Device::Cuda(ordinal as u32), reason: last_error() }),
         }
     }
@@ -89,6 +94,21 @@ impl PagedAttentionKernels {
 
     pub fn kv_block_stride(&self) -> i64 {
         self.kv_block_stride
+    }
+
+    /// Runs `f` with a device workspace of at least `bytes` bytes that outlives the call: it
+    /// is allocated on first use and replaced by a larger one only when a call needs more, so
+    /// repeated calls neither allocate nor synchronise.  Every launch that uses it goes to
+    /// this object's stream, which orders consecutive users; the smaller buffer a growth
+    /// replaces is released with `hipFree`, which waits for the device first.
+    pub fn with_workspace<R>(&self, bytes: usize, f: impl FnOnce(&mut HipSlice<u8>) -> CoreResult<R>)
+                             -> CoreResult<R> {
+        let mut guard = self.workspace.lock().map_err(|_| CoreError::Tensor("workspace lock poisoned".into()))?;
+        if guard.as_ref().map_or(true, |w| w.len() < bytes) {
+            *guard = None;  // free the smaller one first
+            *guard = Some(HipSlice::<u8>::alloc(bytes.max(1), self.ordinal)?);
+        }
+        f(guard.as_mut().expect("workspace allocated above"))
     }
 
     /// mod.rs:196-225

@@ -32,9 +32,11 @@ fn shape_err(what: &str) -> CoreError {
 
 impl PagedAttentionOp {
     /// paged_attn_op.rs:45-166: q [batch, num_heads, head_dim] -> a new output of the same
-    /// shape.  `max_context_len <= 4096` runs v1+ split over every compute unit, longer runs
-    /// the v2 split-K form; both allocate their workspace for the call, as the reference
-    /// allocates its v2 scratch (:113-123).
+    /// shape (zero-filled first, as :86 does).  `max_context_len <= 4096` runs v1+ split over
+    /// every compute unit, longer runs the v2 split-K form.  Their scratch is the kernels'
+    /// grow-only workspace (`PagedAttentionKernels::with_workspace`), not an allocation per
+    /// call as the reference's v2 scratch is (:113-123): the call only queues work on the
+    /// kernels' stream and returns without waiting for it.
     pub fn execute<T: KvElement>(
         &self,
         q: &HipSlice<T>,
@@ -68,24 +70,27 @@ impl PagedAttentionOp {
         let (h, hkv, d, bs) = (self.num_heads as i32, self.num_kv_heads as i32, self.head_dim as i32,
                                self.block_size as i32);
         let v1_ws = k.v1_workspace_bytes(batch as i32, h, hkv, d, bs, max_blocks as i32);
-        // SAFETY: shapes checked above; indices are the caller's responsibility, as in the reference.
-        unsafe {
-            if max_context_len <= V1_MAX_CONTEXT {
-                let mut ws = HipSlice::<u8>::alloc(v1_ws, k.ordinal())?;
-                k.launch_v1_split(q, k_cache, v_cache, block_table, context_lens, &mut out, self.scale, h, hkv, d, bs,
-                                  max_blocks as i32, batch as i32, &mut ws)?;
-                let _ = rotation_metadata;  // identity rotation
-                // The workspace is freed after the kernels that use it have run.
-                crate::hip::hipStreamSynchronize(k.stream());
-            } else {
-                let parts = (max_context_len + EXECUTE_V2_PARTITION - 1) / EXECUTE_V2_PARTITION;
-                let bytes = k.v2_workspace_bytes(batch as i32, h, parts as i32, d).max(v1_ws);
-                let mut ws = HipSlice::<u8>::alloc(bytes, k.ordinal())?;
-                k.launch_v2(q, k_cache, v_cache, block_table, context_lens, &mut out, self.scale, h, hkv, d, bs,
-                            max_blocks as i32, batch as i32, max_context_len as i32, EXECUTE_V2_PARTITION as i32,
-                            &mut ws)?;
-                crate::hip::hipStreamSynchronize(k.stream());
-            }
+        let _ = rotation_metadata;  // identity rotation
+        if max_context_len <= V1_MAX_CONTEXT {
+            k.with_workspace(v1_ws, |ws| {
+                // SAFETY: shapes checked above; indices are the caller's responsibility, as in
+                // the reference.
+                unsafe {
+                    k.launch_v1_split(q, k_cache, v_cache, block_table, context_lens, &mut out, self.scale, h, hkv,
+                                      d, bs, max_blocks as i32, batch as i32, ws)
+                }
+            })?;
+        } else {
+            let parts = (max_context_len + EXECUTE_V2_PARTITION - 1) / EXECUTE_V2_PARTITION;
+            let bytes = k.v2_workspace_bytes(batch as i32, h, parts as i32, d).max(v1_ws);
+            k.with_workspace(bytes, |ws| {
+                // SAFETY: as above.
+                unsafe {
+                    k.launch_v2(q, k_cache, v_cache, block_table, context_lens, &mut out, self.scale, h, hkv, d, bs,
+                                max_blocks as i32, batch as i32, max_context_len as i32,
+                                EXECUTE_V2_PARTITION as i32, ws)
+                }
+            })?;
         }
         Ok(out)
     }

@@ -23,6 +23,8 @@
 #define OR_F32 0
 #define OR_BF16 1
 #define OR_F16 2
+/* head_dim bound of the gathered prefill rows (larger ones take prefill_row) */
+#define OR_MAX_GATHER_D 1024
 
 /* ------------------------------------------------------------ elements ---- */
 
@@ -429,16 +431,60 @@ void or_prefill_packed(const void* q, const void* kc, const void* vc, const int3
 /* The same rows as or_prefill_packed, for a list of packed row indices only
  * (rows[i] in [0, cu[S])), spread over `nthreads` POSIX threads: every listed
  * row of `out` is written exactly as or_prefill_packed writes it, the others
- * are left untouched.  For long streams where every row would take minutes. */
+ * are left untouched.  For long streams where every row would take minutes.
+ *
+ * Speed only: the K and V rows of every (sequence, kv-head) that a listed row
+ * needs are first gathered once into contiguous fp32 arrays [ctx, D] (the
+ * values ld() returns), so the per-row loops read plain floats.  The products,
+ * sums and their order are those of prefill_row, so the results are the same
+ * bits (tests/test_oracle.py checks this). */
 typedef struct {
   const dec_args* a;
   const int32_t* cu;
   const int32_t* rows;
   float* out;
+  float** kg; /* [s * Hkv + kvh] -> gathered K rows [ctx_s, D] (NULL if unused) */
+  float** vg;
   int nrows;
   int next;
   pthread_mutex_t mu;
 } prefill_job;
+
+static void prefill_row_gathered(const prefill_job* job, int s, int row, double* sc, double* acc) {
+  const dec_args* a = job->a;
+  const int L = job->cu[s + 1] - job->cu[s];
+  const int pos = a->ctx[s] - L + (row - job->cu[s]);
+  const int H = a->H, D = a->D;
+  for (int h = 0; h < H; ++h) {
+    float* o = job->out + ((int64_t)row * H + h) * D;
+    if (pos < 0) {
+      memset(o, 0, sizeof(float) * D);
+      continue;
+    }
+    const int kvh = h / (H / a->Hkv);
+    const float* K = job->kg[(int64_t)s * a->Hkv + kvh];
+    const float* V = job->vg[(int64_t)s * a->Hkv + kvh];
+    double qd[OR_MAX_GATHER_D];
+    for (int d = 0; d < D; ++d) qd[d] = (double)ld(a->q, ((int64_t)row * H + h) * D + d, a->dt);
+    double mx = -INFINITY;
+    for (int t = 0; t <= pos; ++t) {
+      const float* kr = K + (int64_t)t * D;
+      double dot = 0.0;
+      for (int d = 0; d < D; ++d) dot += qd[d] * (double)kr[d];
+      sc[t] = dot * (double)a->scale;
+      if (sc[t] > mx) mx = sc[t];
+    }
+    double sum = 0.0;
+    for (int d = 0; d < D; ++d) acc[d] = 0.0;
+    for (int t = 0; t <= pos; ++t) {
+      const double e = exp(sc[t] - mx);
+      sum += e;
+      const float* vr = V + (int64_t)t * D;
+      for (int d = 0; d < D; ++d) acc[d] += e * (double)vr[d];
+    }
+    for (int d = 0; d < D; ++d) o[d] = (float)(acc[d] / sum);
+  }
+}
 
 static void* prefill_worker(void* arg) {
   prefill_job* job = (prefill_job*)arg;
@@ -453,7 +499,8 @@ static void* prefill_worker(void* arg) {
     const int row = job->rows[i];
     int s = 0;
     while (s + 1 < a->B && job->cu[s + 1] <= row) ++s;
-    prefill_row(a, job->cu, job->out, s, row, sc, acc);
+    if (a->D <= OR_MAX_GATHER_D) prefill_row_gathered(job, s, row, sc, acc);
+    else prefill_row(a, job->cu, job->out, s, row, sc, acc);
   }
   free(sc);
   free(acc);
@@ -472,6 +519,29 @@ void or_prefill_packed_rows(const void* q, const void* kc, const void* vc, const
   job.out = out;
   job.nrows = nrows;
   job.next = 0;
+  job.kg = (float**)calloc((size_t)S * Hkv, sizeof(float*));
+  job.vg = (float**)calloc((size_t)S * Hkv, sizeof(float*));
+  /* Gather the (sequence, kv-head) rows the listed rows read: positions 0 .. ctx - 1. */
+  if (D <= OR_MAX_GATHER_D) {
+    for (int i = 0; i < nrows; ++i) {
+      int s = 0;
+      while (s + 1 < S && cu[s + 1] <= rows[i]) ++s;
+      if (job.kg[(int64_t)s * Hkv] || ctx[s] <= 0) continue;
+      for (int h = 0; h < Hkv; ++h) {
+        float* K = (float*)malloc(sizeof(float) * (size_t)ctx[s] * D);
+        float* V = (float*)malloc(sizeof(float) * (size_t)ctx[s] * D);
+        for (int t = 0; t < ctx[s]; ++t) {
+          const int64_t r = token_row(&a, s, h, t);
+          for (int d = 0; d < D; ++d) {
+            K[(int64_t)t * D + d] = ld(kc, r + d, dt);
+            V[(int64_t)t * D + d] = ld(vc, r + d, dt);
+          }
+        }
+        job.kg[(int64_t)s * Hkv + h] = K;
+        job.vg[(int64_t)s * Hkv + h] = V;
+      }
+    }
+  }
   pthread_mutex_init(&job.mu, NULL);
   if (nthreads < 1) nthreads = 1;
   pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * nthreads);
@@ -479,6 +549,12 @@ void or_prefill_packed_rows(const void* q, const void* kc, const void* vc, const
   for (int i = 0; i < nthreads; ++i) pthread_join(th[i], NULL);
   free(th);
   pthread_mutex_destroy(&job.mu);
+  for (int64_t i = 0; i < (int64_t)S * Hkv; ++i) {
+    free(job.kg[i]);
+    free(job.vg[i]);
+  }
+  free(job.kg);
+  free(job.vg);
 }
 
 /* ------------------------------------------- reference CPU attention path --- */

@@ -342,6 +342,19 @@ struct DecodeTile {
   __device__ __forceinline__ void load(const S* kb, const S* vb, uint4 (&kk)[NK], uint4 (&vv)[NV]) const {
     load_part<1, 0>(kb, vb, kk, vv);
   }
+  // load(), or with live == false the same number of load instructions, each reading the first
+  // 16 bytes of kb (of vb) in every lane: one line per instruction instead of 16 rows.  A
+  // pipeline that issues a fixed number of loads per step (so that the compiler's waits are
+  // exact counts) fills its slots past the last block this way.
+  __device__ __forceinline__ void load_or_line(const S* kb, const S* vb, bool live, uint4 (&kk)[NK],
+                                               uint4 (&vv)[NV]) const {
+    const int lm = live ? -1 : 0;
+    const uint4* kp = reinterpret_cast<const uint4*>(kb + ((col * D + seg * 8) & lm));
+#pragma unroll
+    for (int i = 0; i < NK; ++i) kk[i] = stream_load16(kp + ((4 * i) & lm));
+#pragma unroll
+    for (int i = 0; i < NV; ++i) vv[i] = stream_load16(vb + (((i * TPI + vrow) * D + vd0) & lm));
+  }
   // The same into entries [B*NK, (B+1)*NK) and [B*NV, (B+1)*NV) of an NB-block ring slot.
   template <int NB, int B>
   __device__ __forceinline__ void load_part(const S* kb, const S* vb, uint4 (&kk)[NB * NK], uint4 (&vv)[NB * NV]) const {
@@ -606,26 +619,28 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
   const int32_t* bt = block_table + (int64_t)s * a.max_blocks;
   const int64_t head_off = (int64_t)kvh * a.block_size * D;
   const int sh = a.bs_shift, sub_mask = (1 << sh) - 1;
+  // Block j of this wave, or (j >= nb) one line of its last block per load instruction.
   auto load_block = [&](int j, uint4 (&kk)[NK], uint4 (&vv)[NV]) {
-    const int lb = b0 + w + j * kWaves;
+    const int lb = b0 + w + min(j, nb - 1) * kWaves;
     const int64_t off = (int64_t)bt[lb >> sh] * a.kv_stride + head_off + (int64_t)(lb & sub_mask) * (kBS * D);
-    tile.load(kc + off, vc + off, kk, vv);
+    tile.load_or_line(kc + off, vc + off, j < nb, kk, vv);
   };
 
-  // Software pipeline: kPrefetch blocks in flight ahead of the one being computed; past
-  // the end the prefetch re-reads the wave's last block (a cache hit), so every step issues
-  // the same loads and the waits stay exact counts instead of full drains.
+  // Software pipeline: kPrefetch blocks in flight ahead of the one being computed.  Every
+  // step issues the same load instructions, so the waits stay exact counts instead of full
+  // drains; past the end they read one line of the wave's last block each (a re-read of the
+  // whole block was 1 in 8 of a P = 512 partition's requests).
   uint4 kbuf[NBUF][NK], vbuf[NBUF][NV];
   if (nb > 0) {
 #pragma unroll
-    for (int u = 0; u < kPrefetch; ++u) load_block(min(u, nb - 1), kbuf[u], vbuf[u]);
+    for (int u = 0; u < kPrefetch; ++u) load_block(u, kbuf[u], vbuf[u]);
   }
   for (int j0 = 0; j0 < nb; j0 += NBUF) {
 #pragma unroll
     for (int u = 0; u < NBUF; ++u) {
       const int j = j0 + u;
       if (j < nb) {
-        load_block(min(j + kPrefetch, nb - 1), kbuf[(u + kPrefetch) % NBUF], vbuf[(u + kPrefetch) % NBUF]);
+        load_block(j + kPrefetch, kbuf[(u + kPrefetch) % NBUF], vbuf[(u + kPrefetch) % NBUF]);
         tile.step(kbuf[u], vbuf[u], (b0 + w + j * kWaves) * kBS, ctx, a.scale_log2, p_lds[w][j & 1],
                   alpha_lds[w][j & 1]);
       }

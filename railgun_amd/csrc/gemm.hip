@@ -295,8 +295,11 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
     }
     // NORM: the MFMA takes x and W with one of them scaled by the norm weight of its k and
     // rounded — W when the tile has fewer W fragments than X fragments, else x — and the row
-    // scale 1 / rms(x) is applied to the sums at the end.
-    constexpr bool SCALE_W = NB < MB;
+    // scale 1 / rms(x) is applied to the sums at the end.  fp16 always scales W: x is the
+    // residual stream, not yet divided by its rms, and x * w_norm can pass fp16's 65504 (inf,
+    // then NaN logits) where the normalised operand of the unfused chain is about 1 in size;
+    // bf16 has fp32's exponent range and takes the cheaper side.
+    constexpr bool SCALE_W = NB < MB || std::is_same<T, f16_t>::value;
     float nw[8];  // the norm weight of this lane's 8 k
     if constexpr (NORM) {
       const uint4 u = *reinterpret_cast<const uint4*>(lds + RG::BYTES + (cb + c) * kChunkBytes + (4 * w + g) * 16);

@@ -18,9 +18,10 @@ then decode slots, :mod:`railgun_amd.batch`) runs as:
   MFMA GEMM, unless hipBLASLt (``F.linear``) measured more than 5 % faster for that shape on
   this device: each (rows, out, in) shape is timed when an eager step first meets it (three
   interleaved graph-replay trials of each, medians compared).  Larger (prefill) steps use
-  hipBLASLt.  The MLP's gate/up projection and SiLU·mul run as one ``rg_linear_silu_mul`` (over
-  a copy of the gate/up weight with the rows interleaved in blocks of 16) when that measured
-  faster than the projection followed by ``rg_silu_and_mul``.
+  hipBLASLt.  The MLP's gate/up projection and SiLU·mul run as one ``rg_linear_silu_mul`` (the
+  gate/up weight is held with its rows interleaved in blocks of 16, replaced in place) when that
+  measured faster than the projection followed by ``rg_silu_and_mul``.  ``choices`` (or the
+  ``RAILGUN_LLAMA_CHOICES`` environment variable) fixes these choices instead of timing them.
 
 Every layer owns a KV pool in Railgun's fused layout ``[NB, 2, H_kv, bs, D]``
 (crates/vllm-paged-attention/src/block.rs:70,89-95); the reference shares one pool across
@@ -29,7 +30,9 @@ fp32, every op's result rounded once to the activation dtype, as in candle.
 """
 from __future__ import annotations
 
+import logging
 import math
+import os
 from dataclasses import dataclass
 from typing import Optional
 
@@ -39,8 +42,21 @@ import torch.nn.functional as F
 
 from .batch import StepBatch
 from .kv_pool import GpuBlockPool
-from .ops import (LINEAR_MAX_ROWS, PagedAttentionKernels, interleave_gate_up, linear, linear_residual,
-                  linear_silu_mul, linear_workspace_bytes, rms_norm, rope_cos_sin_table, silu_and_mul)
+from .ops import (LINEAR_MAX_ROWS, PagedAttentionKernels, deinterleave_gate_up, interleave_gate_up, linear,
+                  linear_residual, linear_silu_mul, linear_workspace_bytes, rms_norm, rope_cos_sin_table,
+                  silu_and_mul)
+
+log = logging.getLogger(__name__)
+
+# How RailgunLlama picks between the equivalent forms of a step's projections (rg_linear or
+# hipBLASLt, fused or separate SiLU·mul and RoPE + cache write, RmsNorm folded or not):
+# "measured" times both once per shape on the device and keeps the faster (with a 5 % margin
+# for the hand-written form), "rg" always takes the hand-written / fused / folded form where the
+# shape allows it, "blas" always hipBLASLt and the separate launches.  The forms round
+# differently, so a fixed mode makes the logits of a step the same in every process and on
+# every box.  The constructor's `choices` argument wins over the environment variable.
+CHOICE_MODES = ("measured", "rg", "blas")
+CHOICES_ENV = "RAILGUN_LLAMA_CHOICES"
 
 
 def graph_us(fn, calls: int = 10, replays: int = 3) -> float:
@@ -98,6 +114,10 @@ class LayerWeights:
     post_norm: torch.Tensor    # [hidden]
     w_gate_up: torch.Tensor    # [2 I, hidden]: gate_proj, up_proj stacked
     w_down: torch.Tensor       # [hidden, I]
+    # True once RailgunLlama has replaced w_gate_up in place by its rows interleaved in blocks
+    # of 16 (interleave_gate_up: the layout rg_linear_silu_mul reads), so that only one copy
+    # of the weight is held; deinterleave_gate_up gives the stacked rows back.
+    gate_up_interleaved: bool = False
 
 
 @dataclass
@@ -186,7 +206,12 @@ class RailgunLlama:
     (engine.rs:238-245 samples from those)."""
 
     def __init__(self, cfg: LlamaConfig, weights: LlamaWeights, pool: GpuBlockPool,
-                 kernels: Optional[PagedAttentionKernels] = None, max_position: Optional[int] = None):
+                 kernels: Optional[PagedAttentionKernels] = None, max_position: Optional[int] = None,
+                 choices: Optional[str] = None):
+        mode = choices or os.environ.get(CHOICES_ENV) or "measured"
+        if mode not in CHOICE_MODES:
+            raise ValueError(f"choices must be one of {CHOICE_MODES}, got {mode!r}")
+        self.choice_mode = mode
         self.cfg = cfg
         self.w = weights
         self.pool = pool
@@ -201,7 +226,15 @@ class RailgunLlama:
         self.linear_choice: dict = {}
         # rows -> True for rg_linear_silu_mul, False for the projection + rg_silu_and_mul
         self.mlp_choice: dict = {}
-        self._w_gate_up_il: dict = {}  # layer -> interleaved gate/up weight
+        # The fused MLP form reads the gate/up weight with its rows interleaved in blocks of 16:
+        # each layer's weight is replaced by that layout in place (one copy held, not two); the
+        # separate form then de-interleaves the projection's output columns instead.
+        self._w_gate_up_il: dict = {}  # layer -> interleaved copy, only for weights left stacked
+        if mode != "blas" and self.dtype in (torch.bfloat16, torch.float16) and cfg.intermediate_size % 16 == 0:
+            for L in weights.layers:
+                if not L.gate_up_interleaved:
+                    L.w_gate_up = interleave_gate_up(L.w_gate_up)
+                    L.gate_up_interleaved = True
         # rows -> True for rg_linear_qkv_rope_reshape_and_cache, False for the projection +
         # rg_qkv_rope_reshape_and_cache
         self.qkv_choice: dict = {}
@@ -272,7 +305,9 @@ class RailgunLlama:
         use_rg = self.linear_choice.get(key)
         ws_bytes = linear_workspace_bytes(rows, n, k)
         if use_rg is None:
-            if torch.cuda.is_current_stream_capturing():
+            if self._fixed() is not None:
+                use_rg = self._fixed()
+            elif torch.cuda.is_current_stream_capturing():
                 use_rg = True                  # no timing inside a capture: the kernel built for it
             else:
                 out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
@@ -280,6 +315,8 @@ class RailgunLlama:
                 t_rg, t_blas = self._time_pair(lambda j: linear(x, peers[j], out, ws),
                                                lambda j: F.linear(x, peers[j]), len(peers))
                 use_rg = not t_blas < 0.95 * t_rg
+                log.info("projection %s: rg_linear %.2f us, hipBLASLt %.2f us -> %s", key, t_rg, t_blas,
+                         "rg_linear" if use_rg else "hipBLASLt")
             self.linear_choice[key] = use_rg
         if not use_rg:
             return F.linear(x, weight)
@@ -291,31 +328,32 @@ class RailgunLlama:
         inter = int(act.shape[1])
         rows = int(h.shape[0])
         if not (self._rg_linear_fits(h, L.w_gate_up) and inter % 16 == 0):
-            silu_and_mul(self._linear(h, "w_gate_up", layer), act)
+            self._mlp_act_separate(layer, h, act)
             return
         fused = self.mlp_choice.get(rows)
         if fused is None:
-            if torch.cuda.is_current_stream_capturing():
+            if self._fixed() is not None:
+                fused = self._fixed()
+            elif torch.cuda.is_current_stream_capturing():
                 fused = True
             else:
                 n = len(self.w.layers)
-                for j in range(n):
-                    if j not in self._w_gate_up_il:
-                        self._w_gate_up_il[j] = interleave_gate_up(self.w.layers[j].w_gate_up)
                 self._linear(h, "w_gate_up", layer)  # settles the projection's own choice outside the timing
-                t_f, t_s = self._time_pair(lambda j: linear_silu_mul(h, self._w_gate_up_il[j], act),
-                                           lambda j: silu_and_mul(self._linear(h, "w_gate_up", j), act), n)
+                t_f, t_s = self._time_pair(lambda j: linear_silu_mul(h, self._gate_up_il(j), act),
+                                           lambda j: self._mlp_act_separate(j, h, act), n)
                 fused = not t_s < 0.95 * t_f
-                if not fused and not any(self.mlp_choice.values()):
-                    self._w_gate_up_il.clear()
+                log.info("MLP at %d rows: fused gate/up + SiLU·mul %.2f us, separate %.2f us -> %s", rows, t_f,
+                         t_s, "fused" if fused else "separate")
             self.mlp_choice[rows] = fused
         if fused:
-            w_il = self._w_gate_up_il.get(layer)
-            if w_il is None:
-                w_il = self._w_gate_up_il[layer] = interleave_gate_up(L.w_gate_up)
-            linear_silu_mul(h, w_il, act)
+            linear_silu_mul(h, self._gate_up_il(layer), act)
         else:
-            silu_and_mul(self._linear(h, "w_gate_up", layer), act)
+            self._mlp_act_separate(layer, h, act)
+
+    def _mlp_act_separate(self, layer: int, h: torch.Tensor, act: torch.Tensor) -> None:
+        """The gate/up projection, then rg_silu_and_mul over [gate | up] columns."""
+        y = self._linear(h, "w_gate_up", layer)
+        silu_and_mul(deinterleave_gate_up(y) if self.w.layers[layer].gate_up_interleaved else y, act)
 
     def _qkv_rope_cache(self, layer: int, h: torch.Tensor, q: torch.Tensor, st: DeviceStep) -> None:
         """q/k/v = h @ wqkv^T, RoPE on q and k, k and v into the paged cache: fused in the
@@ -341,12 +379,16 @@ class RailgunLlama:
             return
         use_fused = self.qkv_choice.get(rows)
         if use_fused is None:
-            if torch.cuda.is_current_stream_capturing():
+            if self._fixed() is not None:
+                use_fused = self._fixed()
+            elif torch.cuda.is_current_stream_capturing():
                 use_fused = True
             else:
                 self._linear(h, "wqkv", layer)  # settles the projection's own choice outside the timing
                 t_f, t_u = self._time_pair(fused, unfused, len(peers))
                 use_fused = not t_u < 0.95 * t_f
+                log.info("q/k/v at %d rows: fused with RoPE + cache write %.2f us, separate %.2f us -> %s", rows,
+                         t_f, t_u, "fused" if use_fused else "separate")
             self.qkv_choice[rows] = use_fused
         (fused if use_fused else unfused)(layer)
 
@@ -366,10 +408,28 @@ class RailgunLlama:
                 and self.dtype in (torch.bfloat16, torch.float16))
 
     def _gate_up_il(self, layer: int) -> torch.Tensor:
+        """Layer `layer`'s gate/up weight in the interleaved layout rg_linear_silu_mul reads: the
+        weight itself once interleaved in place, else a copy kept beside it."""
+        L = self.w.layers[layer]
+        if L.gate_up_interleaved:
+            return L.w_gate_up
         w_il = self._w_gate_up_il.get(layer)
         if w_il is None:
-            w_il = self._w_gate_up_il[layer] = interleave_gate_up(self.w.layers[layer].w_gate_up)
+            w_il = self._w_gate_up_il[layer] = interleave_gate_up(L.w_gate_up)
         return w_il
+
+    def _fixed(self) -> Optional[bool]:
+        """The form a fixed choice mode takes (True: hand-written / fused / folded), None when
+        the choices are measured."""
+        return None if self.choice_mode == "measured" else self.choice_mode == "rg"
+
+    def choices(self) -> dict:
+        """The choices made so far, by kind and shape (for logs and reproducing a run)."""
+        return {"mode": self.choice_mode,
+                "linear": {f"{r}x{n}x{k}": "rg_linear" if v else "hipblaslt"
+                           for (r, n, k), v in self.linear_choice.items()},
+                "mlp_fused": dict(self.mlp_choice), "qkv_fused": dict(self.qkv_choice),
+                "norms_folded": dict(self.norm_chain)}
 
     def _use_norm_chain(self, st: DeviceStep) -> tuple:
         """Which RmsNorms of this step's layers are folded into the projection after them, as
@@ -385,7 +445,9 @@ class RailgunLlama:
         use = self.norm_chain.get(rows)
         if use is not None:
             return (use, use) if isinstance(use, bool) else use
-        if torch.cuda.is_current_stream_capturing():
+        if self._fixed() is not None:
+            use = (self._fixed(), self._fixed())
+        elif torch.cuda.is_current_stream_capturing():
             use = (True, True)
         else:
             H, D, eps = cfg.num_attention_heads, cfg.head_dim, cfg.rms_norm_eps
@@ -424,6 +486,8 @@ class RailgunLlama:
             t_af, t_au = self._time_pair(attn_folded, attn_unfolded, n)
             t_mf, t_mu = self._time_pair(mlp_folded, mlp_unfolded, n)
             use = (not t_au < 0.95 * t_af, not t_mu < 0.95 * t_mf)
+            log.info("RmsNorm folds at %d rows: input norm %.2f / %.2f us, post-attention norm %.2f / %.2f us "
+                     "(folded / separate) -> %s", rows, t_af, t_au, t_mf, t_mu, use)
         self.norm_chain[rows] = use
         return use
 

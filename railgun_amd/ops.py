@@ -272,6 +272,20 @@ class PagedAttentionKernels:
             raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "x must be [T, K] with unit column stride, weight_qkv "
                                                              "and q_out contiguous, one dtype")
         tokens, k = (int(d) for d in x.shape)
+        # The entry derives N = (H + 2 H_kv) D from the head counts and reads that many weight
+        # rows, writes T H D values of q and reads the cos/sin rows at head_dim floats each.
+        n = (num_heads + 2 * num_kv_heads) * head_dim
+        if weight_qkv.dim() != 2 or tuple(weight_qkv.shape) != (n, k):
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT,
+                               f"weight_qkv must be [(H + 2 H_kv) D, K] = [{n}, {k}], got {tuple(weight_qkv.shape)}")
+        if q_out.numel() < tokens * num_heads * head_dim or q_out.dtype != x.dtype:
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT,
+                               f"q_out must hold [T, H, D] = [{tokens}, {num_heads}, {head_dim}] of x's dtype")
+        if cos_sin.dim() != 2 or int(cos_sin.shape[1]) != head_dim or cos_sin.dtype != torch.float32:
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT,
+                               f"cos_sin must be a float32 [max_position, head_dim = {head_dim}] table")
+        if int(positions.numel()) < tokens or int(slot_mapping.numel()) < tokens:
+            raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "positions and slot_mapping need one entry per token")
         if norm_weight is not None:
             _require_cuda(norm_weight)
             if tuple(norm_weight.shape) != (k,) or not norm_weight.is_contiguous() or norm_weight.dtype != x.dtype:
@@ -500,6 +514,18 @@ def interleave_gate_up(w_gate_up: torch.Tensor) -> torch.Tensor:
     return w_gate_up.view(2, two_i // 32, 16, k).transpose(0, 1).contiguous().view(two_i, k)
 
 
+def deinterleave_gate_up(y: torch.Tensor) -> torch.Tensor:
+    """The inverse permutation of interleave_gate_up along the last dimension: [..., 2 I] with
+    gate and up columns interleaved in blocks of 16 -> gate columns, then up columns (a copy).
+    Applied to x @ weight_il^T it gives x @ w_gate_up^T; to weight_il itself, w_gate_up."""
+    two_i = int(y.shape[-1])
+    if two_i % 32 != 0:
+        raise RailgunError(_lib.RG_ERR_NOT_SUPPORTED, "deinterleave_gate_up: intermediate size must be a multiple "
+                                                      "of 16")
+    lead = tuple(y.shape[:-1])
+    return y.reshape(*lead, two_i // 32, 2, 16).transpose(-3, -2).reshape(*lead, two_i).contiguous()
+
+
 def linear_silu_mul(x: torch.Tensor, weight_il: torch.Tensor, out: Optional[torch.Tensor] = None,
                     norm_weight: Optional[torch.Tensor] = None, eps: float = 0.0) -> torch.Tensor:
     """out [rows, I] = silu(x @ gate^T) * (x @ up^T), each step rounded as rg_linear followed by
@@ -560,6 +586,6 @@ def linear_residual(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tenso
 
 
 __all__ = ["LINEAR_MAX_ROWS", "PagedAttentionKernels", "PagedAttentionOp", "RailgunError", "cache_geometry",
-           "dtype_code", "interleave_gate_up", "linear", "linear_residual", "linear_silu_mul", "linear_workspace_bytes",
-           "rms_norm", "rope_cos_sin_table", "silu_and_mul", "V1_MAX_CONTEXT",
-           "V2_PARTITION_SIZE"]
+           "deinterleave_gate_up", "dtype_code", "interleave_gate_up", "linear", "linear_residual",
+           "linear_silu_mul", "linear_workspace_bytes", "rms_norm", "rope_cos_sin_table", "silu_and_mul",
+           "V1_MAX_CONTEXT", "V2_PARTITION_SIZE"]

@@ -246,13 +246,13 @@ def test_generic_path_shapes(device, kernels, dt, D, bs, G):
     assert_close(gpu_v2(kernels, inp, 2 * bs), want, dt, "v2")
 
 
-@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("bs", [32, 64, 128, 256])
 @pytest.mark.parametrize("dt,D,G", [("bf16", 128, 4), ("f16", 64, 8), ("f32", 128, 4), ("bf16", 64, 1)])
 def test_mfma_path_block_sizes(device, kernels, dt, D, G, bs):
     """Block sizes 16 << j on the MFMA grid and stream-K kernels, which work in 16-token
-    sub-blocks of each block: ragged contexts (0, 1, sub-block and block boundaries), v1
-    without a workspace (grid kernel; generic for fp32), with one (stream-K), v2 with P = 2 bs,
-    and the fused pool layout."""
+    sub-blocks of each block (256 = 16 << 4, the largest shift they take): ragged contexts (0,
+    1, sub-block and block boundaries), v1 without a workspace (grid kernel; generic for fp32),
+    with one (stream-K), v2 with P = 2 bs, and the fused pool layout."""
     Hkv = 2
     for fused in (False, True):
         inp = make_inputs(device, CTX_RAGGED + [bs - 1, bs, bs + 1, 3 * bs + 16], dt, H=Hkv * G, Hkv=Hkv, D=D,
@@ -289,15 +289,16 @@ def test_stream_head_dim256_many_units(device, kernels):
     assert_close(gpu_v1(kernels, inp, True), want, "bf16", "D=256")
 
 
-@pytest.mark.parametrize("bs", [32, 64])
+@pytest.mark.parametrize("bs", [32, 64, 256])
 def test_stream_block_sizes_many_units(device, kernels, bs):
-    """Stream-K with 32- and 64-token blocks at a config-5-like load (128 sequences, contexts
-    U[64, 8192], 32 / 8 heads, head_dim 64, bf16): many units per worker, segments crossed mid
-    range, block-table window refills, each window entry a (block, sub-block) pair."""
+    """Stream-K with 32-, 64- and 256-token blocks at a config-5-like load (128 sequences,
+    contexts U[64, 8192], 32 / 8 heads, head_dim 64, bf16): many units per worker, segments
+    crossed mid range, block-table window refills, each window entry a (block, sub-block) pair
+    (at 256, sixteen sub-blocks per block: the largest shift of the packing)."""
     rng = np.random.default_rng(700 + bs)
     ctx = rng.integers(64, 8192, 128, endpoint=True).astype(np.int32)
     inp = _big_decode_inputs(device, ctx, "bf16", 32, 8, 64, seed=700 + bs, mb=8192 // bs, bs=bs)
-    assert _stream_units(ctx, 8, 4) > 64 * _stream_workers(device)
+    assert _stream_units(ctx, 8, 4) > 48 * _stream_workers(device)
     want = orc.cpu_attention_gathered(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"], "bf16",
                                       nthreads=_threads())
     assert_close(gpu_v1(kernels, inp, True), want, "bf16", f"bs={bs}")
@@ -378,6 +379,42 @@ def test_config2_full_decode(device, kernels):
     assert_close(gpu_v1(kernels, inp, True), want, "bf16", "v1 split")
     assert_close(gpu_v1(kernels, inp, False), want, "bf16", "v1 single")
     assert_close(gpu_v2(kernels, inp, 512), want, "bf16", "v2 P=512")
+
+
+def test_config2_step_chain(device, kernels):
+    """The bench's timed config-2 step end to end at full size (64 sequences, contexts U[512,
+    4096], bf16, 32/8, D 128, block 16): rg_rope_reshape_and_cache of the 64 new tokens (RoPE
+    theta 5e5 at position ctx - 1, the decode convention of scheduler.rs:258-263, written at
+    their slots), then rg_paged_attention_v1 with its workspace over the updated pool.  The
+    oracle runs the same chain: its rope_reshape_and_cache, then the reference CPU path over
+    the gathered blocks.  Rotated q and both whole caches bit-exact; attention within the bf16
+    tolerance (each sequence's last key is the token just written)."""
+    from railgun_amd.ops import rope_cos_sin_table
+
+    w = wl.config2()
+    B, H, hkv, D, bs = w.batch, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
+    rng = np.random.default_rng(w.seed + 7)
+    shape = (w.num_blocks, hkv, bs, D)
+    kc, vc = normal(rng, shape, "bf16"), normal(rng, shape, "bf16")
+    q, k, v = normal(rng, (B, H, D), "bf16"), normal(rng, (B, hkv, D), "bf16"), normal(rng, (B, hkv, D), "bf16")
+    pos, slots = w.positions, w.slot_mapping
+    assert np.array_equal(pos, w.context_lens - 1)
+    table = rope_cos_sin_table(int(w.context_lens.max()), D, w.rope_theta)
+    dq, dkc, dvc = to_dev(q, "bf16", device), to_dev(kc, "bf16", device), to_dev(vc, "bf16", device)
+    kernels.launch_rope_reshape_and_cache(dq, to_dev(k, "bf16", device), to_dev(v, "bf16", device), dkc, dvc,
+                                          table.to(device), i32(pos, device), i32(slots, device), H, hkv, D, bs, B)
+    out = torch.full_like(dq, float("nan"))
+    ws = torch.empty(max(kernels.v1_workspace_bytes(B, H, hkv, D, bs, w.max_blocks), 1), dtype=torch.uint8,
+                     device=device)
+    kernels.launch_v1(dq, dkc, dvc, i32(w.block_table, device), i32(w.context_lens, device), out, w.scale, H, hkv,
+                      D, bs, w.max_blocks, B, workspace=ws)
+    torch.cuda.synchronize()
+    orc.rope_reshape_and_cache(q, k, v, kc, vc, table.numpy(), pos, slots, "bf16", bs)
+    np.testing.assert_array_equal(from_dev(dq, "bf16"), q, err_msg="rotated q")
+    np.testing.assert_array_equal(from_dev(dkc, "bf16"), kc, err_msg="key cache after the step's write")
+    np.testing.assert_array_equal(from_dev(dvc, "bf16"), vc, err_msg="value cache after the step's write")
+    want = orc.cpu_attention_gathered(q, kc, vc, w.block_table, w.context_lens, w.scale, "bf16", nthreads=_threads())
+    assert_close(dev_f32(out), want, "bf16", "config-2 step: RoPE + cache write, then v1")
 
 
 def test_config3_v2_matches_v1(device, kernels):

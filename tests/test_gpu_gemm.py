@@ -253,6 +253,22 @@ def test_linear_qkv_rope_refuses_unsupported(device, kernels):
     with pytest.raises(RailgunError) as e:
         kernels.launch_linear_qkv_rope_reshape_and_cache(x, w, q, pool[:, 0], pool[:, 1], cs, i, i, 2, 1, 128, 16)
     assert e.value.code == _lib.RG_ERR_NOT_SUPPORTED
+    # Shapes that disagree with the head counts are refused on the host before any launch: the
+    # entry would read (H + 2 H_kv) D weight rows and write T H D values of q.
+    x = torch.zeros(4, 256, dtype=torch.bfloat16, device=device)
+    q = torch.empty(4, 2, 64, dtype=torch.bfloat16, device=device)
+    pool = torch.zeros(4, 2, 1, 16, 64, dtype=torch.bfloat16, device=device)
+    cs = torch.zeros(16, 64, dtype=torch.float32, device=device)
+    good_w = torch.zeros(4 * 64, 256, dtype=torch.bfloat16, device=device)
+    bad = [dict(w=torch.zeros(3 * 64, 256, dtype=torch.bfloat16, device=device)),   # too few weight rows
+           dict(w=torch.zeros(4 * 64, 384, dtype=torch.bfloat16, device=device)),   # K of the weight != x's
+           dict(q=torch.empty(4, 1, 64, dtype=torch.bfloat16, device=device)),       # q_out too small
+           dict(cs=torch.zeros(16, 32, dtype=torch.float32, device=device))]         # cos/sin rows too narrow
+    for case in bad:
+        with pytest.raises(RailgunError) as e:
+            kernels.launch_linear_qkv_rope_reshape_and_cache(x, case.get("w", good_w), case.get("q", q), pool[:, 0],
+                                                             pool[:, 1], case.get("cs", cs), i, i, 2, 1, 64, 16)
+        assert e.value.code == _lib.RG_ERR_INVALID_ARGUMENT, case
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
@@ -377,6 +393,71 @@ def test_rms_norm_linear_qkv_rope_reshape_and_cache(device, kernels, T, H, Hkv, 
     vb = 2 * (dpre[tok, H + Hkv:] + e * vref.abs()) + 1e-5
     assert bool(((flat[sl[tok], 0] - kref).abs() <= kb).all()), "k cache"
     assert bool(((flat[sl[tok], 1] - vref).abs() <= vb).all()), "v cache"
+
+
+@pytest.mark.parametrize("M", [1, 4, 128])
+def test_rms_norm_linear_fp16_residual_range(device, kernels, M):
+    """fp16 residual rows far from 1 in size, through both folded norms: |x| up to 3e4 with
+    norm weights up to 3 (x * w_norm past fp16's 65504 if it were rounded before the division
+    by rms(x), which the unfused chain does first) and |x| around 1e-4 (x * w_norm in fp16's
+    subnormals).  The outputs are finite and within the fp32 chain's bound of one rounding of
+    every W * w_norm product, of the projection and of the outputs."""
+    from railgun_amd.ops import interleave_gate_up, linear_silu_mul, rope_cos_sin_table
+    t = torch.float16
+    g = torch.Generator().manual_seed(77 + M)
+    K, I = 2048, 512
+    mags = torch.tensor([3e4, 1e-4, 1.0, 2e4])[torch.arange(M) % 4]
+    x = (mags[:, None] * torch.randn(M, K, generator=g).clamp(-2, 2)).to(t)
+    nw = (1 + 2 * torch.rand(K, generator=g)).to(t)
+    assert float((x.float() * nw.float()).abs().max()) > 65504 and bool(torch.isfinite(x.float()).all())
+    w = (0.05 * torch.randn(2 * I, K, generator=g)).to(t)
+    x, nw, w = x.to(device), nw.to(device), w.to(device)
+    eps = 1e-5
+    e = 2 ** -11
+    h, rs = _norm_ref(x, nw, eps)
+    wf = w.float().cpu()
+    absx = (x.float().cpu() * nw.float().cpu()).abs()
+
+    got = linear_silu_mul(x, interleave_gate_up(w), norm_weight=nw, eps=eps).float().cpu()
+    gv, uv = h @ wf[:I].T, h @ wf[I:].T
+    dg = e * rs * (absx @ wf[:I].abs().T) + e * gv.abs()
+    du = e * rs * (absx @ wf[I:].abs().T) + e * uv.abs()
+    sig = torch.sigmoid(gv)
+    act, ref = gv * sig, gv * sig * uv
+    dsilu = (sig * (1 + gv * (1 - sig))).abs()
+    bound = 2 * (dsilu * dg * uv.abs() + act.abs() * du + 2 * e * ref.abs()) + 1e-3 * ref.abs().mean() + 1e-6
+    assert bool(torch.isfinite(got).all()), "gate/up: non-finite output"
+    assert bool(((got - ref).abs() <= bound).all()), f"gate/up: max excess {float(((got - ref).abs() - bound).max()):.3g}"
+
+    H, Hkv, D, bs = 8, 2, 64, 16
+    wq = (0.05 * torch.randn((H + 2 * Hkv) * D, K, generator=g)).to(t).to(device)
+    nb = M // bs + 4
+    pos = torch.arange(M, dtype=torch.int32, device=device)
+    slots = torch.arange(M, dtype=torch.int32, device=device)
+    cs = rope_cos_sin_table(max(M, 2), D, 500000.0, device)
+    pool = torch.zeros(nb, 2, Hkv, bs, D, dtype=t, device=device)
+    q = torch.empty(M, H, D, dtype=t, device=device)
+    kernels.launch_linear_qkv_rope_reshape_and_cache(x, wq, q, pool[:, 0], pool[:, 1], cs, pos, slots, H, Hkv, D, bs,
+                                                     norm_weight=nw, eps=eps)
+    torch.cuda.synchronize()
+    wqf = wq.float().cpu()
+    pre = (h @ wqf.T).view(M, H + 2 * Hkv, D)
+    dpre = (e * rs * (absx @ wqf.abs().T)).view(M, H + 2 * Hkv, D) + e * pre.abs()
+    half = D // 2
+    csc = cs.cpu()[pos.cpu().long()]
+    c, s = csc[:, :half][:, None, :], csc[:, half:][:, None, :]
+    lo, hi = pre[..., :half], pre[..., half:]
+    rot = torch.cat([lo * c - hi * s, hi * c + lo * s], -1)
+    dl, dh = dpre[..., :half], dpre[..., half:]
+    drot = torch.cat([dl * c.abs() + dh * s.abs(), dh * c.abs() + dl * s.abs()], -1)
+    qb = 2 * (drot + e * rot.abs()) + 1e-5
+    got_q = q.float().cpu()
+    assert bool(torch.isfinite(got_q).all()), "q: non-finite output"
+    assert bool(((got_q - rot[:, :H]).abs() <= qb[:, :H]).all()), \
+        f"q: max excess {float(((got_q - rot[:, :H]).abs() - qb[:, :H]).max()):.3g}"
+    flat = pool.float().cpu().permute(0, 3, 1, 2, 4).reshape(nb * bs, 2, Hkv, D)[:M]
+    assert bool(torch.isfinite(flat).all()), "cache: non-finite rows"
+    assert bool(((flat[:, 0] - rot[:, H:H + Hkv]).abs() <= qb[:, H:H + Hkv]).all()), "k cache"
 
 
 def test_rms_norm_linear_refuses_unsupported(device, kernels):

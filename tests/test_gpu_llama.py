@@ -24,7 +24,7 @@ from oracle import llama_ref
 from railgun_amd.batch import DecodeSlot, PrefillChunk, pack_step
 from railgun_amd.kv_pool import GpuBlockPool
 from railgun_amd.llama import DeviceStep, LlamaConfig, LlamaWeights, RailgunLlama
-from railgun_amd.ops import rms_norm, rope_cos_sin_table, silu_and_mul
+from railgun_amd.ops import deinterleave_gate_up, rms_norm, rope_cos_sin_table, silu_and_mul
 
 pytestmark = pytest.mark.gpu
 transformers = pytest.importorskip("transformers")
@@ -166,7 +166,8 @@ class _Fixed(dict):
         return self.value
 
 
-@pytest.mark.parametrize("gemm", ["measured", "rg_linear", "norm_chain", "fold_attn_only", "fold_mlp_only"])
+@pytest.mark.parametrize("gemm", ["measured", "rg_linear", "norm_chain", "fold_attn_only", "fold_mlp_only",
+                                  "choices_rg", "choices_blas"])
 @pytest.mark.parametrize("name", list(CONFIGS))
 def test_llama_prefill_decode_mixed(device, kernels, name, gemm):
     """Prefill, mixed and decode steps against the CPU model.  With gemm="rg_linear" every
@@ -175,7 +176,9 @@ def test_llama_prefill_decode_mixed(device, kernels, name, gemm):
     fused (rg_linear_qkv_rope_reshape_and_cache); "norm_chain" also folds the RmsNorms into those
     projections and the residual adds into o_proj / down_proj (rg_rms_norm_linear_*,
     rg_linear_residual), "fold_attn_only" / "fold_mlp_only" one side of it; "measured" keeps the
-    per-shape timing choice of normal use."""
+    per-shape timing choice of normal use.  "choices_rg" / "choices_blas" are the constructor's
+    fixed modes (every hand-written, fused and folded form; hipBLASLt and separate launches with
+    the gate/up weight left stacked)."""
     _mixed_steps(device, kernels, CONFIGS[name], gemm, torch.bfloat16)
 
 
@@ -193,8 +196,10 @@ def _mixed_steps(device, kernels, cfg, gemm, dtype):
         sd = {k: v.to(dtype).float() for k, v in sd.items()}
     w = LlamaWeights.from_state_dict(cfg, sd, device, dtype=dtype)
     pool = GpuBlockPool.for_model(cfg, nb, bs, device, dtype=dtype)
-    model = RailgunLlama(cfg, w, pool, kernels, max_position=4096)
-    if gemm != "measured":
+    mode = {"choices_rg": "rg", "choices_blas": "blas"}.get(gemm)
+    model = RailgunLlama(cfg, w, pool, kernels, max_position=4096, choices=mode)
+    assert w.layers[0].gate_up_interleaved == (mode != "blas")
+    if gemm not in ("measured", "choices_rg", "choices_blas"):
         model.linear_choice = _AlwaysRgLinear()
         model.mlp_choice = _AlwaysRgLinear()
         model.qkv_choice = _AlwaysRgLinear()
@@ -221,6 +226,13 @@ def _mixed_steps(device, kernels, cfg, gemm, dtype):
     # step 3: decode only, every sequence one token further
     ext = [rng.integers(0, cfg.vocab_size) for _ in lens]
     run(pack_step([], [DecodeSlot(int(t), n + 1, bt) for t, n, bt in zip(ext, lens, bts)], bs), "decode")
+    if mode is not None:
+        made = model.choices()
+        assert made["mode"] == mode
+        want = mode == "rg"
+        assert all(v == ("rg_linear" if want else "hipblaslt") for v in made["linear"].values())
+        assert all(v == want for v in made["mlp_fused"].values()) and all(v == want for v in made["qkv_fused"].values())
+        assert all(v == (want, want) for v in made["norms_folded"].values())
 
 
 def _hf_state_of(cfg: LlamaConfig, w: LlamaWeights) -> dict:
@@ -231,7 +243,9 @@ def _hf_state_of(cfg: LlamaConfig, w: LlamaWeights) -> dict:
     sd = {"model.embed_tokens.weight": f(w.embed), "model.norm.weight": f(w.norm)}
     for i, L in enumerate(w.layers):
         p = f"model.layers.{i}."
-        qkv, gu = f(L.wqkv), f(L.w_gate_up)
+        qkv = f(L.wqkv)
+        # (the interleave permutes the weight's rows: de-interleave along dim 0)
+        gu = f(deinterleave_gate_up(L.w_gate_up.t()).t() if L.gate_up_interleaved else L.w_gate_up)
         sd[p + "self_attn.q_proj.weight"] = qkv[:H * D]
         sd[p + "self_attn.k_proj.weight"] = qkv[H * D:(H + Hkv) * D]
         sd[p + "self_attn.v_proj.weight"] = qkv[(H + Hkv) * D:]

@@ -222,3 +222,21 @@ def test_interleave_gate_up_layout():
     for j in range(inter // 16):
         assert torch.equal(il[32 * j:32 * j + 16], w[16 * j:16 * j + 16])
         assert torch.equal(il[32 * j + 16:32 * j + 32], w[inter + 16 * j:inter + 16 * j + 16])
+
+
+def test_deinterleave_gate_up_inverts_the_layout():
+    """deinterleave_gate_up undoes interleave_gate_up on the weight rows, and on the columns of
+    a product: x @ interleaved^T, de-interleaved, is x @ w_gate_up^T exactly (a permutation of
+    the same sums), which is what the model's separate MLP form relies on once the weight is
+    held interleaved."""
+    import torch
+
+    from railgun_amd.ops import deinterleave_gate_up, interleave_gate_up
+    g = torch.Generator().manual_seed(3)
+    inter, k, rows = 64, 32, 5
+    w = torch.randn(2 * inter, k, generator=g)
+    il = interleave_gate_up(w)
+    assert not torch.equal(il, w)
+    assert torch.equal(deinterleave_gate_up(il.t()).t(), w)
+    x = torch.randn(rows, k, generator=g)
+    assert torch.equal(deinterleave_gate_up(x @ il.t()), x @ w.t())

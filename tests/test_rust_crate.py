@@ -172,3 +172,49 @@ def test_every_ffi_entry_is_called_by_the_crate():
     body = open(os.path.join(CRATE, "kernels.rs")).read() + open(os.path.join(CRATE, "op.rs")).read()
     for name in header_prototypes():
         assert f"ffi::{name}(" in body, f"no wrapper calls {name}"
+
+
+def _fn_body(path: str, name: str) -> str:
+    """The text of `pub fn name` in a Rust source file, up to the next `pub fn` or the file's end."""
+    text = open(path).read()
+    m = re.search(rf"pub (?:unsafe )?fn {name}\b", text)
+    assert m, f"{name} not found in {path}"
+    nxt = re.search(r"\n    pub (?:unsafe )?fn ", text[m.end():])
+    return text[m.start():m.end() + (nxt.start() if nxt else len(text))]
+
+
+# Calls that stall the host or allocate device scratch on every call.
+_STALLS = ("hipStreamSynchronize", "hipDeviceSynchronize", "hipEventSynchronize", "hipMalloc", "hipFree",
+           "HipSlice::<u8>::alloc")
+
+
+def test_execute_neither_synchronises_nor_allocates_scratch(tmp_path):
+    """PagedAttentionOp::execute queues its launches and returns: the split-K scratch is the
+    kernels' grow-only workspace (with_workspace), never a per-call allocation freed after a
+    stream synchronisation.  The check is shown to see a synchronize planted in the body."""
+    op_rs = os.path.join(CRATE, "op.rs")
+    body = _fn_body(op_rs, "execute")
+    for call in _STALLS:
+        assert call not in body, f"execute calls {call}"
+    assert body.count("with_workspace(") == 2, "both branches (v1+, v2) take the shared workspace"
+    planted = tmp_path / "op.rs"
+    planted.write_text(open(op_rs).read().replace("        Ok(out)\n",
+                                                  "        crate::hip::hipStreamSynchronize(k.stream());\n"
+                                                  "        Ok(out)\n", 1))
+    assert any(call in _fn_body(str(planted), "execute") for call in _STALLS)
+    # The workspace lives in the kernels object, which one Arc shares across layers
+    # (vllm-models model.rs:127), grows only when a call needs more, and is never freed by execute.
+    grow = _fn_body(os.path.join(CRATE, "kernels.rs"), "with_workspace")
+    assert "w.len() < bytes" in grow and "HipSlice::<u8>::alloc" in grow
+
+
+def test_op_fields_match_the_reference_struct():
+    """The op keeps exactly the reference's public fields (paged_attn_op.rs:12-19), so the
+    struct literal of its call site (vllm-models attention.rs:109-116) builds it unchanged."""
+    text = open(os.path.join(CRATE, "op.rs")).read()
+    m = re.search(r"pub struct PagedAttentionOp \{(.*?)\n\}", text, re.S)
+    assert m
+    fields = re.findall(r"^\s*(pub\s+)?([a-z_]+):", m.group(1), re.M)
+    assert [(bool(p), n) for p, n in fields] == [(True, n) for n in
+                                                 ("scale", "num_heads", "num_kv_heads", "head_dim", "block_size",
+                                                  "kernels")]

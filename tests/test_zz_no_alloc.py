@@ -97,3 +97,35 @@ def test_no_alloc_refuses_shapes_beyond_the_scratch(device, kernels):
     assert st == _lib.RG_ERR_WORKSPACE
     assert b"static scratch" in lib.rg_last_error()
     assert bool((out == 7.0).all())
+
+
+def test_no_alloc_under_graph_capture(device, kernels):
+    """The entry under HIP graph capture, as its header allows: captured once (torch's capture
+    stream) and replayed four times, with eager work between the replays — a call of the same
+    entry on other inputs, which rewrites the shared static scratch, and, before the third
+    replay, a new q written into the captured input buffer.  Every replay is bit-equal to the
+    eager call on the inputs the buffers then hold (the graph records only the two kernel
+    launches: no allocation, no memset)."""
+    lib = kernels.lib
+    inp = _inputs(device, wl.config2().context_lens[:32], 32, 8, 128, seed=73)
+    other = _inputs(device, [5, 900, 3000], 32, 8, 64, seed=74)
+    want = _no_alloc(lib, inp)
+    torch.cuda.synchronize()
+    out = torch.full_like(inp["q"], float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = lib.rg_paged_attention_v1_no_alloc(*_args(inp, out), torch.cuda.current_stream().cuda_stream)
+    assert st == _lib.RG_OK, lib.rg_last_error()
+    torch.cuda.synchronize()
+    g = torch.Generator(device=device)
+    g.manual_seed(75)
+    for i in range(4):
+        _no_alloc(lib, other)
+        if i == 2:
+            inp["q"].copy_(torch.randn(inp["q"].shape, generator=g, device=device).to(torch.bfloat16))
+            want = _no_alloc(lib, inp)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {i}"
