@@ -245,10 +245,11 @@ def side_v2(device, gen, steps: int) -> dict:
                                "frac_hbm_peak": round(gbs_pair / HBM_PEAK_GBS, 4)}}
 
 
-def side_fp32(device, gen, steps: int) -> dict:
+def side_fp32(device, gen, steps: int, num_heads: int = 32) -> dict:
     """Config 2's decode (64 sequences, contexts U[512, 4096], 32 / 8 heads, head_dim 128) in fp32,
     the reference launchers' element type: paged attention v1 with its workspace (the fp32
-    stream-K tile), K calls back to back.  Algorithmic bytes as for bf16, at 4 bytes per element."""
+    stream-K tile), K calls back to back.  Algorithmic bytes as for bf16, at 4 bytes per element.
+    With num_heads 24 instead: the same load in bf16 at Llama-3.2-3B's heads (24 / 8, GQA 3)."""
     import dataclasses
 
     import torch
@@ -256,12 +257,13 @@ def side_fp32(device, gen, steps: int) -> dict:
     from railgun_amd import workloads as wl
     from railgun_amd.ops import PagedAttentionKernels
 
-    w = dataclasses.replace(wl.config2(), dtype="f32")
+    dt = torch.float32 if num_heads == 32 else torch.bfloat16
+    w = dataclasses.replace(wl.config2(), dtype="f32" if dt == torch.float32 else "bf16", num_heads=num_heads)
     kernels = PagedAttentionKernels(0)
     shape = (w.num_blocks, w.num_kv_heads, w.block_size, w.head_dim)
-    kc = torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
-    vc = torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
-    q = torch.randn((w.batch, w.num_heads, w.head_dim), generator=gen, device=device, dtype=torch.float32)
+    kc = torch.randn(shape, generator=gen, device=device, dtype=torch.float32).to(dt)
+    vc = torch.randn(shape, generator=gen, device=device, dtype=torch.float32).to(dt)
+    q = torch.randn((w.batch, w.num_heads, w.head_dim), generator=gen, device=device, dtype=torch.float32).to(dt)
     out = torch.empty_like(q)
     bt, ctx = torch.from_numpy(w.block_table).to(device), torch.from_numpy(w.context_lens).to(device)
     nbytes = kernels.v1_workspace_bytes(w.batch, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size, w.max_blocks)
@@ -275,20 +277,28 @@ def side_fp32(device, gen, steps: int) -> dict:
     gbs = w.decode_bytes() / (ms * 1e-3) / 1e9
     del kc, vc, ws
     torch.cuda.empty_cache()
+    if dt == torch.bfloat16:
+        return {"workload": f"config2_load_bf16_decode_{num_heads}q_{w.num_kv_heads}kv",
+                "kernel": f"paged_attention_v1 (stream-K + merge, GQA {num_heads // w.num_kv_heads})",
+                "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                "bytes": w.decode_bytes()}
     return {"workload": "config2_shape_fp32_decode", "kernel": "paged_attention_v1 (fp32 stream-K + merge)",
             "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "bytes": w.decode_bytes()}
 
 
-def side_prefill(device, gen, steps: int, fp32: bool = False) -> dict:
+def side_prefill(device, gen, steps: int, fp32: bool = False, num_heads: int = 32) -> dict:
     """Config 4's packed causal prefill (bf16; with fp32 the same shapes in the reference's
-    element type, on the fp32 MFMA kernel, against the 157.3 TFLOP/s dense fp32 MFMA peak)."""
+    element type, on the fp32 MFMA kernel, against the 157.3 TFLOP/s dense fp32 MFMA peak; with
+    num_heads 24 the bf16 shapes at Llama-3.2-3B's heads, 24 / 8)."""
+    import dataclasses
+
     import torch
 
     from railgun_amd import workloads as wl
     from railgun_amd.ops import PagedAttentionKernels, PagedAttentionOp, rope_cos_sin_table
 
-    w = wl.config4()
+    w = dataclasses.replace(wl.config4(), num_heads=num_heads)
     kernels = PagedAttentionKernels(0)
     op = PagedAttentionOp(w.scale, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size, kernels)
     T = w.num_tokens
@@ -316,6 +326,10 @@ def side_prefill(device, gen, steps: int, fp32: bool = False) -> dict:
         return {"workload": "config4_shape_fp32_packed_prefill", "kernel": "prefill_f32_kernel "
                 "(v_mfma_f32_32x32x2_f32)", "tokens": T, "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 2),
                 "frac_fp32_mfma_peak": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4), "flops": w.causal_flops()}
+    if num_heads != 32:
+        return {"workload": f"config4_shape_bf16_prefill_{num_heads}q_{w.num_kv_heads}kv", "tokens": T,
+                "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 2),
+                "frac_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops": w.causal_flops()}
     return {"workload": w.name, "tokens": T, "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 2),
             "frac_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops": w.causal_flops(),
             "traffic": measured_traffic("prefill_config4")}
@@ -577,6 +591,9 @@ def main() -> int:
         result["prefill"] = side_prefill(device, gen, 10)
         log("[bench] config4 prefill in fp32 ...")
         result["fp32_prefill"] = side_prefill(device, gen, 3, fp32=True)
+        log("[bench] GQA 3 (24 / 8 heads): config 2 decode load, config 4 prefill ...")
+        result["gqa3"] = {"decode": side_fp32(device, gen, max(3, args.steps // 5), num_heads=24),
+                          "prefill": side_prefill(device, gen, 10, num_heads=24)}
         log("[bench] config5 model step ...")
         result["model_step"] = side_model(device, 10)
         log("[bench] config5 projections ...")

@@ -304,8 +304,11 @@ struct DecodeTile {
   static constexpr int ROWV = D / 8;        // 16-byte vectors per token row
   static constexpr int TPI = 64 / ROWV;     // tokens covered by one V load instruction
   static constexpr int NV = kBS / TPI;      // V loads per block
-  static constexpr int GP = G < 4 ? 4 : G;  // padded heads per LDS row
-  static constexpr int HG = (G + 3) / 4;    // MFMA output rows holding distinct heads
+  static constexpr int HG = (G + 3) / 4;    // MFMA output row groups (4 rows each) holding distinct heads
+  // Heads per LDS row, padded to whole row groups: the softmax writes 4 rows per group, so for
+  // G not a multiple of 4 (3, 5, 6, 7) the last group's rows past G (copies of heads m % G)
+  // land in padding instead of the next token's row.
+  static constexpr int GP = 4 * HG;
   static constexpr int ACC = 8;             // output dims per lane and head (acc[h][0..ACC))
 
   int col, seg, vrow, vd0;
@@ -447,8 +450,8 @@ struct DecodeTileF32 {
   static constexpr int ROWV = D / 4;        // 16-byte vectors per token row
   static constexpr int TPI = 64 / ROWV;     // tokens covered by one V load instruction
   static constexpr int NV = kBS / TPI;      // V loads per block
-  static constexpr int GP = G < 4 ? 4 : G;
   static constexpr int HG = (G + 3) / 4;
+  static constexpr int GP = 4 * HG;  // as DecodeTile
   static constexpr int ACC = 4;
   static_assert(NK >= 1 && TPI >= 1 && NV >= 1, "head_dim 64 or 128");
 
@@ -1289,6 +1292,18 @@ bool launch_mfma_g(const DecodeArgs& a, int G, dim3 grid, hipStream_t s) {
     case 2: launch_mfma<T, D, 2>(a, grid, s); return true;
     case 4: launch_mfma<T, D, 4>(a, grid, s); return true;
     case 8: launch_mfma<T, D, 8>(a, grid, s); return true;
+    case 3:
+    case 5:
+    case 6:
+    case 7:
+      if constexpr (D <= 128) {
+        if (G == 3) launch_mfma<T, D, 3>(a, grid, s);
+        else if (G == 5) launch_mfma<T, D, 5>(a, grid, s);
+        else if (G == 6) launch_mfma<T, D, 6>(a, grid, s);
+        else launch_mfma<T, D, 7>(a, grid, s);
+        return true;
+      }
+      return false;
     case 16:
       if constexpr (D < 256) {
         launch_mfma<T, D, 16>(a, grid, s);
@@ -1299,12 +1314,21 @@ bool launch_mfma_g(const DecodeArgs& a, int G, dim3 grid, hipStream_t s) {
   }
 }
 
+// GQA ratios of the MFMA tiles: the q-heads of a kv-head are replicated over the 16 rows of the
+// A operand (row m holds head m % G), so any G up to 16 has its heads in the first G rows; the
+// powers of two at every head_dim, G = 3, 5, 6 and 7 (Llama-3.2-3B 24/8, Qwen2.5-14B 40/8,
+// Qwen2-7B 28/4, ...) at head_dim 64 and 128.
+bool mfma_group_size(int G, int head_dim) {
+  return G == 1 || G == 2 || G == 4 || G == 8 || G == 16 ||
+         ((G == 3 || G == 5 || G == 6 || G == 7) && head_dim <= 128);
+}
+
 bool mfma_applies(const DecodeArgs& a, int32_t dtype) {
   const int G = a.num_heads / a.num_kv_heads;
   const int eb = dtype_bytes(dtype);
   return (dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && a.bs_shift >= 0 &&
          (a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256) &&
-         (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && a.partition_size % kBS == 0 &&
+         mfma_group_size(G, a.head_dim) && a.partition_size % kBS == 0 &&
          aligned16(a.q) && aligned16(a.k_cache) && aligned16(a.v_cache) &&
          (a.kv_stride * eb) % 16 == 0 &&
          (a.out == nullptr || (reinterpret_cast<uintptr_t>(a.out) & 3u) == 0);
@@ -1322,7 +1346,7 @@ bool stream_applies(const DecodeArgs& a, int32_t dtype) {
   if (dtype != RG_DTYPE_F32) return mfma_applies(a, dtype);
   const int G = a.num_heads / a.num_kv_heads;
   return a.bs_shift >= 0 && (a.head_dim == 64 || a.head_dim == 128) &&
-         (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && aligned16(a.q) && aligned16(a.k_cache) &&
+         mfma_group_size(G, a.head_dim) && aligned16(a.q) && aligned16(a.k_cache) &&
          aligned16(a.v_cache) && (a.kv_stride * 4) % 16 == 0 && (a.out == nullptr || (reinterpret_cast<uintptr_t>(a.out) & 3u) == 0);
 }
 
@@ -1464,7 +1488,16 @@ void launch_stream_g(const StreamArgs& sa, const DecodeArgs& a, int G, hipStream
     case 2: launch_stream<T, D, 2>(sa, a, s); break;
     case 4: launch_stream<T, D, 4>(sa, a, s); break;
     case 8: launch_stream<T, D, 8>(sa, a, s); break;
-    default: launch_stream<T, D, 16>(sa, a, s); break;
+    case 16: launch_stream<T, D, 16>(sa, a, s); break;
+    default:
+      // G = 3, 5, 6, 7 (stream_applies admits them at head_dim 64 and 128 only)
+      if constexpr (D <= 128) {
+        if (G == 3) launch_stream<T, D, 3>(sa, a, s);
+        else if (G == 5) launch_stream<T, D, 5>(sa, a, s);
+        else if (G == 6) launch_stream<T, D, 6>(sa, a, s);
+        else if (G == 7) launch_stream<T, D, 7>(sa, a, s);
+      }
+      break;
   }
 }
 

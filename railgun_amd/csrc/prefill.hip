@@ -43,6 +43,9 @@ struct PrefillArgs {
   int32_t sched_kbound;  // > 0: bound on the work keys of the sorted schedule (MFMA path)
   int64_t kv_stride;
   uint32_t kv_stride_bytes;  // MFMA path: block stride in bytes (below 2^32)
+  // MFMA path: (kv_stride / (16 D)) << 3 | j for blocks of 16 << j tokens: the block stride in
+  // 16-row sub-blocks and the sub-blocks per block (one scalar: the kernel is at its SGPR limit).
+  uint32_t win_param;
 };
 
 // Sequence owning packed row `row`: the last s with cu_seqlens[s] <= row.
@@ -157,7 +160,10 @@ template <> struct mfma32<f16_t> {
 constexpr int kPT = 32;               // queries per tile and keys per key tile
 constexpr int kPWaves = 4;            // waves per workgroup: (heads per workgroup) x (query subtiles)
 constexpr int kPThreads = kPWaves * 64;
-constexpr int kBlk = 16;              // KV block size on the MFMA path (two blocks per key tile)
+// Key sub-block of the MFMA path: 16 tokens, two per key tile.  A KV block of 16 << j tokens
+// holds 2^j of them (the rows of one kv-head in a block are contiguous, so a sub-block is 16
+// consecutive rows of it).
+constexpr int kBlk = 16;
 
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 
@@ -179,6 +185,26 @@ constexpr int kPStages = RG_PF_STAGES;  // K/V tiles in flight (ring in LDS)
 #endif
 constexpr int kKAhead = RG_PF_KAHEAD;
 constexpr int kVAhead = RG_PF_VAHEAD;
+// Wave priority around the MFMA bursts of the tile loop: 1 while a wave issues its QK or PV
+// MFMAs (and the operand reads between them), 0 for its softmax.  Three waves share each SIMD;
+// with the priority the one that has MFMAs ready is issued first, so the matrix pipe is fed
+// while the others run their softmax in the gaps.
+#ifndef RG_PF_PRIO
+#define RG_PF_PRIO 1
+#endif
+// Split softmax: the probabilities of a tile's keys 16..31 are formed while the PV MFMAs of keys
+// 0..15 run (interleaved in one wave), instead of all probabilities before the PV product.
+#ifndef RG_PF_SPLIT
+#define RG_PF_SPLIT 0
+#endif
+template <int P>
+__device__ __forceinline__ void set_wave_prio() {
+  if constexpr (RG_PF_PRIO != 0) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(P);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
 // Sorted schedule tables (LDS): work keys up to kSchedKeys, sequences up to kSchedSeqs.
 #ifndef RG_PF_SCHED_KEYS
 #define RG_PF_SCHED_KEYS 512
@@ -362,11 +388,12 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   // copies (K: key lane & 15, chunk 4n + lane / 16; V: key kl of the instruction, physical
   // chunk swizzled by the row), and the LDS offset of the instruction inside a ring stage.
   const int cb = w >> 1, cp = w & 1;
-  auto copy_key = [&](int ld) {
-    if (ld < HALF_INS) return kBlk * cb + (lane & (kBlk - 1));
+  auto copy_key_of = [&](int ld, int ln) {
+    if (ld < HALF_INS) return kBlk * cb + (ln & (kBlk - 1));
     const int vi = cb * TL::BLK_INS + cp * HALF_INS + ld % HALF_INS;
-    return vi * (1024 / (D * 2)) + lane / TL::VCHUNKS;
+    return vi * (1024 / (D * 2)) + ln / TL::VCHUNKS;
   };
+  auto copy_key = [&](int ld) { return copy_key_of(ld, lane); };
   int32_t lane_off[LOADS_PER_WAVE];
   uint32_t ins_lds[LOADS_PER_WAVE];
 #pragma unroll
@@ -450,17 +477,29 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     return u < n_items ? u : n_items;
   };
 
-  // Per-unit registers, loaded ahead of the unit: the block-table window (lane i holds the
-  // numbers of blocks 2 wb + i and 2 wb + 64 + i, clamped to the unit's last block, i.e. of key
-  // tiles wb .. wb + 63; a tile's two block numbers are then v_readlane's) and the Q^T operand
+  // Per-unit registers, loaded ahead of the unit: the block-table window and the Q^T operand
   // (lane holds q[query j][16i + 8hh .. +8] for every d chunk i; zero for rows without a
-  // position).
+  // position).  Window: lane i holds the cache addresses, in units of 16 rows (16 D elements),
+  // of this kv-head's rows of 16-token sub-blocks 2 wb + i and 2 wb + 64 + i (clamped to the
+  // unit's last sub-block), i.e. of key tiles wb .. wb + 63, so a tile's two sub-block addresses
+  // are v_readlane's and a copy's address is one multiply by a constant.  Sub-block v lies in
+  // block table entry v >> bs_shift, at row 16 (v & (2^bs_shift - 1)) of the kv-head's rows.
   int btw0 = 0, btw1 = 0;
   uint4 qb[NKC];
-  auto load_window = [&](const Unit& un, int wbase, int last_blk) {
+  auto load_window = [&](const Unit& un, int wbase, int last_sub) {
     const int32_t* bt = block_table + (int64_t)un.s * a.max_blocks;
-    btw0 = bt[min(2 * wbase + lane, last_blk)];
-    btw1 = bt[min(2 * wbase + 64 + lane, last_blk)];
+    // (Derived here from the one packed argument behind an empty asm, not hoisted into scalar
+    // registers that would stay live across the unit loop.)
+    uint32_t wp = a.win_param;
+    asm volatile("" : "+s"(wp));
+    const int sh = (int)(wp & 7u);
+    const int v0 = min(2 * wbase + lane, last_sub), v1 = min(2 * wbase + 64 + lane, last_sub);
+    // Unsigned 32-bit: the address of the pool's last row in units of 16 D elements is below
+    // 2^32 for any pool the device holds (2^32 * 32 D bytes is 8 TB at head_dim 64).
+    const uint32_t head = (uint32_t)kvh << sh;  // the kv-head's first sub-block within a block
+    const uint32_t spb = wp >> 3, sm = (1u << sh) - 1u;
+    btw0 = (int)((uint32_t)bt[v0 >> sh] * spb + head + ((uint32_t)v0 & sm));
+    btw1 = (int)((uint32_t)bt[v1 >> sh] * spb + head + ((uint32_t)v1 & sm));
   };
   auto load_unit = [&](const Unit& un) {
     const int q0 = un.t * UR;
@@ -495,8 +534,7 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   int wb = 0;
   // Q and the window have landed; nothing else is in flight.
   __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
-  const int64_t head_off = (int64_t)kvh * kBlk * D;
-  const uint32_t head_off_bytes = (uint32_t)head_off * 2u;
+  constexpr uint32_t kSubBytes = kBlk * D * 2;  // one window unit: 16 rows
   const int nkt = pos_max >= 0 ? pos_max / kPT + 1 : 0;
   const uint32_t lds_base = (uint32_t)(uintptr_t)((RG_LDS char*)lds);
 
@@ -511,7 +549,7 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     const uint32_t sbase = lds_base + st * TL::BYTES;
     if (kt * kPT + kPT - 1 <= pos_max) {
       const uint32_t e = (uint32_t)__builtin_amdgcn_readlane(r < 64 ? btw0 : btw1, (r & 63) + cb);
-      const uint64_t boff = (uint64_t)e * a.kv_stride_bytes + head_off_bytes;
+      const uint64_t boff = (uint64_t)e * kSubBytes;
       const char* kbase = reinterpret_cast<const char*>(kc) + boff;
       const char* vbase = reinterpret_cast<const char*>(vc) + boff;
 #pragma unroll
@@ -522,12 +560,16 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     }
     const int e0 = __builtin_amdgcn_readlane(r < 64 ? btw0 : btw1, r & 63);
     const int e1 = __builtin_amdgcn_readlane(r < 64 ? btw0 : btw1, (r & 63) + 1);
-    const int64_t blk0 = (int64_t)e0 * a.kv_stride + head_off;
-    const int64_t blk1 = (int64_t)e1 * a.kv_stride + head_off;
+    const int64_t blk0 = (int64_t)(uint32_t)e0 * (kBlk * D);
+    const int64_t blk1 = (int64_t)(uint32_t)e1 * (kBlk * D);
+    // (The lane's keys are formed here from an opaque copy of the lane index, not kept from the
+    // set-up: this path runs once per unit and the registers are all taken around it.)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
 #pragma unroll
     for (int ld = 0; ld < LOADS_PER_WAVE; ++ld) {
       // The copy of key lane_key (within the tile) with the clamped key's row instead.
-      const int kl = copy_key(ld);
+      const int kl = copy_key_of(ld, ln);
       const int key = min(kt * kPT + kl, pos_max) - kt * kPT;
       const int64_t src = (key < kBlk ? blk0 : blk1) + (int64_t)((key & (kBlk - 1)) - (kl & (kBlk - 1))) * D +
                           lane_off[ld];
@@ -639,6 +681,19 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     }
     l_run = s0 + s1;
   };
+  // The probabilities of keys 16h .. 16h + 15 only (scores c[8h .. 8h + 7]) into pk[4h .. 4h + 3],
+  // their row sum added to l_run.
+  auto probs_half = [&](const f32x16_t& c, int h, uint32_t (&pk)[8]) {
+#pragma unroll
+    for (int v = 8 * h; v < 8 * h + 8; v += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(c[v], a.scale_log2, -m_run));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(c[v + 1], a.scale_log2, -m_run));
+      pk[v / 2] = pack2<T>(p0, p1);
+    }
+    const float s0 = pair_sum<T>(pk[4 * h + 2], pair_sum<T>(pk[4 * h], l_run));
+    const float s1 = pair_sum<T>(pk[4 * h + 3], pair_sum<T>(pk[4 * h + 1], 0.f));
+    l_run = s0 + s1;
+  };
   // O^T += V^T P^T for the tile in stage st, in two 16-key MFMA steps.  The A operand comes
   // from the transposing LDS read: in each 16-lane group, lane 4e+q points at
   // V[key0 + e][d0 + 4q .. +4] and lane i receives V[key0 .. key0+3][d0 + i].
@@ -673,6 +728,32 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
       const uint4 pb = make_uint4(pk[4 * n], pk[4 * n + 1], pk[4 * n + 2], pk[4 * n + 3]);
       __builtin_amdgcn_sched_barrier(0);
       o[m % NDB] = MF::run(va[m % kVA], pb, o[m % NDB]);
+      if (m + kVA < 2 * NDB) va[m % kVA] = v_operand(st, m + kVA);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // accumulate with the probabilities of keys 16..31 formed under the PV MFMAs of keys 0..15
+  // (pk[0..3] are ready on entry).
+  auto accumulate_split = [&](int st, const f32x16_t& c, uint32_t (&pk)[8], uint4 (&va)[kVA]) {
+    const uint4 pb0 = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+#pragma unroll
+    for (int m = 0; m < NDB; ++m) {
+      o[m] = MF::run(va[m % kVA], pb0, o[m]);
+      if (m + kVA < 2 * NDB) va[m % kVA] = v_operand(st, m + kVA);
+    }
+    probs_half(c, 1, pk);
+#pragma unroll
+    for (int m = 0; m < NDB; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two LDS reads
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint4 pb1 = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+#pragma unroll
+    for (int m = NDB; m < 2 * NDB; ++m) {
+      __builtin_amdgcn_sched_barrier(0);
+      o[m % NDB] = MF::run(va[m % kVA], pb1, o[m % NDB]);
       if (m + kVA < 2 * NDB) va[m % kVA] = v_operand(st, m + kVA);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -722,15 +803,25 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   auto tile_step = [&](int kt, auto sc) __attribute__((always_inline)) {
     constexpr int S = decltype(sc)::value;
     wait_for(kt);
+    set_wave_prio<1>();
     f32x16_t c = scores(S);
     // The copies of tile kt + kPStages - 1 go out while the QK MFMAs run.
     if (kt + kPStages - 1 < nkt) issue_tile(kt + kPStages - 1, S == 0 ? kPStages - 1 : S - 1);
     uint4 va[kVA];
     v_prefetch(S, va);
+    set_wave_prio<0>();
     update_max(mask_max(c, kt));
     uint32_t pk[8];
-    probs(c, pk);
-    accumulate(S, pk, va);
+    if constexpr (RG_PF_SPLIT != 0) {
+      probs_half(c, 0, pk);
+      set_wave_prio<1>();
+      accumulate_split(S, c, pk, va);
+    } else {
+      probs(c, pk);
+      set_wave_prio<1>();
+      accumulate(S, pk, va);
+    }
+    set_wave_prio<0>();
   };
   int kt = 0;
   int st = 0;  // ring stage of tile kt (kt % kPStages, kept as a rotating counter)
@@ -783,7 +874,7 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
           const int dl = 32 * db + 8 * jb - pass * DP;  // + 4 hh
           const uint32_t w0 = pack2<T>(o[db][4 * jb] * inv, o[db][4 * jb + 1] * inv);
           const uint32_t w1 = pack2<T>(o[db][4 * jb + 2] * inv, o[db][4 * jb + 3] * inv);
-          const int off = wr * (DP * 2) + (((dl >> 3) ^ (wr & (CH - 1))) << 4) + 8 * hh;
+          const int off = wr * (DP * 2) + (((dl >> 3) ^ (wr & (CH - 1))) << 4) + 8 * (lr >> 5);
           *reinterpret_cast<uint2*>(ebuf + off) = make_uint2(w0, w1);
         }
       wave_lds_fence();
@@ -1038,19 +1129,26 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
   }
   PrefillArgs a{query, key_cache, value_cache, block_table, context_lens, cu_seqlens, output,
                 scale * kLog2e, num_heads, num_kv_heads, head_dim, block_size,
-                max_blocks_per_seq, num_seqs, num_tokens, 0, 0, stride, 0};
+                max_blocks_per_seq, num_seqs, num_tokens, 0, 0, stride, 0, 0};
+  int bs_shift = -1;  // block_size = 16 << bs_shift on the MFMA path
+  for (int j = 0; j <= 4; ++j)
+    if (block_size == (kBlk << j)) bs_shift = j;
   hipStream_t s = as_stream(stream);
   const int eb = dtype_bytes(dtype);
-  // The MFMA tile kernel: bf16 / f16, head_dim 64 / 128, block 16 and a GQA ratio G of 1, 2
-  // or a multiple of 4 (GW = min(G, 4) heads per workgroup).
+  // The MFMA tile kernel: bf16 / f16, head_dim 64 / 128, block 16 << j (j <= 4), any GQA ratio G: a
+  // workgroup takes GW heads of one kv-head on 4 / GW subtiles of 32 rows, GW = 4 when 4
+  // divides G, else 2 when 2 does (G = 6: three workgroups of two heads per kv-head), else 1
+  // (G = 3, 5, 7: one head per workgroup, the G workgroups of a kv-head share its K/V tiles in
+  // the L2 of their die).
   const int G = num_heads / num_kv_heads;
-  const int GW = G >= 4 ? 4 : G;
-  if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && scale > 0.f && (G == 1 || G == 2 || G % 4 == 0) &&
-      block_size == kBlk &&
+  const int GW = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
+  if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && scale > 0.f &&
+      bs_shift >= 0 && stride % (kBlk * head_dim) == 0 && stride / (kBlk * head_dim) < (1 << 28) &&
       (head_dim == 64 || head_dim == 128) && max_blocks_per_seq > 0 && aligned16(query) &&
       aligned16(key_cache) && aligned16(value_cache) && (stride * eb) % 16 == 0 &&
       stride * eb <= (int64_t)UINT32_MAX && aligned16(output)) {
     a.kv_stride_bytes = (uint32_t)(stride * eb);
+    a.win_param = (uint32_t)(stride / (kBlk * head_dim)) << 3 | (uint32_t)bs_shift;
     const int64_t UR = (int64_t)kPT * (kPWaves / GW);  // rows per unit
     // Units per sequence from max_query_len (a hint: the kernel's last rank covers any units
     // beyond it; no query run is longer than num_tokens).
@@ -1092,9 +1190,9 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
     }
     return check_launch(op);
   }
-  // The fp32 MFMA tile kernel: head_dim 64 / 128, the GQA ratios of the 16-bit kernel, any
-  // block size, 16-byte aligned rows.
-  if (dtype == RG_DTYPE_F32 && (G == 1 || G == 2 || G % 4 == 0) && (head_dim == 64 || head_dim == 128) &&
+  // The fp32 MFMA tile kernel: head_dim 64 / 128, any GQA ratio (GW as above), any block size,
+  // 16-byte aligned rows.
+  if (dtype == RG_DTYPE_F32 && (head_dim == 64 || head_dim == 128) &&
       max_blocks_per_seq > 0 && num_seqs <= 65535 && aligned16(query) && aligned16(key_cache) &&
       aligned16(value_cache) && aligned16(output) && stride % 4 == 0) {
     const int64_t UR = (int64_t)kPT * (kPWaves / GW);

@@ -103,11 +103,12 @@ CTX_RAGGED = [1, 15, 16, 17, 33, 300, 0, 511, 1024]
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 5, 6, 7, 8, 16])
 def test_mfma_path_shapes(device, kernels, dt, D, G):
-    """MFMA kernels (block 16): every GQA ratio, ragged contexts incl. 0 and 1.  bf16 / f16 run
-    the grid kernel without a workspace and stream-K with one; fp32 runs the generic kernel
-    without a workspace and the fp32 stream-K tile (QK^T on fp32 MFMA) with one."""
+    """MFMA kernels (block 16): every GQA ratio (3, 5, 6, 7 fill the 16 operand rows unevenly:
+    row m holds head m % G), ragged contexts incl. 0 and 1.  bf16 / f16 run the grid kernel
+    without a workspace and stream-K with one; fp32 runs the generic kernel without a workspace
+    and the fp32 stream-K tile (QK^T on fp32 MFMA) with one."""
     Hkv = 2
     inp = make_inputs(device, CTX_RAGGED, dt, H=Hkv * G, Hkv=Hkv, D=D, seed=10 * G + D)
     want = oracle_v1_plus(inp)
@@ -275,6 +276,25 @@ def test_mfma_head_dim256(device, kernels, dt, G):
         for ws in (False, True):
             assert_close(gpu_v1(kernels, inp, ws), want, dt, f"bs={bs} ws={ws}")
         assert_close(gpu_v2(kernels, inp, 64), want, dt, f"bs={bs} v2")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("H,Hkv", [(24, 8), (28, 4), (40, 8), (48, 8)])
+def test_stream_gqa_model_shapes(device, kernels, H, Hkv, dt):
+    """Stream-K decode at the head counts of models whose GQA ratio is no power of two, head_dim
+    128: Llama-3.2-3B (24 / 8, G 3), Qwen2-7B (28 / 4, G 7), Qwen2.5-14B (40 / 8, G 5), and
+    48 / 8 (G 6); 64 sequences with contexts U[512, 4096] (config 2's load: many units per
+    worker, segments crossed mid range, window refills), against the oracle."""
+    rng = np.random.default_rng(H * 10 + Hkv)
+    ctx = rng.integers(512, 4096, 64, endpoint=True).astype(np.int32)
+    inp = _big_decode_inputs(device, ctx, dt, H, Hkv, 128, seed=H + Hkv, mb=256)
+    assert _stream_units(ctx, Hkv, 1) > 16 * _stream_workers(device)
+    want = orc.cpu_attention_gathered(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"], dt,
+                                      nthreads=_threads())
+    assert_close(gpu_v1(kernels, inp, True), want, dt, f"{H}/{Hkv} stream-K")
+    if dt == "bf16":
+        assert_close(gpu_v1(kernels, inp, False), want, dt, f"{H}/{Hkv} grid kernel")
+        assert_close(gpu_v2(kernels, inp, 512), want, dt, f"{H}/{Hkv} v2")
 
 
 def test_stream_head_dim256_many_units(device, kernels):

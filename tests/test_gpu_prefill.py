@@ -115,15 +115,15 @@ def _gqa_workload(G: int, D: int, lens, prior, seed: int, H: int = 32, mb: int =
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f32"])
-@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 5, 6, 7, 8, 16])
 @pytest.mark.parametrize("D", [64, 128])
 def test_prefill_mfma_gqa_ratios(device, kernels, G, D, dt):
     """The MFMA prefill kernels (bf16 and fp32) beyond GQA 4: one head per workgroup on four
-    32-row subtiles (G 1), two heads on two (G 2), one or several head groups of one kv-head
-    (G 4, 8, 16).  Ragged units (1 to 200 rows, lengths around the 32 / 64 / 128-row unit
-    sizes), prior context, a sequence whose rows end inside a unit's first subtile; every row
-    against the oracle."""
-    H = 16 if G == 1 else 32
+    32-row subtiles (G 1, 3, 5, 7), two heads on two (G 2, 6: three workgroups of two heads per
+    kv-head), one or several head groups of one kv-head (G 4, 8, 16).  Ragged units (1 to 200
+    rows, lengths around the 32 / 64 / 128-row unit sizes), prior context, a sequence whose
+    rows end inside a unit's first subtile; every row against the oracle."""
+    H = 16 if G == 1 else 32 if 32 % G == 0 else 4 * G
     w = _gqa_workload(G, D, [1, 31, 33, 64, 65, 100, 129, 200, 7], [0, 0, 40, 0, 17, 300, 0, 64, 1000],
                       seed=100 + G + D, H=H, dt=dt)
     _run(device, kernels, w, seed=200 + G + D, row_sample=True, row_stride=1)
@@ -136,6 +136,48 @@ def test_prefill_f32_long_and_block_sizes(device, kernels, bs):
     address any block size); every sequence on a row sample against the oracle."""
     w = _gqa_workload(4, 128, [1200, 700, 333, 64], [0, 2000, 5, 100], seed=500 + bs, dt="f32", bs=bs)
     _run(device, kernels, w, seed=600 + bs, row_sample=True)
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128, 256])
+@pytest.mark.parametrize("D,G,dt", [(128, 4, "bf16"), (64, 8, "f16"), (128, 3, "bf16")])
+def test_prefill_mfma_block_sizes(device, kernels, bs, D, G, dt):
+    """The 16-bit MFMA prefill at KV blocks of 16 << j tokens (a block holds 2^j of the kernel's
+    16-token sub-blocks; its block-table window holds sub-block addresses): sequences of up to
+    1,200 rows after up to 2,600 cached positions (the window moves past 128 sub-blocks), a
+    sequence whose rows end inside a block, every sequence on a row sample against the oracle."""
+    w = _gqa_workload(G, D, [1200, 700, 33, 5, 257], [0, 2600, 17, 250, 100], seed=800 + bs + D + G,
+                      H=8 * G, dt=dt, bs=bs)
+    _run(device, kernels, w, seed=900 + bs + D, row_sample=True)
+
+
+@pytest.mark.parametrize("pad", [0, 8])
+def test_prefill_fused_pool_and_odd_stride(device, kernels, pad):
+    """Caches that are views of a larger pool: Railgun's fused [NB, 2, H_kv, bs, D] pool (block
+    stride 2 H_kv bs D, a multiple of 16 D: the MFMA kernel) and, with pad 8, blocks 8 elements
+    apart beyond their rows (a stride the MFMA kernel's sub-block addressing cannot express:
+    the generic kernel takes it).  bf16, block 32, GQA 4, head_dim 128, against the oracle."""
+    rng = np.random.default_rng(60 + pad)
+    lens = np.array([300, 45, 129], np.int32)
+    prior = np.array([0, 500, 64], np.int32)
+    bs, H, hkv, D = 32, 32, 8, 128
+    bt = wl.assign_blocks(prior + lens, bs, 40, 20, rng)
+    T = int(lens.sum())
+    ctx = prior + lens
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q = normal(rng, (T, H, D), "bf16")
+    blk = hkv * bs * D
+    pool = normal(rng, (40, 2 * blk + pad), "bf16")
+    kv = [pool[:, i * blk:(i + 1) * blk].reshape(40, hkv, bs, D) for i in (0, 1)]
+    dpool = to_dev(pool, "bf16", device)
+    dk, dv = (dpool[:, i * blk:(i + 1) * blk].view(40, hkv, bs, D) for i in (0, 1))
+    assert dk.stride(0) == 2 * blk + pad
+    out = torch.full((T, H, D), float("nan"), dtype=torch.bfloat16, device=device)
+    scale = 1.0 / math.sqrt(D)
+    kernels.launch_prefill_packed(to_dev(q, "bf16", device), dk, dv, i32(bt, device), i32(ctx, device),
+                                  i32(cu, device), out, scale, H, hkv, D, bs, 20, len(lens), T, int(lens.max()))
+    torch.cuda.synchronize()
+    want = orc.prefill_packed(q, kv[0], kv[1], bt, ctx, cu, scale, "bf16")
+    assert_close(dev_f32(out), want, "bf16", f"pad {pad}")
 
 
 @pytest.mark.parametrize("max_query_len", [None, 1])
@@ -154,6 +196,18 @@ def test_prefill_mfma_gqa_long(device, kernels, G):
     H = 8 * G
     w = _gqa_workload(G, 128, [1200, 700, 333, 1023, 64], [0, 2000, 5, 0, 100], seed=300 + G, H=H)
     _run(device, kernels, w, seed=400 + G, row_sample=True)
+
+
+@pytest.mark.parametrize("H,Hkv", [(24, 8), (28, 4), (40, 8)])
+def test_prefill_gqa_model_shapes(device, kernels, H, Hkv):
+    """Packed prefill at the head counts of models whose GQA ratio is no power of two, bf16
+    head_dim 128: Llama-3.2-3B (24 / 8), Qwen2-7B (28 / 4), Qwen2.5-14B (40 / 8); config 4's
+    sequence lengths (12 sequences, up to 1,890 rows, many units per workgroup), every sequence
+    on a row sample against the oracle."""
+    G = H // Hkv
+    c4 = wl.config4()
+    w = _gqa_workload(G, 128, c4.seq_lens, np.zeros_like(c4.seq_lens), seed=H + Hkv, H=H)
+    _run(device, kernels, w, seed=H * Hkv, row_sample=True)
 
 
 @pytest.mark.parametrize("max_query_len", [None, 1])
