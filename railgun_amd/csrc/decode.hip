@@ -453,7 +453,7 @@ struct DecodeTileF32 {
   static constexpr int HG = (G + 3) / 4;
   static constexpr int GP = 4 * HG;  // as DecodeTile
   static constexpr int ACC = 4;
-  static_assert(NK >= 1 && TPI >= 1 && NV >= 1, "head_dim 64 or 128");
+  static_assert(NK >= 1 && TPI >= 1 && NV >= 1, "head_dim 64, 128 or 256");
 
   int col, seg, vrow, vd0;
   float qa[DQ];
@@ -748,8 +748,8 @@ constexpr int sk_bpu() { return D <= 64 ? (G >= 8 ? 2 : RG_SK_BPU_D64) : RG_SK_B
 template <int D, int G>
 constexpr int sk_prefetch() { return D <= 64 ? RG_SK_PREFETCH_D64 : D >= 256 ? 2 : RG_SK_PREFETCH; }
 // fp32 rows are twice as long: one-block units (8 KB of K and of V at head_dim 128), one in
-// flight ahead at head_dim 128 and two at head_dim 64 (the register ring of the 16-bit tiles'
-// depth would not fit).
+// flight ahead at head_dim 128 and 256 and two at head_dim 64 (the register ring of the 16-bit
+// tiles' depth would not fit).
 template <typename T, int D, int G>
 constexpr int sk_bpu_for() { return std::is_same_v<T, f32_t> ? 1 : sk_bpu<D, G>(); }
 template <typename T, int D, int G>
@@ -1340,12 +1340,13 @@ bool grid_mfma_applies(const DecodeArgs& a, int32_t dtype) {
   return mfma_applies(a, dtype) && !(a.head_dim == 256 && a.num_heads / a.num_kv_heads == 16);
 }
 
-// The stream-K decode: the MFMA shapes in bf16 / f16, and the same shapes in fp32 (head_dim 64
-// or 128).
+// The stream-K decode: the MFMA shapes in bf16 / f16, and the same shapes in fp32 (head_dim 64,
+// 128 or 256; at 256 a worker holds a block's K and V rows, 128 VGPRs, next to the q row's 64: it
+// runs with AGPRs as extra registers, one wave per SIMD as always).
 bool stream_applies(const DecodeArgs& a, int32_t dtype) {
   if (dtype != RG_DTYPE_F32) return mfma_applies(a, dtype);
   const int G = a.num_heads / a.num_kv_heads;
-  return a.bs_shift >= 0 && (a.head_dim == 64 || a.head_dim == 128) &&
+  return a.bs_shift >= 0 && (a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256) &&
          mfma_group_size(G, a.head_dim) && aligned16(a.q) && aligned16(a.k_cache) &&
          aligned16(a.v_cache) && (a.kv_stride * 4) % 16 == 0 && (a.out == nullptr || (reinterpret_cast<uintptr_t>(a.out) & 3u) == 0);
 }
@@ -1532,7 +1533,8 @@ int run_stream(const char* op, const DecodeArgs& a, int32_t dtype, const Shape& 
     else if (sh.D == 128) launch_stream_g<f16_t, 128>(sa, a, G, s);
     else launch_stream_g<f16_t, 64>(sa, a, G, s);
   } else {
-    if (sh.D == 128) launch_stream_g<f32_t, 128>(sa, a, G, s);
+    if (sh.D == 256) launch_stream_g<f32_t, 256>(sa, a, G, s);
+    else if (sh.D == 128) launch_stream_g<f32_t, 128>(sa, a, G, s);
     else launch_stream_g<f32_t, 64>(sa, a, G, s);
   }
   return check_launch(op);

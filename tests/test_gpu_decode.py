@@ -264,11 +264,13 @@ def test_mfma_path_block_sizes(device, kernels, dt, D, G, bs):
         assert_close(gpu_v2(kernels, inp, 2 * bs), want, dt, f"fused={fused} v2")
 
 
-@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
 def test_mfma_head_dim256(device, kernels, dt, G):
     """head_dim 256 on the MFMA kernels (grid without a workspace, except G = 16, which the
-    generic kernel serves; stream-K with one; v2) over ragged contexts, 16- and 32-token blocks."""
+    generic kernel serves; stream-K with one; v2) over ragged contexts, 16- and 32-token blocks.
+    In fp32 (the reference's element type): the generic kernel without a workspace, the fp32
+    stream-K tile with one."""
     Hkv = 2
     for bs in (16, 32):
         inp = make_inputs(device, CTX_RAGGED, dt, H=Hkv * G, Hkv=Hkv, D=256, bs=bs, seed=256 + G + bs)
@@ -297,16 +299,18 @@ def test_stream_gqa_model_shapes(device, kernels, H, Hkv, dt):
         assert_close(gpu_v2(kernels, inp, 512), want, dt, f"{H}/{Hkv} v2")
 
 
-def test_stream_head_dim256_many_units(device, kernels):
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_stream_head_dim256_many_units(device, kernels, dt):
     """head_dim 256, 16 / 4 heads (Gemma-like grouping), 96 sequences with contexts U[64, 4096],
-    bf16: tens of one-block units per worker, window refills, segments crossed mid range."""
+    bf16 and fp32: tens of one-block units per worker, window refills, segments crossed mid
+    range."""
     rng = np.random.default_rng(901)
     ctx = rng.integers(64, 4096, 96, endpoint=True).astype(np.int32)
-    inp = _big_decode_inputs(device, ctx, "bf16", 16, 4, 256, seed=901, mb=256)
+    inp = _big_decode_inputs(device, ctx, dt, 16, 4, 256, seed=901, mb=256)
     assert _stream_units(ctx, 4, 1) > 16 * _stream_workers(device)
-    want = orc.cpu_attention_gathered(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"], "bf16",
+    want = orc.cpu_attention_gathered(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"], dt,
                                       nthreads=_threads())
-    assert_close(gpu_v1(kernels, inp, True), want, "bf16", "D=256")
+    assert_close(gpu_v1(kernels, inp, True), want, dt, "D=256")
 
 
 @pytest.mark.parametrize("bs", [32, 64, 256])
