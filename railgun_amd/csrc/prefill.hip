@@ -46,6 +46,10 @@ struct PrefillArgs {
   // MFMA path: (kv_stride / (16 D)) << 3 | j for blocks of 16 << j tokens: the block stride in
   // 16-row sub-blocks and the sub-blocks per block (one scalar: the kernel is at its SGPR limit).
   uint32_t win_param;
+  // MFMA path, sorted schedule: > 0 when the workgroups of a head group sit three to a CU in
+  // sched_cols columns (workgroup q of the group shares its CU with q +- sched_cols): the items
+  // are dealt to the columns in snake order and split inside a column by dispatch slot.
+  int32_t sched_cols;
 };
 
 // Sequence owning packed row `row`: the last s with cu_seqlens[s] <= row.
@@ -189,6 +193,28 @@ constexpr int kVAhead = RG_PF_VAHEAD;
 // MFMAs (and the operand reads between them), 0 for its softmax.  Three waves share each SIMD;
 // with the priority the one that has MFMAs ready is issued first, so the matrix pipe is fed
 // while the others run their softmax in the gaps.
+// Column split of the sorted schedule (sched_cols > 0).  The three workgroups of a CU are
+// dispatched in order and the oldest wins issue arbitration, so with equal work they end in
+// dispatch order, ~27 us apart at config 4 (per-workgroup timestamps): the CU then runs its
+// last stretch with one or two workgroups.  Inside a column the items (longest first) go one
+// by one to the slot whose finish time (load + item) / rate is least, with the slots' rates
+// measured while all three run (0.92 : 0.72 : 0.57 per us at config 4 -> 13 : 10 : 8), an
+// item costing its key tiles plus RG_PF_UNIT_COST tiles of unit set-up and epilogue.
+#ifndef RG_PF_WEIGHTED
+#define RG_PF_WEIGHTED 1
+#endif
+#ifndef RG_PF_SLOT_W0
+#define RG_PF_SLOT_W0 13
+#endif
+#ifndef RG_PF_SLOT_W1
+#define RG_PF_SLOT_W1 10
+#endif
+#ifndef RG_PF_SLOT_W2
+#define RG_PF_SLOT_W2 8
+#endif
+#ifndef RG_PF_UNIT_COST
+#define RG_PF_UNIT_COST 3
+#endif
 #ifndef RG_PF_PRIO
 #define RG_PF_PRIO 1
 #endif
@@ -470,8 +496,63 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   // r * Q + Q - 1 - q on odd rounds, for the Q workgroups of the kv-head); n_items once done.
   // (A shared work counter was measured: it evens out the workgroups of a CU but not the
   // CU's finish time, and its round trips cost more than it saved.)
+  // With columns (sched_cols = C > 0) the snake runs over the C columns instead (round r of
+  // column c: position r * C + c, or r * C + C - 1 - c), and the column's first 64 rounds are
+  // split between its three workgroups (slot qw / C, dispatch order) by the weighted greedy
+  // above, which every workgroup of the column computes alike from its own copy of the
+  // tables.  Rounds from 64 on go to the slots in turn.  Each wave keeps this state in LDS,
+  // not in registers (the kernel is at its scalar-register limit): the rounds of the first 64
+  // it has not yet taken (`sched_mine`) and (C, column, its next round from 64 on).
+  __shared__ uint64_t sched_mine[kPWaves];
+  __shared__ int4 sched_colw[kPWaves];
+  {
+    const int cols = sorted ? a.sched_cols : 0;
+    const int col = cols > 0 ? qw % cols : 0, slot = cols > 0 ? qw / cols : 0;
+    uint64_t mine = 0;
+    const int u = lane * cols + ((lane & 1) ? cols - 1 - col : col);
+    int cost = 0;
+    if (cols > 0 && u < n_items) {
+      int lo = 1, hi = kb;  // the item's key, as in resolve
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (sched_b[mid] > u) lo = mid;
+        else hi = mid - 1;
+      }
+      cost = lo * QS + RG_PF_UNIT_COST;
+    }
+    constexpr int F0 = RG_PF_SLOT_W1 * RG_PF_SLOT_W2, F1 = RG_PF_SLOT_W0 * RG_PF_SLOT_W2,
+                  F2 = RG_PF_SLOT_W0 * RG_PF_SLOT_W1;
+    int l0 = 0, l1 = 0, l2 = 0;
+    for (int i = 0; i < 64; ++i) {
+      const int c = __builtin_amdgcn_readlane(cost, i);
+      if (c == 0) break;  // past the column's last item
+      // finish times (l_s + c) / w_s, compared as (l_s + c) * (product of the other weights)
+      const int f0 = (l0 + c) * F0, f1 = (l1 + c) * F1, f2 = (l2 + c) * F2;
+      const int sl = f0 <= f1 ? (f0 <= f2 ? 0 : 2) : (f1 <= f2 ? 1 : 2);
+      if (sl == 0) l0 += c;
+      else if (sl == 1) l1 += c;
+      else l2 += c;
+      if (sl == slot) mine |= 1ull << i;
+    }
+    sched_mine[w] = mine;
+    sched_colw[w] = make_int4(cols, col, 64 + slot, 0);
+  }
   int round = 0;
   auto take_item = [&]() -> int {
+    const int4 cw = sched_colw[w];
+    if (cw.x > 0) {
+      int r;
+      const uint64_t mine = sched_mine[w];
+      if (mine != 0) {
+        r = __builtin_ctzll(mine);
+        sched_mine[w] = mine & (mine - 1);
+      } else {
+        r = cw.z;
+        sched_colw[w].z = r + 3;
+      }
+      const int u = r * cw.x + ((r & 1) ? cw.x - 1 - cw.y : cw.y);
+      return u < n_items ? u : n_items;
+    }
     const int r = round++;
     const int u = r * nq_wg + ((r & 1) ? nq_wg - 1 - qw : qw);
     return u < n_items ? u : n_items;
@@ -1166,6 +1247,13 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
     const int64_t per_group =
         std::min<int64_t>(items, std::max<int64_t>(1, RG_PF_WG_PER_CU * device_cu_count() / ngroups));
     const dim3 grid((unsigned)(per_group * ngroups));
+    // Columns: every CU holds three workgroups of one head group (workgroup b shares its CU with
+    // b +- cu_count, measured), i.e. the group's workgroups q, q + C, q + 2C with C = cu / groups.
+    const int64_t cus = device_cu_count();
+    if (RG_PF_WEIGHTED && RG_PF_WG_PER_CU == 3 && a.sched_kbound > 0 && cus % ngroups == 0 &&
+        per_group == 3 * (cus / ngroups)) {
+      a.sched_cols = (int32_t)(cus / ngroups);
+    }
     auto go = [&](auto tag, auto dtag, auto gtag) {
       using T = decltype(tag);
       constexpr int D = decltype(dtag)::value;

@@ -363,3 +363,34 @@ def test_prefill_rising_scores(device, kernels, dt):
     got = dev_f32(out)
     assert not np.isnan(got).any()
     assert_close(got, want, dt, "rising scores")
+
+
+def test_prefill_column_schedule_past_64_rounds(device, kernels):
+    """The column split of the sorted schedule past a column's first 64 rounds, which the
+    weighted greedy does not cover (those rounds go to the three workgroups of a CU in turn):
+    256 q-heads over 64 kv-heads (64 head groups of 4, so 4 columns on a 256-CU device), 36
+    sequences of 256 rows, every other one after cached positions: 288 units per group, 72
+    rounds per column.  Every output row is written (the output starts as NaN) and 3 rows of
+    each sequence match the oracle at every head."""
+    rng = np.random.default_rng(64)
+    H, hkv, D, bs, dt = 256, 64, 64, 16, "bf16"
+    lens = np.full(36, 256, np.int32)
+    prior = np.where(np.arange(36) % 2 == 1, rng.integers(1, 300, 36), 0).astype(np.int32)
+    ctx = prior + lens
+    mb = int(((ctx + bs - 1) // bs).max())
+    nb = int(((ctx + bs - 1) // bs).sum()) + 4
+    bt = wl.assign_blocks(ctx, bs, nb, mb, rng)
+    T = int(lens.sum())
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q = normal(rng, (T, H, D), dt)
+    kc, vc = normal(rng, (nb, hkv, bs, D), dt), normal(rng, (nb, hkv, bs, D), dt)
+    scale = 1.0 / math.sqrt(D)
+    out = torch.full((T, H, D), float("nan"), dtype=TORCH_DT[dt], device=device)
+    kernels.launch_prefill_packed(to_dev(q, dt, device), to_dev(kc, dt, device), to_dev(vc, dt, device),
+                                  i32(bt, device), i32(ctx, device), i32(cu, device), out, scale, H, hkv, D, bs, mb,
+                                  len(lens), T, int(lens.max()))
+    torch.cuda.synchronize()
+    assert not bool(torch.isnan(out).any()), "rows left unwritten"
+    rows = np.array([r for s in range(len(lens)) for r in (cu[s], cu[s] + 131, cu[s + 1] - 1)], np.int32)
+    want = orc.prefill_packed_rows(q, kc, vc, bt, ctx, cu, rows, scale, dt, nthreads=_threads())
+    assert_close(dev_f32(out[torch.from_numpy(rows).long().to(device)]), want, dt, "sampled rows")
