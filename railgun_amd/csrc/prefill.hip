@@ -7,9 +7,9 @@
 //
 // prefill_generic_kernel: one wave per (row, q-head), any dtype / head_dim /
 // block size; each lane owns 4 dims and the keys are visited in order with an
-// online softmax.  prefill_mfma_kernel (bf16/f16, head_dim 64/128, GQA 1, 2 or a multiple
-// of 4) is the MFMA tile kernel used whenever it applies; prefill_f32_kernel is its fp32
-// counterpart on v_mfma_f32_32x32x2_f32.
+// online softmax.  prefill_mfma_kernel (bf16/f16, head_dim 64/128/256, any GQA ratio) is the
+// MFMA tile kernel used whenever it applies; prefill_f32_kernel is its fp32 counterpart on
+// v_mfma_f32_32x32x2_f32.
 #include <math.h>
 
 #include <algorithm>
@@ -180,6 +180,13 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 #endif
 
 constexpr int kPStages = RG_PF_STAGES;  // K/V tiles in flight (ring in LDS)
+// head_dim 256: the O accumulators (128 VGPRs) and the Q^T operand (64) leave room for one wave
+// per SIMD, so one workgroup per CU, with a four-stage ring (4 x 32 KB) to keep three key tiles
+// in flight while it computes.
+template <int D>
+constexpr int pf_wg_per_cu() { return D > 128 ? 1 : RG_PF_WG_PER_CU; }
+template <int D>
+constexpr int pf_stages() { return D > 128 ? 4 : kPStages; }
 // LDS operand reads in flight ahead of the MFMA that uses them: K (QK^T) and V (PV).
 #ifndef RG_PF_KAHEAD
 #define RG_PF_KAHEAD 4
@@ -286,13 +293,14 @@ struct PTile {
 };
 
 template <typename T, int D, int GW>
-__global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kernel(
+__global__ __launch_bounds__(kPThreads, pf_wg_per_cu<D>()) void prefill_mfma_kernel(
     PrefillArgs a, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, const int32_t* __restrict__ cu_seqlens) {
   using MF = mfma32<T>;
   using S = uint16_t;
   using TL = PTile<D>;
+  constexpr int NST = pf_stages<D>();  // ring stages
   // Heads per workgroup GW (1, 2 or 4) and query subtiles QS = 4 / GW: wave w computes head
   // w % GW on query subtile w / GW of the unit, which has UR = 32 * QS rows.
   static_assert(GW == 1 || GW == 2 || GW == 4, "heads per workgroup");
@@ -305,7 +313,7 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   constexpr int HALF_INS = TL::BLK_INS / 2;
   static_assert(HALF_INS >= 1 && TL::BLK_INS % 2 == 0, "block copies split over two waves");
   constexpr int LOADS_PER_WAVE = 2 * HALF_INS;
-  __shared__ __attribute__((aligned(16))) char lds[kPStages * TL::BYTES];
+  __shared__ __attribute__((aligned(16))) char lds[NST * TL::BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -627,7 +635,12 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   // pos_max, with per-lane addresses (the slow path).
   auto issue_tile = [&](int kt, int st) {
     const int r = 2 * (kt - wb);  // even: both blocks sit in the same window register
-    const uint32_t sbase = lds_base + st * TL::BYTES;
+    // (The stage base is formed here from an opaque copy of the LDS base: hoisted, every
+    // (stage, copy) pair of the unrolled ring kept its own M0 value in a scalar register, 32 at
+    // head_dim 256.)
+    uint32_t lb = lds_base;
+    asm volatile("" : "+s"(lb));
+    const uint32_t sbase = lb + st * TL::BYTES;
     if (kt * kPT + kPT - 1 <= pos_max) {
       const uint32_t e = (uint32_t)__builtin_amdgcn_readlane(r < 64 ? btw0 : btw1, (r & 63) + cb);
       const uint64_t boff = (uint64_t)e * kSubBytes;
@@ -671,9 +684,9 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   // The tile loop runs each tile in order (scores, maximum, probabilities, PV); the overlap
   // of one wave's softmax with another's MFMAs comes from the three workgroups sharing each
   // SIMD.  Ring: iteration kt reads tile kt's K and V from its stage; copies of tiles
-  // kt+1 .. kt+kPStages-1 are in flight (tile kt+kPStages-1 issued during kt's QK MFMAs into
+  // kt+1 .. kt+NST-1 are in flight (tile kt+NST-1 issued during kt's QK MFMAs into
   // the stage tile kt-1 left).
-  static_assert(kPStages >= 3 && kPStages <= 64, "ring depth");
+  static_assert(NST >= 3 && NST <= 64, "ring depth");
   const char* vlds = lds + TL::KBYTES;
   const int grp = lane >> 4;
   const int e_row = (lane >> 2) & 3;
@@ -849,20 +862,20 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     tile_barrier();
   };
 
-  // In-order tile loop: the copies of tiles kt .. min(kt + kPStages - 2, nkt - 1) are in flight
+  // In-order tile loop: the copies of tiles kt .. min(kt + NST - 2, nkt - 1) are in flight
   // when iteration kt starts; once tile kt has landed everywhere (wait + barrier, which also
-  // shows every wave is done with tile kt - 1), stage (kt - 1) % kPStages takes tile
-  // kt + kPStages - 1 (if there is one), then tile kt is computed: scores, maximum,
+  // shows every wave is done with tile kt - 1), stage (kt - 1) % NST takes tile
+  // kt + NST - 1 (if there is one), then tile kt is computed: scores, maximum,
   // probabilities, PV.
-  static_assert(kPStages == 3 || kPStages == 4, "ring depth");
-  auto wait_for = [&](int kt) {  // tile kt landed; min(kPStages - 2, nkt - 1 - kt) newer tiles may not have
+  static_assert(NST == 3 || NST == 4, "ring depth");
+  auto wait_for = [&](int kt) {  // tile kt landed; min(NST - 2, nkt - 1 - kt) newer tiles may not have
     const int newer = nkt - 1 - kt;
-    if (newer >= kPStages - 2) wait_tiles(std::integral_constant<int, kPStages - 2>{});
-    else if (kPStages == 4 && newer == 1) wait_tiles(std::integral_constant<int, 1>{});
+    if (newer >= NST - 2) wait_tiles(std::integral_constant<int, NST - 2>{});
+    else if (NST == 4 && newer == 1) wait_tiles(std::integral_constant<int, 1>{});
     else wait_tiles(std::integral_constant<int, 0>{});
   };
 #pragma unroll
-  for (int p = 0; p < kPStages - 1; ++p)
+  for (int p = 0; p < NST - 1; ++p)
     if (p < nkt) issue_tile(p, p);
   // Next unit (the next tile of this item, or the first unit of the next item), found while
   // the first copies are in flight: it needs only the LDS tables and the static item order.
@@ -886,8 +899,8 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     wait_for(kt);
     set_wave_prio<1>();
     f32x16_t c = scores(S);
-    // The copies of tile kt + kPStages - 1 go out while the QK MFMAs run.
-    if (kt + kPStages - 1 < nkt) issue_tile(kt + kPStages - 1, S == 0 ? kPStages - 1 : S - 1);
+    // The copies of tile kt + NST - 1 go out while the QK MFMAs run.
+    if (kt + NST - 1 < nkt) issue_tile(kt + NST - 1, S == 0 ? NST - 1 : S - 1);
     uint4 va[kVA];
     v_prefetch(S, va);
     set_wave_prio<0>();
@@ -905,16 +918,16 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     set_wave_prio<0>();
   };
   int kt = 0;
-  int st = 0;  // ring stage of tile kt (kt % kPStages, kept as a rotating counter)
+  int st = 0;  // ring stage of tile kt (kt % NST, kept as a rotating counter)
   while (kt < nkt) {
-  // Iterations whose refill tile kt + kPStages - 1 lies in the current block-table window.
-  const int kend = min(nkt, wb + 65 - kPStages);
+  // Iterations whose refill tile kt + NST - 1 lies in the current block-table window.
+  const int kend = min(nkt, wb + 65 - NST);
   for (; kt < kend; ++kt) {
     // One copy of the tile per ring stage, so that each stage's LDS offsets are immediates.
     [&]<int... S>(std::integer_sequence<int, S...>) {
       ((st == S ? tile_step(kt, std::integral_constant<int, S>{}) : void()), ...);
-    }(std::make_integer_sequence<int, kPStages>{});
-    st = st == kPStages - 1 ? 0 : st + 1;
+    }(std::make_integer_sequence<int, NST>{});
+    st = st == NST - 1 ? 0 : st + 1;
   }
   if (kt >= nkt) break;
   wb += 64;
@@ -927,11 +940,11 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
   tile_barrier();
   // Normalise (the two halves of a query's keys live in lanes l and l ^ 32) and write; rows
   // without a position get zeros.  The tile goes out through LDS, DP columns at a time: each
-  // wave writes its rows into its quarter of ring stage kPStages - 1 (16-byte chunks XOR-
+  // wave writes its rows into its quarter of ring stage NST - 1 (16-byte chunks XOR-
   // swizzled by the row), then reads whole row pieces back, so that every store writes
   // 16 bytes per lane over full runs of a row.  That stage is free here: after the barrier
   // above nobody reads the ring, the next unit's prologue fills stages 0 and 1, and stage
-  // kPStages - 1 is refilled only after the next unit's first barrier.
+  // NST - 1 is refilled only after the next unit's first barrier.
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = row_ok ? 1.f / l_tot : 0.f;
   if (nhave) load_unit(nxt);
@@ -940,7 +953,7 @@ __global__ __launch_bounds__(kPThreads, RG_PF_WG_PER_CU) void prefill_mfma_kerne
     constexpr int CH = DP / 8;                            // 16-byte chunks per row piece
     constexpr int RPR = 64 / CH;                          // rows per read
     static_assert(D % DP == 0 && DP % 32 == 0 && 64 % CH == 0, "epilogue passes");
-    char* ebuf = lds + (kPStages - 1) * TL::BYTES + w * (TL::BYTES / kPWaves);
+    char* ebuf = lds + (NST - 1) * TL::BYTES + w * (TL::BYTES / kPWaves);
     // (The lane's rows are formed here, not hoisted out of the unit loop, where they would
     // take registers for the whole loop.)
     int lr = lane;
@@ -1216,7 +1229,7 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
     if (block_size == (kBlk << j)) bs_shift = j;
   hipStream_t s = as_stream(stream);
   const int eb = dtype_bytes(dtype);
-  // The MFMA tile kernel: bf16 / f16, head_dim 64 / 128, block 16 << j (j <= 4), any GQA ratio G: a
+  // The MFMA tile kernel: bf16 / f16, head_dim 64 / 128 / 256, block 16 << j (j <= 4), any GQA ratio G: a
   // workgroup takes GW heads of one kv-head on 4 / GW subtiles of 32 rows, GW = 4 when 4
   // divides G, else 2 when 2 does (G = 6: three workgroups of two heads per kv-head), else 1
   // (G = 3, 5, 7: one head per workgroup, the G workgroups of a kv-head share its K/V tiles in
@@ -1225,7 +1238,7 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
   const int GW = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
   if ((dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && scale > 0.f &&
       bs_shift >= 0 && stride % (kBlk * head_dim) == 0 && stride / (kBlk * head_dim) < (1 << 28) &&
-      (head_dim == 64 || head_dim == 128) && max_blocks_per_seq > 0 && aligned16(query) &&
+      (head_dim == 64 || head_dim == 128 || head_dim == 256) && max_blocks_per_seq > 0 && aligned16(query) &&
       aligned16(key_cache) && aligned16(value_cache) && (stride * eb) % 16 == 0 &&
       stride * eb <= (int64_t)UINT32_MAX && aligned16(output)) {
     a.kv_stride_bytes = (uint32_t)(stride * eb);
@@ -1240,17 +1253,18 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
     const int64_t kbound =
         (std::max<int64_t>((int64_t)max_blocks_per_seq * block_size, num_tokens) + 2 * UR - 2) / UR + 1;
     a.sched_kbound = (kbound <= kSchedKeys && num_seqs <= kSchedSeqs) ? (int32_t)kbound : 0;
-    // RG_PF_WG_PER_CU resident workgroups per CU, split evenly over the head groups, at most
-    // one per item.
+    // RG_PF_WG_PER_CU resident workgroups per CU (one at head_dim 256), split evenly over the
+    // head groups, at most one per item.
     const int64_t ngroups = num_heads / GW;
     const int64_t items = (int64_t)a.rank_tiles * num_seqs;
+    const int64_t wg_per_cu = head_dim > 128 ? pf_wg_per_cu<256>() : pf_wg_per_cu<128>();
     const int64_t per_group =
-        std::min<int64_t>(items, std::max<int64_t>(1, RG_PF_WG_PER_CU * device_cu_count() / ngroups));
+        std::min<int64_t>(items, std::max<int64_t>(1, wg_per_cu * device_cu_count() / ngroups));
     const dim3 grid((unsigned)(per_group * ngroups));
     // Columns: every CU holds three workgroups of one head group (workgroup b shares its CU with
     // b +- cu_count, measured), i.e. the group's workgroups q, q + C, q + 2C with C = cu / groups.
     const int64_t cus = device_cu_count();
-    if (RG_PF_WEIGHTED && RG_PF_WG_PER_CU == 3 && a.sched_kbound > 0 && cus % ngroups == 0 &&
+    if (RG_PF_WEIGHTED && wg_per_cu == 3 && a.sched_kbound > 0 && cus % ngroups == 0 &&
         per_group == 3 * (cus / ngroups)) {
       a.sched_cols = (int32_t)(cus / ngroups);
     }
@@ -1269,11 +1283,14 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
     };
     using D64 = std::integral_constant<int, 64>;
     using D128 = std::integral_constant<int, 128>;
+    using D256 = std::integral_constant<int, 256>;
     if (dtype == RG_DTYPE_BF16) {
-      if (head_dim == 128) go_gw(bf16_t{}, D128{});
+      if (head_dim == 256) go_gw(bf16_t{}, D256{});
+      else if (head_dim == 128) go_gw(bf16_t{}, D128{});
       else go_gw(bf16_t{}, D64{});
     } else {
-      if (head_dim == 128) go_gw(f16_t{}, D128{});
+      if (head_dim == 256) go_gw(f16_t{}, D256{});
+      else if (head_dim == 128) go_gw(f16_t{}, D128{});
       else go_gw(f16_t{}, D64{});
     }
     return check_launch(op);

@@ -58,11 +58,16 @@ def kernel_descriptors(tmp_path) -> dict[str, dict[str, int]]:
     return kernels
 
 
-# Scalar registers a kernel may park in VGPR lanes (v_writelane / v_readlane, no memory): the
-# 16-bit prefill kernels at head_dim 128 sit at the 106-SGPR limit and keep a few set-up values
-# (the K cache base, two LDS offsets) there, reloaded once per query unit, outside the tile loop.
-# A larger count means a change pushed live scalars into the inner loops; it fails here.
-MAX_SGPR_LANE_SPILLS = 8
+# Scalar registers a kernel may park in VGPR lanes (v_writelane / v_readlane, no memory): only
+# the 16-bit prefill kernels at head_dim 256, which sit at the 106-SGPR limit and keep about ten
+# set-up values there, stored at the unit set-up and none reloaded inside the tile loop.  Every
+# other kernel keeps its scalars in SGPRs; a count above these means a change pushed live scalars
+# towards the inner loops, and it fails here.
+MAX_SGPR_LANE_SPILLS = 12
+
+
+def _lane_spill_limit(name: str) -> int:
+    return MAX_SGPR_LANE_SPILLS if "prefill_mfma_kernel" in name and "Li256E" in name else 0
 
 
 def test_no_kernel_uses_scratch(tmp_path):
@@ -72,7 +77,5 @@ def test_no_kernel_uses_scratch(tmp_path):
     bad = {k: (v["private_segment_fixed_size"], v.get("vgpr_spill_count", 0), v.get("sgpr_spill_count", 0))
            for k, v in kernels.items()
            if v["private_segment_fixed_size"] or v.get("vgpr_spill_count", 0)
-           or v.get("sgpr_spill_count", 0) > MAX_SGPR_LANE_SPILLS}
+           or v.get("sgpr_spill_count", 0) > _lane_spill_limit(k)}
     assert not bad, f"kernels with scratch or spills (bytes/lane, vgpr spills, sgpr spills): {bad}"
-    lane_spills = {k: v.get("sgpr_spill_count", 0) for k, v in kernels.items() if v.get("sgpr_spill_count", 0)}
-    assert all("prefill_mfma_kernel" in k for k in lane_spills), lane_spills
