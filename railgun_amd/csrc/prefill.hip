@@ -1011,7 +1011,7 @@ __global__ __launch_bounds__(kPThreads, pf_wg_per_cu<D>()) void prefill_mfma_ker
 //    operand is 32 consecutive floats of a V row per half-wave (V tile row-major in LDS).
 //    Lane l accumulates O[query l % 32][d block b: 8 j + 4 h + r].
 template <int D, int GW>
-__global__ __launch_bounds__(kPThreads, 2) void prefill_f32_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPThreads, D > 128 ? 1 : 2) void prefill_f32_kernel(PrefillArgs a) {
   typedef float f32x16 __attribute__((ext_vector_type(16)));
   constexpr int QS = kPWaves / GW;      // 32-row subtiles per unit
   constexpr int UR = kPT * QS;          // rows per unit
@@ -1295,9 +1295,9 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
     }
     return check_launch(op);
   }
-  // The fp32 MFMA tile kernel: head_dim 64 / 128, any GQA ratio (GW as above), any block size,
-  // 16-byte aligned rows.
-  if (dtype == RG_DTYPE_F32 && (head_dim == 64 || head_dim == 128) &&
+  // The fp32 MFMA tile kernel: head_dim 64 / 128 / 256, any GQA ratio (GW as above), any block
+  // size, 16-byte aligned rows (at head_dim 256 one workgroup per CU: 128 KB of K/V buffers).
+  if (dtype == RG_DTYPE_F32 && (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
       max_blocks_per_seq > 0 && num_seqs <= 65535 && aligned16(query) && aligned16(key_cache) &&
       aligned16(value_cache) && aligned16(output) && stride % 4 == 0) {
     const int64_t UR = (int64_t)kPT * (kPWaves / GW);
@@ -1313,7 +1313,8 @@ extern "C" int rg_prefill_packed(const void* query, const void* key_cache, const
       else if (GW == 2) go(dtag, std::integral_constant<int, 2>{});
       else go(dtag, std::integral_constant<int, 1>{});
     };
-    if (head_dim == 128) go_gw(std::integral_constant<int, 128>{});
+    if (head_dim == 256) go_gw(std::integral_constant<int, 256>{});
+    else if (head_dim == 128) go_gw(std::integral_constant<int, 128>{});
     else go_gw(std::integral_constant<int, 64>{});
     return check_launch(op);
   }

@@ -396,12 +396,13 @@ def test_prefill_column_schedule_past_64_rounds(device, kernels):
     assert_close(dev_f32(out[torch.from_numpy(rows).long().to(device)]), want, dt, "sampled rows")
 
 
-@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("G", [1, 2, 4, 8])
 def test_prefill_mfma_head_dim256(device, kernels, dt, G):
-    """head_dim 256 on the 16-bit MFMA kernel (one workgroup per CU, a four-stage ring), every
-    GQA grouping (one, two and four heads per workgroup): fresh and chunked sequences, a row
-    shorter than a tile, blocks of 16 and 32 tokens, every row against the oracle."""
+    """head_dim 256 on the MFMA kernels (16-bit: one workgroup per CU, a four-stage ring; fp32:
+    one workgroup per CU, two 64 KB K/V buffers), every GQA grouping (one, two and four heads
+    per workgroup): fresh and chunked sequences, a row shorter than a tile, blocks of 16 and 32
+    tokens, every row against the oracle."""
     hkv = 2
     lens = np.array([1, 33, 100, 250], np.int32)
     prior = np.array([0, 40, 0, 300], np.int32)
@@ -415,10 +416,12 @@ def test_prefill_mfma_head_dim256(device, kernels, dt, G):
         _run(device, kernels, w, seed=2561 + G + bs)
 
 
-def test_prefill_head_dim256_many_units(device, kernels):
-    """head_dim 256 with several units per workgroup: 16 / 4 heads (4 head groups, 64 workgroups
-    each on a 256-CU device), 8 sequences of 400-1,500 rows after up to 500 cached positions
-    (~220 units per group), sampled rows of every sequence against the oracle."""
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_prefill_head_dim256_many_units(device, kernels, dt):
+    """head_dim 256 with several units per workgroup (16-bit: 4 head groups, 64 persistent
+    workgroups each on a 256-CU device): 16 / 4 heads, 8 sequences of 400-1,500 rows after up to
+    500 cached positions (~220 units per group), sampled rows of every sequence against the
+    oracle."""
     rng = np.random.default_rng(2562)
     lens = rng.integers(400, 1500, 8, endpoint=True).astype(np.int32)
     prior = rng.integers(0, 500, 8, endpoint=True).astype(np.int32)
@@ -426,6 +429,6 @@ def test_prefill_head_dim256_many_units(device, kernels):
     mb = int(((ctx + 15) // 16).max())
     nb = int(((ctx + 15) // 16).sum()) + 8
     bt = wl.assign_blocks(ctx, 16, nb, mb, rng)
-    w = wl.PrefillWorkload("d256_many", "bf16", 16, 4, 256, 16, nb, lens, bt, 2562, prior=prior)
+    w = wl.PrefillWorkload("d256_many", dt, 16, 4, 256, 16, nb, lens, bt, 2562, prior=prior)
     assert int(((lens + 31) // 32).sum()) > 3 * 64
     _run(device, kernels, w, seed=2563, row_sample=True, row_stride=97)
