@@ -73,7 +73,17 @@ struct GemmArgs {
   // NORM kernels: X rows are RMS-normalised with this weight [K] (see the kernel).
   const uint16_t* norm_w;
   float norm_eps;
+  int32_t stagger;  // 1: workgroups start their K loop at staggered chunks (see the kernel)
 };
+
+// Weights from this size on run with staggered chunk order: measured at the Llama-3.2-1B
+// projections (paired runs, 128 / 1 rows), gate/up (67 MB) -6.5 / -16 %, the LM head (525 MB)
+// -3.5 / -5.5 %, down (34 MB) -1.4 / -5 %, while qkv (12.6 MB) and o_proj (8.4 MB) were 1-4 %
+// slower staggered.
+#ifndef RG_GEMM_STAGGER_MIN_BYTES
+#define RG_GEMM_STAGGER_MIN_BYTES (16ll << 20)
+#endif
+int32_t stagger_for(int32_t N, int32_t K) { return (int64_t)N * K * 2 >= RG_GEMM_STAGGER_MIN_BYTES ? 1 : 0; }
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -246,9 +256,18 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
     const int row = 4 * (w * NB + q) + (lane >> 4);
     woff[q] = (uint32_t)(row * a.ldw * 2 + (((lane & 15) ^ (row & 15)) << 4));
   }
+  // With a.stagger, loop position c reads chunk (c + rot) mod chunks, rot = the workgroup's
+  // position among those of its die (workgroup b runs on XCD b mod 8): the workgroups of a die
+  // start at different chunks instead of all reading chunk c of their rows at once (X and W
+  // rows are K * 2 bytes apart, so chunk c of every row tends to fall in the same L2 channel).
+  const int rot = a.stagger && chunks > 0 ? (int)((blockIdx.x >> 3) % (unsigned)chunks) : 0;
+  auto chunk_of = [&](int c) __attribute__((always_inline)) {
+    const int cc = c + rot;
+    return cc >= chunks ? cc - chunks : cc;
+  };
   auto issue = [&](int c) __attribute__((always_inline)) {
     const uint32_t slot = lds_base + (uint32_t)((c % RG::SLOTS) * RG::SLOT);
-    const int64_t kb = (int64_t)c * kChunkBytes;
+    const int64_t kb = (int64_t)chunk_of(c) * kChunkBytes;
 #pragma unroll
     for (int q = 0; q < MB; ++q) lds_dma16_s(xbase + kb, xoff[q], slot + (w * MB + q) * 1024);
 #pragma unroll
@@ -302,7 +321,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
     constexpr bool SCALE_W = NB < MB || std::is_same<T, f16_t>::value;
     float nw[8];  // the norm weight of this lane's 8 k
     if constexpr (NORM) {
-      const uint4 u = *reinterpret_cast<const uint4*>(lds + RG::BYTES + (cb + c) * kChunkBytes + (4 * w + g) * 16);
+      const uint4 u = *reinterpret_cast<const uint4*>(lds + RG::BYTES + (cb + chunk_of(c)) * kChunkBytes + (4 * w + g) * 16);
       unpack8<T>(u, nw);
       if constexpr (SCALE_W) {
 #pragma unroll
@@ -623,6 +642,7 @@ int linear_entry(const char* op, const void* x, const void* weight, void* out, i
   }
   GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
              static_cast<float*>(workspace), M, N, K, ldx, ldw, ldo, plan.mtiles, plan.xcd};
+  a.stagger = stagger_for(N, K);
   hipStream_t s = as_stream(stream);
   if (dtype == RG_DTYPE_BF16) launch_gemm<bf16_t, EPI>(a, plan.nb, plan.mb, plan.splits, s);
   else launch_gemm<f16_t, EPI>(a, plan.nb, plan.mb, plan.splits, s);
@@ -654,6 +674,7 @@ int silu_mul_entry(const char* op, const void* x, const void* norm_weight, float
              static_cast<uint16_t*>(out), nullptr, M, 2 * I, K, ldx, ldw, ldo, plan.mtiles, plan.xcd};
   a.norm_w = static_cast<const uint16_t*>(norm_weight);
   a.norm_eps = eps;
+  a.stagger = stagger_for(2 * I, K);
   hipStream_t s = as_stream(stream);
   if (norm) {
     if (dtype == RG_DTYPE_BF16) launch_gemm_silu_mul<bf16_t, true>(a, plan.nb, plan.mb, s);
@@ -697,7 +718,8 @@ int qkv_rope_entry(const char* op, const void* x, const void* norm_weight, float
   GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight_qkv), static_cast<uint16_t*>(q_out),
              nullptr, M, N, K, ldx, ldw, ldq, plan.mtiles, plan.xcd,
              cos_sin, positions, slot_mapping, static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
-             kv_stride, num_heads, num_kv_heads, block_size, static_cast<const uint16_t*>(norm_weight), eps};
+             kv_stride, num_heads, num_kv_heads, block_size, static_cast<const uint16_t*>(norm_weight), eps,
+             stagger_for(N, K)};
   hipStream_t s = as_stream(stream);
   if (norm) {
     if (dtype == RG_DTYPE_BF16) launch_gemm_rope<bf16_t, true>(a, nb, plan.mb, s);
