@@ -707,12 +707,13 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 // unit b covering blocks [b * BPU, b * BPU + BPU) of the sequence (sk_bpu: 1 at head_dim 128,
 // 4 at head_dim 64, 2 at head_dim 64 with G >= 8); segment g = s * num_kv_heads + kvh is the
 // run of units of one (s, kv-head).
-// Worker k (one wave) takes units [k*U/W, (k+1)*U/W) of the U units, so every wave streams
-// the same number of units whatever the context lengths are.  A worker emits one partial
+// Worker k (one wave) takes a contiguous range of the U units, the k-th of W equal shares of
+// their cost (the units' bytes plus a fixed cost per segment start, see the kernel), so every
+// wave streams the same work whatever the context lengths are.  A worker emits one partial
 // (m, l, acc) for every segment it touches, at partial index k + g (distinct for all
 // (worker, segment) pairs because each worker's segments and each segment's workers are
-// consecutive).  decode_stream_merge_kernel combines the partials of each segment.  When
-// U < W only the first U workers are used, so every worker of a segment's range owns units.
+// consecutive).  decode_stream_merge_kernel combines the partials of each segment.  With few
+// units only the first workers are used, so every worker of a segment's range owns units.
 
 // Units in flight ahead of the one being computed, per stream-K worker.  The workers are
 // one wave per SIMD (RG_SK_WAVES_PER_CU = 4): two waves sharing a SIMD progress at
@@ -778,9 +779,14 @@ struct StreamArgs {
   int32_t bs_shift;      // block_size = 16 << bs_shift
 };
 
-__device__ __forceinline__ int64_t worker_start(int64_t k, int64_t U, int64_t W) { return k * U / W; }
-// The worker whose range contains unit u (the last k with worker_start(k) <= u).
-__device__ __forceinline__ int64_t worker_of(int64_t u, int64_t U, int64_t W) { return ((u + 1) * W - 1) / U; }
+// Cost of a segment start, in KB of K/V streaming.  A worker's end time tracks the segments it
+// touches (per-worker timestamps at config 2, 1,024 workers of ~69 units: each extra segment
+// start -- q load, partial write, the pipeline's restart -- ends the worker ~1.6 us later, about
+// 10 KB of its stream), so the split evens out (unit KB) x units + RG_SK_SEG_COST_KB x segment
+// starts instead of units alone.  0: units only.
+#ifndef RG_SK_SEG_COST_KB
+#define RG_SK_SEG_COST_KB 10
+#endif
 
 // 16-token sub-blocks of sequence s: ceil(ctx/16) per kv-head (context clamped to the table
 // row, max_blocks of them).
@@ -811,32 +817,6 @@ __device__ __forceinline__ int64_t wave_incl_scan(int64_t v, int lane) {
   return v;
 }
 
-// Total units U and, if `target` >= 0, the sequence containing unit `target` and the first
-// unit of that sequence.  Every lane returns the same values.
-template <int BPU>
-__device__ __forceinline__ int64_t scan_units(const int32_t* ctxl, int batch, int max_blocks, int hkv,
-                                              int lane, int64_t target, int& seq_out, int64_t& seq_start) {
-  int64_t base = 0;
-  seq_out = -1;
-  seq_start = 0;
-  for (int c0 = 0; c0 < batch; c0 += 64) {
-    const int s = c0 + lane;
-    const int64_t n = s < batch ? (int64_t)seq_units<BPU>(ctxl, s, max_blocks) * hkv : 0;
-    const int64_t incl = wave_incl_scan(n, lane) + base;
-    const int64_t excl = incl - n;
-    if (target >= 0 && seq_out < 0) {
-      const uint64_t hit = __ballot(n > 0 && excl <= target && target < incl);
-      if (hit) {
-        const int l = __ffsll((unsigned long long)hit) - 1;
-        seq_out = c0 + l;
-        seq_start = __shfl(excl, l, 64);
-      }
-    }
-    base = __shfl(incl, 63, 64);
-  }
-  return base;
-}
-
 template <typename T, int D, int G>
 __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
     StreamArgs a, const typename DecodeTileFor<T, D, G>::S* __restrict__ q_ptr,
@@ -856,35 +836,131 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   const int lane = threadIdx.x;
   const int64_t k = blockIdx.x;
   const int hkv = a.num_kv_heads;
-  // Total units U, this worker's range [u0, u1) and the sequence holding u0.  Up to 64
-  // sequences take one pass (one context length per lane); larger batches scan twice.
-  int64_t U, W, u0, u1, seq_start;
-  int s;
-  if (a.batch <= 64) {
-    const int64_t n = lane < a.batch ? (int64_t)seq_units<BPU>(context_lens, lane, a.max_blocks) * hkv : 0;
-    const int64_t incl = wave_incl_scan(n, lane);
-    const int64_t excl = incl - n;
-    U = uniform64(__shfl(incl, 63, 64));
-    // With fewer units than workers only the first U workers run (one unit each), so that
-    // every worker between a segment's first and last one owns a unit and writes a partial.
-    W = min<int64_t>(a.num_workers, U);
+  // Total units U, this worker's range [u0, u1) and the sequence holding u0: one pass over
+  // the context lengths for up to 64 sequences (one per lane), two for larger batches.
+  //
+  // The split evens out cost, not units: unit u of segment g (segments numbered over the
+  // non-empty ones, in unit order) sits at z(u) = KQ u + KS (g + 1), KQ its K/V kilobytes and KS
+  // a segment start's (RG_SK_SEG_COST_KB; with 0, KQ = 1 and the split is by units), and of the
+  // total C = KQ U + KS S worker k takes the units with k C / W <= z(u) < (k + 1) C / W.
+  // Consecutive z are at most KQ + KS apart, so with W <= C / (KQ + KS) every worker owns a unit
+  // (with fewer units than workers, only the first workers run), as the merge's segment ranges
+  // need.
+  constexpr int64_t KS = RG_SK_SEG_COST_KB;
+  constexpr int64_t KQ = KS > 0 ? (int64_t)BPU * kBS * D * sizeof(typename Tile::S) * 2 / 1024 : 1;
+  static_assert(KQ >= 1, "unit cost");
+  int64_t C, W, u0, u1, seq_start;
+  int s, seq_seg;  // the sequence holding u0 and the index of its first segment
+  // Lanes below this one whose sequence has units (a sequence's segments all do or all don't).
+  auto below = [&](bool f) __attribute__((always_inline)) -> int {
+    const uint64_t m = __ballot(f);
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+  };
+  // The first unit at or after cost x in a sequence of nb units per kv-head whose costs start
+  // at cx and units at ex (j == nb: the next segment's first unit).  The offset into one
+  // sequence fits 32 bits for any table the device holds; the division is done in 32 bits then.
+  auto unit_in = [&](int64_t x, int64_t cx, int64_t ex, int64_t nb) __attribute__((always_inline)) -> int64_t {
+    const int64_t seg = KS + KQ * nb, o = x - cx;
+    const int64_t kv = (o >> 31) == 0 && (seg >> 31) == 0 ? (int64_t)((uint32_t)o / (uint32_t)seg) : o / seg;
+    const int64_t r = o - kv * seg;
+    const int64_t j = r <= KS ? 0 : (r - KS + KQ - 1) / KQ;
+    return ex + kv * nb + j;
+  };
+  // k C / W in 32 bits when it fits.
+  auto share = [&](int64_t kk) __attribute__((always_inline)) -> int64_t {
+    const int64_t v = kk * C;
+    return (v >> 32) == 0 ? (int64_t)((uint32_t)v / (uint32_t)W) : v / W;
+  };
+  {
+    // First pass over the sequences, 64 per step: the totals U and C.  A batch of up to 64 keeps
+    // its lane values (units n, inclusive unit scan, non-empty sequences below) for the second.
+    int64_t U = 0, ne = 0, n1 = 0, incl1 = 0, nb1 = 0;
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+      const int q = c0 + lane;
+      const int64_t n = q < a.batch ? (int64_t)seq_units<BPU>(context_lens, q, a.max_blocks) * hkv : 0;
+      const int64_t incl = wave_incl_scan(n, lane) + U;
+      if (c0 == 0) {
+        n1 = n;
+        incl1 = incl;
+        nb1 = below(n > 0);
+      }
+      U = uniform64(__shfl(incl, 63, 64));
+      ne += __builtin_popcountll(__ballot(n > 0));
+    }
+    C = KQ * U + KS * hkv * ne;
+    W = min<int64_t>(a.num_workers, C / (KQ + KS));
     if (k >= W) return;
-    u0 = worker_start(k, U, W);
-    u1 = worker_start(k + 1, U, W);
-    const uint64_t hit = __ballot(n > 0 && excl <= u0 && u0 < incl);
-    s = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)hit) - 1);
-    seq_start = uniform64(__shfl(excl, s, 64));
-  } else {
-    int s_dummy;
-    int64_t st_dummy;
-    U = uniform64(scan_units<BPU>(context_lens, a.batch, a.max_blocks, hkv, lane, -1, s_dummy, st_dummy));
-    W = min<int64_t>(a.num_workers, U);
-    if (k >= W) return;
-    u0 = worker_start(k, U, W);
-    u1 = worker_start(k + 1, U, W);
-    scan_units<BPU>(context_lens, a.batch, a.max_blocks, hkv, lane, u0, s, seq_start);
+    // Second pass: the units at costs x0 = k C / W and x1 = (k + 1) C / W (the last worker ends at
+    // U), and the sequence holding u0 with the index of its first segment.
+    const int64_t x0 = share(k), x1 = k + 1 < W ? share(k + 1) : C;
+    u0 = U;
+    u1 = U;
+    s = -1;
+    seq_start = 0;
+    seq_seg = 0;
+    bool rolled = false;  // u0 is the first unit past the sequence whose costs hold x0
+    bool need1 = x1 < C;
+    auto resolve = [&](int c0, int64_t n, int64_t incl, int64_t nb_) __attribute__((always_inline)) {
+      const int64_t excl = incl - n;
+      const int64_t cexcl = KQ * excl + KS * hkv * nb_, cincl = cexcl + (n > 0 ? KQ * n + KS * hkv : 0);
+      if (s < 0) {
+        const uint64_t h = __ballot(n > 0 && cexcl <= x0 && x0 < cincl);
+        if (h) {
+          const int l = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)h) - 1);
+          const int64_t el = uniform64(__shfl(excl, l, 64)), nl = uniform64(__shfl(n, l, 64));
+          u0 = unit_in(x0, uniform64(__shfl(cexcl, l, 64)), el, nl / hkv);
+          s = c0 + l;
+          seq_start = el;
+          seq_seg = (int)(hkv * uniform64(__shfl(nb_, l, 64)));
+          rolled = u0 == el + nl;
+        }
+      }
+      if (need1) {
+        const uint64_t h = __ballot(n > 0 && cexcl <= x1 && x1 < cincl);
+        if (h) {
+          const int l = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)h) - 1);
+          u1 = unit_in(x1, uniform64(__shfl(cexcl, l, 64)), uniform64(__shfl(excl, l, 64)),
+                       uniform64(__shfl(n, l, 64)) / hkv);
+          need1 = false;
+        }
+      }
+    };
+    if (a.batch <= 64) {
+      resolve(0, n1, incl1, nb1);
+    } else {
+      int64_t ub = 0, nb = 0;
+      for (int c0 = 0; c0 < a.batch && (s < 0 || need1); c0 += 64) {
+        const int q = c0 + lane;
+        const int64_t n = q < a.batch ? (int64_t)seq_units<BPU>(context_lens, q, a.max_blocks) * hkv : 0;
+        const int64_t incl = wave_incl_scan(n, lane) + ub;
+        resolve(c0, n, incl, nb + below(n > 0));
+        ub = uniform64(__shfl(incl, 63, 64));
+        nb += __builtin_popcountll(__ballot(n > 0));
+      }
+    }
+    if (rolled) {
+      // u0 is the first unit of a later sequence (a share boundary in the cost of a sequence's
+      // last unit, past its start): find that sequence by units.
+      int64_t ub = 0, nb = 0;
+      s = -1;
+      for (int c0 = 0; c0 < a.batch && s < 0; c0 += 64) {
+        const int q = c0 + lane;
+        const int64_t n = q < a.batch ? (int64_t)seq_units<BPU>(context_lens, q, a.max_blocks) * hkv : 0;
+        const int64_t incl = wave_incl_scan(n, lane) + ub, excl = incl - n;
+        const int64_t nb_ = nb + below(n > 0);
+        const uint64_t h = __ballot(n > 0 && excl <= u0 && u0 < incl);
+        if (h) {
+          const int l = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)h) - 1);
+          s = c0 + l;
+          seq_start = uniform64(__shfl(excl, l, 64));
+          seq_seg = (int)(hkv * uniform64(__shfl(nb_, l, 64)));
+        }
+        ub = uniform64(__shfl(incl, 63, 64));
+        nb += __builtin_popcountll(__ballot(n > 0));
+      }
+    }
     s = __builtin_amdgcn_readfirstlane(s);
-    seq_start = uniform64(seq_start);
+    seq_seg = __builtin_amdgcn_readfirstlane(seq_seg);
   }
 
   // Cursor of the unit being computed and of the unit being loaded: sequence, kv-head, unit b
@@ -903,6 +979,9 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
     cur.kvh = __builtin_amdgcn_readfirstlane(r / cur.nblk);
     cur.b = __builtin_amdgcn_readfirstlane(r - cur.kvh * cur.nblk);
   }
+  // Index g of the current segment among the non-empty ones (a sequence's costs start at
+  // KQ x its first unit + KS x the segments before it), moved on at each segment end.
+  int seg = seq_seg + cur.kvh;
   // Every lambda of the kernel is forced inline: one left out of line is called with its
   // captures in scratch memory (G = 16, and D = 64 with G = 8, spilled that way).
   auto advance = [&](Cursor& c) __attribute__((always_inline)) {
@@ -976,7 +1055,9 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
     tile.load_q(q_ptr + ((int64_t)c.s * H + (int64_t)c.kvh * G) * D);
     tile.reset();
     if (c.b == 0 && lane == 0) {
-      const int64_t last = worker_of(ubeg + c.nblk - 1, U, W);
+      // The worker of the segment's last unit (the last k with k C / W <= its cost).
+      const int64_t z = KQ * (ubeg + c.nblk - 1) + KS * (seg + 1);
+      const int64_t last = ((z + 1) * W - 1) / C;
       a.seg_desc[(int64_t)c.s * hkv + c.kvh] = make_int2((int)k, (int)(last - k + 1));
     }
   };
@@ -1046,6 +1127,7 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
     if (last_of_segment) {
       end_segment(cur);
       if (j + 1 < n) {
+        ++seg;
         advance(cur);
         begin_segment(cur, u0 + j + 1);
         ctx_cur = min(context_lens[cur.s], a.max_blocks * kBS);

@@ -166,6 +166,26 @@ def _threads() -> int:
     return max(1, min(16, len(os.sched_getaffinity(0))))
 
 
+@pytest.mark.parametrize("B", [60, 130])
+def test_stream_cost_split_short_and_empty_sequences(device, kernels, B):
+    """The stream-K split by cost (units plus a fixed cost per segment start) on short contexts
+    U[1, 600] with a fifth of the sequences empty, 8 / 2 heads, D 128: batches of up to 64 (one
+    pass over the context lengths) and above (chunked passes).  On a 256-CU device the shapes
+    put 18 (B 60, where the cost caps the workers at 909) and 22 (B 130) workers' share
+    boundaries past the last unit of a sequence, so that their ranges start at a later
+    sequence, and send several workers across empty sequences.  Against the oracle."""
+    rng = np.random.default_rng(B)
+    ctx = rng.integers(1, 600, B, endpoint=True).astype(np.int32)
+    ctx[rng.random(B) < 0.2] = 0
+    inp = _big_decode_inputs(device, ctx, "bf16", 8, 2, 128, seed=B + 7, mb=64)
+    assert _stream_units(ctx, 2, 1) > _stream_workers(device)
+    want = orc.cpu_attention_gathered(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"], "bf16",
+                                      nthreads=_threads())
+    got = gpu_v1(kernels, inp, True)
+    assert not np.isnan(got).any()
+    assert_close(got, want, "bf16", f"B={B}")
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 def test_stream_head_dim64_many_units_per_worker(device, kernels, dt):
     """The attention of BASELINE config 5 (Llama-3.2-1B: 32 / 8 heads, head_dim 64, 128 sequences
