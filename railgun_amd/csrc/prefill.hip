@@ -507,44 +507,18 @@ __global__ __launch_bounds__(kPThreads, pf_wg_per_cu<D>()) void prefill_mfma_ker
   // With columns (sched_cols = C > 0) the snake runs over the C columns instead (round r of
   // column c: position r * C + c, or r * C + C - 1 - c), and the column's first 64 rounds are
   // split between its three workgroups (slot qw / C, dispatch order) by the weighted greedy
-  // above, which every workgroup of the column computes alike from its own copy of the
-  // tables.  Rounds from 64 on go to the slots in turn.  Each wave keeps this state in LDS,
+  // of RG_PF_SLOT_W*, which every workgroup of the column computes alike from its own copy of
+  // the tables.  Rounds from 64 on go to the slots in turn.  Each wave keeps this state in LDS,
   // not in registers (the kernel is at its scalar-register limit): the rounds of the first 64
-  // it has not yet taken (`sched_mine`) and (C, column, its next round from 64 on).
+  // it has not yet taken (`sched_mine`) and (C, column, its next round from 64 on).  Rounds 0, 1
+  // and 2 go to slots 0, 1 and 2 (what the greedy gives anyway for items longest first when
+  // F0 < F1 < F2 < 2 F0), so a workgroup knows its first item before the greedy runs: it
+  // resolves that item and sends its loads out first, and the greedy runs while they are in
+  // flight.
   __shared__ uint64_t sched_mine[kPWaves];
   __shared__ int4 sched_colw[kPWaves];
-  {
-    const int cols = sorted ? a.sched_cols : 0;
-    const int col = cols > 0 ? qw % cols : 0, slot = cols > 0 ? qw / cols : 0;
-    uint64_t mine = 0;
-    const int u = lane * cols + ((lane & 1) ? cols - 1 - col : col);
-    int cost = 0;
-    if (cols > 0 && u < n_items) {
-      int lo = 1, hi = kb;  // the item's key, as in resolve
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (sched_b[mid] > u) lo = mid;
-        else hi = mid - 1;
-      }
-      cost = lo * QS + RG_PF_UNIT_COST;
-    }
-    constexpr int F0 = RG_PF_SLOT_W1 * RG_PF_SLOT_W2, F1 = RG_PF_SLOT_W0 * RG_PF_SLOT_W2,
-                  F2 = RG_PF_SLOT_W0 * RG_PF_SLOT_W1;
-    int l0 = 0, l1 = 0, l2 = 0;
-    for (int i = 0; i < 64; ++i) {
-      const int c = __builtin_amdgcn_readlane(cost, i);
-      if (c == 0) break;  // past the column's last item
-      // finish times (l_s + c) / w_s, compared as (l_s + c) * (product of the other weights)
-      const int f0 = (l0 + c) * F0, f1 = (l1 + c) * F1, f2 = (l2 + c) * F2;
-      const int sl = f0 <= f1 ? (f0 <= f2 ? 0 : 2) : (f1 <= f2 ? 1 : 2);
-      if (sl == 0) l0 += c;
-      else if (sl == 1) l1 += c;
-      else l2 += c;
-      if (sl == slot) mine |= 1ull << i;
-    }
-    sched_mine[w] = mine;
-    sched_colw[w] = make_int4(cols, col, 64 + slot, 0);
-  }
+  const int cols = sorted ? a.sched_cols : 0;
+  if (cols == 0) sched_colw[w] = make_int4(0, 0, 0, 0);
   int round = 0;
   auto take_item = [&]() -> int {
     const int4 cw = sched_colw[w];
@@ -567,8 +541,9 @@ __global__ __launch_bounds__(kPThreads, pf_wg_per_cu<D>()) void prefill_mfma_ker
   };
 
   // Per-unit registers, loaded ahead of the unit: the block-table window and the Q^T operand
-  // (lane holds q[query j][16i + 8hh .. +8] for every d chunk i; zero for rows without a
-  // position).  Window: lane i holds the cache addresses, in units of 16 rows (16 D elements),
+  // (lane holds q[query j][16i + 8hh .. +8] for every d chunk i; a row without a position
+  // holds the unit's first row instead: its scores stay finite and its output is written as
+  // zeros, and no select on the loaded value makes the load wait where it is issued).  Window: lane i holds the cache addresses, in units of 16 rows (16 D elements),
   // of this kv-head's rows of 16-token sub-blocks 2 wb + i and 2 wb + 64 + i (clamped to the
   // unit's last sub-block), i.e. of key tiles wb .. wb + 63, so a tile's two sub-block addresses
   // are v_readlane's and a copy's address is one multiply by a constant.  Sub-block v lies in
@@ -583,12 +558,22 @@ __global__ __launch_bounds__(kPThreads, pf_wg_per_cu<D>()) void prefill_mfma_ker
     asm volatile("" : "+s"(wp));
     const int sh = (int)(wp & 7u);
     const int v0 = min(2 * wbase + lane, last_sub), v1 = min(2 * wbase + 64 + lane, last_sub);
-    // Unsigned 32-bit: the address of the pool's last row in units of 16 D elements is below
-    // 2^32 for any pool the device holds (2^32 * 32 D bytes is 8 TB at head_dim 64).
+    // The raw block numbers: finish_window turns them into addresses once they have landed, so
+    // no wait for them falls where the loads are issued (the set-up, or before an epilogue).
+    btw0 = bt[v0 >> sh];
+    btw1 = bt[v1 >> sh];
+  };
+  // Unsigned 32-bit: the address of the pool's last row in units of 16 D elements is below
+  // 2^32 for any pool the device holds (2^32 * 32 D bytes is 8 TB at head_dim 64).
+  auto finish_window = [&](int wbase, int last_sub) {
+    uint32_t wp = a.win_param;
+    asm volatile("" : "+s"(wp));
+    const int sh = (int)(wp & 7u);
+    const int v0 = min(2 * wbase + lane, last_sub), v1 = min(2 * wbase + 64 + lane, last_sub);
     const uint32_t head = (uint32_t)kvh << sh;  // the kv-head's first sub-block within a block
     const uint32_t spb = wp >> 3, sm = (1u << sh) - 1u;
-    btw0 = (int)((uint32_t)bt[v0 >> sh] * spb + head + ((uint32_t)v0 & sm));
-    btw1 = (int)((uint32_t)bt[v1 >> sh] * spb + head + ((uint32_t)v1 & sm));
+    btw0 = (int)((uint32_t)btw0 * spb + head + ((uint32_t)v0 & sm));
+    btw1 = (int)((uint32_t)btw1 * spb + head + ((uint32_t)v1 & sm));
   };
   auto load_unit = [&](const Unit& un) {
     const int q0 = un.t * UR;
@@ -598,18 +583,68 @@ __global__ __launch_bounds__(kPThreads, pf_wg_per_cu<D>()) void prefill_mfma_ker
     if (pos_max >= 0) load_window(un, 0, pos_max / kBlk);
     const uint4* qr = reinterpret_cast<const uint4*>(q + ((int64_t)(un.row0 + (row_ok ? wq0 + j : 0)) * H + head) * D);
 #pragma unroll
-    for (int i = 0; i < NKC; ++i) qb[i] = row_ok ? qr[2 * i + hh] : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < NKC; ++i) qb[i] = qr[2 * i + hh];
   };
 
   Unit cur{};
   bool have = false;
-  for (int u = take_item(); u < n_items; u = take_item()) {
-    if (resolve(u, cur)) {
-      have = true;
-      break;
+  if (cols > 0) {
+    const int col = qw % cols, slot = qw / cols;
+    const int u = slot * cols + ((slot & 1) ? cols - 1 - col : col);  // round `slot` of the column
+    have = u < n_items && resolve(u, cur);
+  } else {
+    for (int u = take_item(); u < n_items; u = take_item()) {
+      if (resolve(u, cur)) {
+        have = true;
+        break;
+      }
     }
   }
   if (have) load_unit(cur);
+  // The split is computed by wave 0 alone, for the four waves (the greedy is a chain of scalar
+  // instructions, and the CU's scalar unit serves all its waves), then published with a barrier
+  // that waits for the LDS writes only (__syncthreads would also wait for the first unit's
+  // loads, which are to land during the greedy).
+  if (cols > 0 && w == 0) {
+    const int col = qw % cols, slot = qw / cols;
+    uint64_t mine = 0;
+    const int u = lane * cols + ((lane & 1) ? cols - 1 - col : col);
+    int cost = 0;
+    if (u < n_items) {
+      int lo = 1, hi = kb;  // the item's key, as in resolve
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (sched_b[mid] > u) lo = mid;
+        else hi = mid - 1;
+      }
+      cost = lo * QS + RG_PF_UNIT_COST;
+    }
+    constexpr int F0 = RG_PF_SLOT_W1 * RG_PF_SLOT_W2, F1 = RG_PF_SLOT_W0 * RG_PF_SLOT_W2,
+                  F2 = RG_PF_SLOT_W0 * RG_PF_SLOT_W1;
+    int l0 = 0, l1 = 0, l2 = 0;
+    for (int i = 0; i < 64; ++i) {
+      const int c = __builtin_amdgcn_readlane(cost, i);
+      if (c == 0) break;  // past the column's last item
+      // Finish times (l_s + c) / w_s, compared as (l_s + c) * (product of the other weights),
+      // times 4 plus the slot: one minimum picks the slot, ties going to the lower one, all in
+      // scalar instructions.  (< 2^31: l_s + c <= 64 (4 kb + 3).)
+      const int sl = i < 3 ? i
+                           : min(min((l0 + c) * (4 * F0), (l1 + c) * (4 * F1) + 1), (l2 + c) * (4 * F2) + 2) & 3;
+      l0 += sl == 0 ? c : 0;
+      l1 += sl == 1 ? c : 0;
+      l2 += sl == 2 ? c : 0;
+      mine |= (uint64_t)(sl == slot) << i;
+    }
+    if (lane < kPWaves) {
+      sched_mine[lane] = mine & ~(1ull << slot);  // round `slot`: the first item, already taken
+      sched_colw[lane] = make_int4(cols, col, 64 + slot, 0);
+    }
+  }
+  if (cols > 0) {
+    wave_lds_fence();
+    tile_barrier();
+  }
+
   while (have) {
   const int row0 = cur.row0;
   const int q0 = cur.t * UR;                   // first query of the unit (within the sequence)
@@ -623,6 +658,7 @@ __global__ __launch_bounds__(kPThreads, pf_wg_per_cu<D>()) void prefill_mfma_ker
   int wb = 0;
   // Q and the window have landed; nothing else is in flight.
   __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
+  if (pos_max >= 0) finish_window(0, pos_max / kBlk);
   constexpr uint32_t kSubBytes = kBlk * D * 2;  // one window unit: 16 rows
   const int nkt = pos_max >= 0 ? pos_max / kPT + 1 : 0;
   const uint32_t lds_base = (uint32_t)(uintptr_t)((RG_LDS char*)lds);
@@ -933,6 +969,7 @@ __global__ __launch_bounds__(kPThreads, pf_wg_per_cu<D>()) void prefill_mfma_ker
   wb += 64;
   load_window(cur, wb, pos_max / kBlk);
   __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
+  finish_window(wb, pos_max / kBlk);
   }
 
   // Every wave is done with the LDS stages after the barrier; the next unit's Q and window
