@@ -577,3 +577,29 @@ def test_stream_fp32_config2_shape(device, kernels):
     assert_close(gpu_v1(kernels, inp, True), want, "f32", "v1 stream-K")
     assert_close(gpu_v1(kernels, inp, True, "v1_plus"), want, "f32", "v1_plus stream-K")
     assert_close(gpu_v2(kernels, inp, 512), want, "f32", "v2")
+
+
+def test_stream_random_shapes(device, kernels):
+    """Twenty seeded random decode batches through the stream-K entry with a workspace, against
+    the oracle: batch 1-150 (one pass over the context lengths and the chunked passes), a quarter
+    of them with empty sequences, contexts up to 3,000 tokens, GQA 1 / 2 / 3 / 4 / 8, head_dim 64
+    / 128, block sizes 16 / 32, bf16 and fp32 — loads from a few units per worker to tens, so the
+    split by cost meets short segments, empty sequences and share boundaries at sequence ends."""
+    rng = np.random.default_rng(2024)
+    for case in range(20):
+        B = int(rng.integers(1, 151))
+        G = int(rng.choice([1, 2, 3, 4, 8]))
+        Hkv = int(rng.choice([1, 2, 4]))
+        D = int(rng.choice([64, 128]))
+        bs = int(rng.choice([16, 32]))
+        dt = "f32" if case % 4 == 3 else "bf16"
+        ctx = rng.integers(1, int(rng.choice([40, 600, 3000])), B, endpoint=True).astype(np.int32)
+        if case % 4 == 1:
+            ctx[rng.random(B) < 0.3] = 0
+        mb = int(max(1, (ctx.max() + bs - 1) // bs))
+        inp = _big_decode_inputs(device, ctx, dt, G * Hkv, Hkv, D, seed=3000 + case, mb=mb, bs=bs)
+        want = orc.cpu_attention_gathered(inp["q"], inp["kc"], inp["vc"], inp["bt"], inp["ctx"], inp["scale"], dt,
+                                          nthreads=_threads())
+        got = gpu_v1(kernels, inp, True)
+        assert not np.isnan(got).any(), f"case {case}"
+        assert_close(got, want, dt, f"case {case}: B={B} G={G} Hkv={Hkv} D={D} bs={bs} {dt}")

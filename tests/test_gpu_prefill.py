@@ -432,3 +432,26 @@ def test_prefill_head_dim256_many_units(device, kernels, dt):
     w = wl.PrefillWorkload("d256_many", dt, 16, 4, 256, 16, nb, lens, bt, 2562, prior=prior)
     assert int(((lens + 31) // 32).sum()) > 3 * 64
     _run(device, kernels, w, seed=2563, row_sample=True, row_stride=97)
+
+
+def test_prefill_random_shapes(device, kernels):
+    """Twelve seeded random packed batches, every row against the oracle: 1-24 sequences of
+    1-300 rows after 0-400 cached positions, GQA 1 / 2 / 3 / 4 / 8 over 1-4 kv-heads (head groups
+    that divide the CU count take the column split, the others the snake), head_dim 64 / 128,
+    blocks of 16 / 32 tokens, bf16, fp16 and fp32."""
+    rng = np.random.default_rng(4096)
+    for case in range(12):
+        S = int(rng.integers(1, 25))
+        G = int(rng.choice([1, 2, 3, 4, 8]))
+        hkv = int(rng.choice([1, 2, 4]))
+        D = int(rng.choice([64, 128]))
+        bs = int(rng.choice([16, 32]))
+        dt = ("bf16", "f16", "f32")[case % 3]
+        lens = rng.integers(1, 300, S, endpoint=True).astype(np.int32)
+        prior = np.where(rng.random(S) < 0.5, rng.integers(0, 400, S, endpoint=True), 0).astype(np.int32)
+        ctx = prior + lens
+        mb = int(((ctx + bs - 1) // bs).max())
+        nb = int(((ctx + bs - 1) // bs).sum()) + 2
+        bt = wl.assign_blocks(ctx, bs, nb, mb, rng)
+        w = wl.PrefillWorkload(f"random{case}", dt, G * hkv, hkv, D, bs, nb, lens, bt, 4096 + case, prior=prior)
+        _run(device, kernels, w, seed=5000 + case)
