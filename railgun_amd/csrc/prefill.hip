@@ -730,6 +730,12 @@ __global__ __launch_bounds__(kPThreads, pf_wg_per_cu<D>()) void prefill_mfma_ker
   // Tiles from here on may hold keys past one of this wave's queries (a wave without rows
   // masks against the unit's last position).
   const int kt_mask = (QS == 1 ? pos_min : min(pos_min, pos_max)) / kPT;
+  // With several row subtiles per unit (QS > 1) the unit's tiles run to its last row, past this
+  // wave's own last row: from tile kt_last + 1 on every key lies beyond all of this wave's rows,
+  // so the tile would add exact zeros (p = 0) and the wave only takes part in its copies and
+  // barrier, leaving the SIMD to the CU's other workgroups.  (-1: no row with a position.)
+  const int wave_last = pos_min + nq - 1;
+  const int kt_last = QS > 1 && nq > 0 && wave_last >= 0 ? wave_last / kPT : QS > 1 ? -1 : nkt;
   const int xor32_addr = (lane ^ 32) << 2;  // ds_bpermute address of the other half's lane
 
   // S^T = K Q^T of the tile in stage st: c[4jb + r] is key 8jb + 4hh + r for query j.  The K
@@ -958,12 +964,19 @@ __global__ __launch_bounds__(kPThreads, pf_wg_per_cu<D>()) void prefill_mfma_ker
   while (kt < nkt) {
   // Iterations whose refill tile kt + NST - 1 lies in the current block-table window.
   const int kend = min(nkt, wb + 65 - NST);
-  for (; kt < kend; ++kt) {
+  for (; kt < min(kend, kt_last + 1); ++kt) {
     // One copy of the tile per ring stage, so that each stage's LDS offsets are immediates.
     [&]<int... S>(std::integer_sequence<int, S...>) {
       ((st == S ? tile_step(kt, std::integral_constant<int, S>{}) : void()), ...);
     }(std::make_integer_sequence<int, NST>{});
     st = st == NST - 1 ? 0 : st + 1;
+  }
+  if constexpr (QS > 1) {
+    for (; kt < kend; ++kt) {  // tiles past this wave's rows: its copies and the barrier only
+      wait_for(kt);
+      if (kt + NST - 1 < nkt) issue_tile(kt + NST - 1, st == 0 ? NST - 1 : st - 1);
+      st = st == NST - 1 ? 0 : st + 1;
+    }
   }
   if (kt >= nkt) break;
   wb += 64;
@@ -1137,8 +1150,16 @@ __global__ __launch_bounds__(kPThreads, D > 128 ? 1 : 2) void prefill_f32_kernel
     for (int b = 0; b < NDB; ++b) o[b] = f32x16{};
     float m = -INFINITY, lsum = 0.f;
 
+    // With several row subtiles per unit (QS > 1) every key of tiles past kfull lies beyond this
+    // wave's own rows (their probabilities are exact zeros): there the wave only copies and
+    // meets the barrier.  (Not at head_dim 64, where the second bound does not fit the scalar
+    // registers.)
+    constexpr bool kSkip = QS > 1 && D >= 128;
+    const int wrow0 = unit * UR + sub * kPT;
+    const int wlast = first + min(wrow0 + kPT, L) - 1;
+    const int kfull = !kSkip ? ntiles : wrow0 < L && wlast >= 0 ? min(ntiles, wlast / kPT + 1) : 0;
     if (ntiles > 0) issue(0);
-    for (int kt = 0; kt < ntiles; ++kt) {
+    for (int kt = 0; kt < kfull; ++kt) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile kt
       tile_barrier();                                   // ... and every wave's
       if (kt + 1 < ntiles) issue(kt + 1);               // the buffer tile kt - 1 used
@@ -1188,6 +1209,13 @@ __global__ __launch_bounds__(kPThreads, D > 128 ? 1 : 2) void prefill_f32_kernel
             o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * b], st[4 * j + r], o[b], 0, 0, 0);
           }
         }
+    }
+    if constexpr (kSkip) {
+      for (int kt = kfull; kt < ntiles; ++kt) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        tile_barrier();
+        if (kt + 1 < ntiles) issue(kt + 1);
+      }
     }
     // The two halves of a query's row sum; rows without keys (or past the sequence) give 0.
     const float ltot = lsum + __shfl_xor(lsum, 32, 64);
