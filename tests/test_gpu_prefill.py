@@ -298,31 +298,36 @@ def test_prefill_repeated_launches_and_streams(device, kernels):
             assert np.array_equal(dev_f32(o), first)
 
 
-@pytest.mark.parametrize("D", [64, 128])
-def test_prefill_rows_without_position(device, kernels, D):
+@pytest.mark.parametrize("D,G,dt", [(64, 4, "bf16"), (128, 4, "bf16"), (128, 1, "bf16"), (128, 3, "bf16"),
+                                    (64, 2, "f16"), (128, 3, "f32"), (128, 1, "f32")])
+def test_prefill_rows_without_position(device, kernels, D, G, dt):
     """Context lengths shorter than the chunk (row j of s has position ctx_s - L_s + j): rows
     with a negative position are zeros and the others attend to positions 0..pos, as in the
-    oracle; a sequence with no cached position at all is zeros throughout (MFMA path, bf16)."""
-    rng = np.random.default_rng(31 + D)
-    lens = np.array([40, 100, 70, 33, 5], np.int32)
-    ctx = np.array([25, 10, 0, 33, 64], np.int32)
-    hkv, H, bs, nb, mb = 2, 8, 16, 64, 8
+    oracle; a sequence with no cached position at all is zeros throughout (MFMA paths).  With
+    G = 1, 2, 3 a unit holds several 32-row subtiles, whose waves stop computing after their own
+    last row: here some subtiles have only rows without a position, or none at all."""
+    rng = np.random.default_rng(31 + D + 7 * G)
+    lens = np.array([40, 100, 70, 33, 5, 130], np.int32)
+    ctx = np.array([25, 10, 0, 33, 64, 40], np.int32)
+    hkv, bs, nb, mb = 2, 16, 64, 9
+    H = G * hkv
     bt = np.stack([rng.permutation(nb)[:mb] for _ in lens]).astype(np.int32)
     T = int(lens.sum())
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
-    q = normal(rng, (T, H, D), "bf16")
-    kc, vc = normal(rng, (nb, hkv, bs, D), "bf16"), normal(rng, (nb, hkv, bs, D), "bf16")
-    out = torch.full((T, H, D), float("nan"), dtype=torch.bfloat16, device=device)
+    q = normal(rng, (T, H, D), dt)
+    kc, vc = normal(rng, (nb, hkv, bs, D), dt), normal(rng, (nb, hkv, bs, D), dt)
+    out = torch.full((T, H, D), float("nan"), dtype=TORCH_DT[dt], device=device)
     scale = 1.0 / math.sqrt(D)
-    kernels.launch_prefill_packed(to_dev(q, "bf16", device), to_dev(kc, "bf16", device), to_dev(vc, "bf16", device),
+    kernels.launch_prefill_packed(to_dev(q, dt, device), to_dev(kc, dt, device), to_dev(vc, dt, device),
                                   i32(bt, device), i32(ctx, device), i32(cu, device), out, scale, H, hkv, D, bs, mb,
                                   len(lens), T, int(lens.max()))
     torch.cuda.synchronize()
-    want = orc.prefill_packed(q, kc, vc, bt, ctx, cu, scale, "bf16")
+    want = orc.prefill_packed(q, kc, vc, bt, ctx, cu, scale, dt)
     got = dev_f32(out)
     assert not np.isnan(got).any()
-    assert_close(got, want, "bf16", "rows without a position")
+    assert_close(got, want, dt, "rows without a position")
     assert np.all(got[cu[2]:cu[3]] == 0)
+    assert np.all(got[cu[5]:cu[5] + 90] == 0)  # positions -90 .. -1
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
