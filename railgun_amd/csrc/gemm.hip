@@ -471,6 +471,118 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
   }
 }
 
+// Wide form for layers with many output columns (the LM head: 128k columns): the 4 waves split
+// the tile's columns instead of K, NW 16-column blocks each, so a workgroup covers 64 NW columns
+// against one copy of X in LDS and X's bytes per weight byte drop from 2 (128 rows against 64
+// columns) to 128 / (64 NW).  Chunks are 64 k (128-byte row pieces, 16-byte piece p of row R at
+// piece p ^ (R % 8)) so that the ring holds several chunks ahead; each wave reads every X
+// fragment and its own W fragments, and holds only its columns' sums: no reduction between the
+// waves, each writes its columns.  Plain or residual epilogue (EPI), one pass over K.
+constexpr int kWideK = 64;
+constexpr int kWideRow = 2 * kWideK;  // bytes of a row piece
+template <int NW, int MB>
+struct WideRing {
+  static constexpr int ROWS = 16 * MB + 16 * NW * kGemmWaves;  // X rows, then W rows
+  static constexpr int SLOT = ROWS * kWideRow;
+  static constexpr int FIT = kLdsBytes / SLOT;
+  static constexpr int AHEAD = FIT >= 5 ? 3 : FIT - 1;
+  static constexpr int SLOTS = FIT >= AHEAD + 2 ? AHEAD + 2 : AHEAD + 1;
+  static constexpr bool TWO_BARRIERS = SLOTS == AHEAD + 1;
+  static constexpr int QX = 16 * MB / 8 / kGemmWaves;  // X copies per wave per chunk (1 KB: 8 rows)
+  static constexpr int QW = 2 * NW;                    // W copies per wave per chunk
+  static constexpr int PER = QX + QW;
+  static_assert(QX * 8 * kGemmWaves == 16 * MB, "X rows per wave");
+  static_assert(AHEAD >= 1 && AHEAD * PER < 64 && SLOTS * SLOT <= kLdsBytes, "wide ring does not fit");
+};
+template <typename T, int NW, int MB, int EPI>
+__global__ __launch_bounds__(kGemmThreads) void wide_gemm_kernel(GemmArgs a) {
+  static_assert(EPI == kEpiPlain || EPI == kEpiResidual, "plain or residual epilogue");
+  using MF = gemm_mfma<T>;
+  using RG = WideRing<NW, MB>;
+  constexpr int D = RG::AHEAD;
+  __shared__ __attribute__((aligned(16))) char lds[RG::SLOTS * RG::SLOT];
+  const uint32_t lds_base = (uint32_t)(uintptr_t)((RG_LDS char*)lds);
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int chunks = a.K / kWideK;
+  const int n0 = blockIdx.x * (16 * NW * kGemmWaves);
+  const int mrows = min(16 * MB, a.M);
+
+  // Copy sources: instruction q of wave w moves X rows 8 (w QX + q) .. +7 (then W rows
+  // 8 (w QW + q) .. +7 of the tile), lane (row + lane / 8, piece (lane % 8) ^ (row % 8)).
+  const char* xbase = reinterpret_cast<const char*>(a.x);
+  const char* wbase = reinterpret_cast<const char*>(a.w + (int64_t)n0 * a.ldw);
+  uint32_t xoff[RG::QX], woff[RG::QW];
+#pragma unroll
+  for (int q = 0; q < RG::QX; ++q) {
+    const int row = 8 * (w * RG::QX + q) + (lane >> 3);
+    xoff[q] = (uint32_t)(min(row, mrows - 1) * a.ldx * 2 + (((lane & 7) ^ (row & 7)) << 4));
+  }
+#pragma unroll
+  for (int q = 0; q < RG::QW; ++q) {
+    const int row = 8 * (w * RG::QW + q) + (lane >> 3);
+    woff[q] = (uint32_t)(row * a.ldw * 2 + (((lane & 7) ^ (row & 7)) << 4));
+  }
+  // Staggered chunk order for large weights, as in skinny_gemm_kernel.
+  const int rot = a.stagger && chunks > 0 ? (int)((blockIdx.x >> 3) % (unsigned)chunks) : 0;
+  auto issue = [&](int c) __attribute__((always_inline)) {
+    const uint32_t slot = lds_base + (uint32_t)((c % RG::SLOTS) * RG::SLOT);
+    const int cc = c + rot;
+    const int64_t kb = (int64_t)(cc >= chunks ? cc - chunks : cc) * kWideRow;
+#pragma unroll
+    for (int q = 0; q < RG::QX; ++q) lds_dma16_s(xbase + kb, xoff[q], slot + (w * RG::QX + q) * 1024);
+#pragma unroll
+    for (int q = 0; q < RG::QW; ++q)
+      lds_dma16_s_nt(wbase + kb, woff[q], slot + 16 * MB * kWideRow + (w * RG::QW + q) * 1024);
+  };
+
+  gf32x4_t acc[NW][MB];
+#pragma unroll
+  for (int i = 0; i < NW; ++i)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[i][mb] = gf32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int c = 0; c < D && c < chunks; ++c) issue(c);
+  for (int c = 0; c < chunks; ++c) {
+    if (c + D < chunks) issue(c + D);
+    const int ahead = min(D, chunks - 1 - c);
+    [&]<int... J>(std::integer_sequence<int, J...>) __attribute__((always_inline)) {
+      ((ahead == J ? wait_vmcnt<J * RG::PER>() : void()), ...);
+    }(std::make_integer_sequence<int, D + 1>{});
+    tile_barrier();
+    const char* slot = lds + (c % RG::SLOTS) * RG::SLOT;
+#pragma unroll
+    for (int ks = 0; ks < kWideK / 32; ++ks) {
+      // Lane (r, g) takes k 32 ks + 8 g .. +8 of row r of each 16-row block: piece 4 ks + g.
+      const int piece = ((4 * ks + g) ^ (r & 7)) << 4;
+      uint4 wv[NW];
+#pragma unroll
+      for (int i = 0; i < NW; ++i)
+        wv[i] = *reinterpret_cast<const uint4*>(slot + (16 * MB + 16 * (w * NW + i) + r) * kWideRow + piece);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(slot + (16 * mb + r) * kWideRow + piece);
+#pragma unroll
+        for (int i = 0; i < NW; ++i) acc[i][mb] = MF::run(wv[i], xv, acc[i][mb]);
+      }
+    }
+    if constexpr (RG::TWO_BARRIERS) tile_barrier();
+  }
+  // Lane (r, g) holds C[16 mb + r][n0 + 16 (w NW + i) + 4 g .. +3].
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    if (16 * mb + r >= mrows) continue;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      const gf32x4_t v = acc[i][mb];
+      uint2* dst = reinterpret_cast<uint2*>(a.c + (int64_t)(16 * mb + r) * a.ldc + n0 + 16 * (w * NW + i) + 4 * g);
+      if constexpr (EPI == kEpiResidual) *dst = add_rounded<T>(*dst, v);
+      else *dst = make_uint2(pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]));
+    }
+  }
+}
+
 // out[m][n] = round(sum over the S splits, in split order, of part[s][m][n]): 4 columns per lane.
 // RES: out[m][n] = round(out[m][n] + round(sum)), the residual add.
 template <typename T, bool RES>
@@ -499,6 +611,29 @@ void launch_gemm_mb(const GemmArgs& a, int mb, int splits, hipStream_t s) {
     hipLaunchKernelGGL((splitk_reduce_kernel<T, EPI == kEpiResidual>), dim3((unsigned)ceil_div(quads, 256)), dim3(256),
                        0, s, a, splits);
   }
+}
+
+// The wide form (wide_gemm_kernel) for layers of at least RG_GEMM_WIDE_MIN_N columns at more than
+// 32 rows, RG_GEMM_WIDE_NW 16-column blocks per wave.  Measured on the Llama-3.2-1B LM head
+// (128,256 x 2048, weights cold, paired runs): 128 rows 154.7 -> 112.0 us (hipBLASLt 133.7),
+// 100 rows 153.1 -> 109.0, 64 rows 121.5 -> 99.3, 40 rows 110.1 -> 96.7; two blocks per wave
+// (128 columns per workgroup) gave 134.9 us at 128 rows.
+#ifndef RG_GEMM_WIDE_MIN_N
+#define RG_GEMM_WIDE_MIN_N 32768
+#endif
+#ifndef RG_GEMM_WIDE_NW
+#define RG_GEMM_WIDE_NW 4
+#endif
+constexpr int kWideCols = 16 * RG_GEMM_WIDE_NW * kGemmWaves;
+bool wide_fits(int M, int N, int K, int64_t ldw) {
+  return RG_GEMM_WIDE_MIN_N > 0 && M > 32 && N >= RG_GEMM_WIDE_MIN_N && N % kWideCols == 0 && K % kWideK == 0 &&
+         (int64_t)(kWideCols - 1) * ldw * 2 + 2 * (int64_t)K <= INT32_MAX;
+}
+template <typename T, int EPI>
+void launch_wide(const GemmArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.N / kWideCols));
+  if (a.M > 64) hipLaunchKernelGGL((wide_gemm_kernel<T, RG_GEMM_WIDE_NW, 8, EPI>), grid, dim3(kGemmThreads), 0, s, a);
+  else hipLaunchKernelGGL((wide_gemm_kernel<T, RG_GEMM_WIDE_NW, 4, EPI>), grid, dim3(kGemmThreads), 0, s, a);
 }
 
 template <typename T, int EPI = kEpiPlain>
@@ -583,6 +718,7 @@ extern "C" size_t rg_linear_workspace_bytes(int32_t num_rows, int32_t out_featur
       in_features <= 0 || in_features % kChunkK != 0) {
     return 0;
   }
+  if (wide_fits(num_rows, out_features, in_features, in_features)) return 0;  // the wide form: one pass
   const GemmPlan p = gemm_plan(num_rows, out_features, in_features, device_cu_count());
   return p.splits > 1 ? (size_t)p.splits * num_rows * out_features * sizeof(float) : 0;
 }
@@ -644,6 +780,11 @@ int linear_entry(const char* op, const void* x, const void* weight, void* out, i
              static_cast<float*>(workspace), M, N, K, ldx, ldw, ldo, plan.mtiles, plan.xcd};
   a.stagger = stagger_for(N, K);
   hipStream_t s = as_stream(stream);
+  if (wide_fits(M, N, K, ldw)) {
+    if (dtype == RG_DTYPE_BF16) launch_wide<bf16_t, EPI>(a, s);
+    else launch_wide<f16_t, EPI>(a, s);
+    return check_launch(op);
+  }
   if (dtype == RG_DTYPE_BF16) launch_gemm<bf16_t, EPI>(a, plan.nb, plan.mb, plan.splits, s);
   else launch_gemm<f16_t, EPI>(a, plan.nb, plan.mb, plan.splits, s);
   return check_launch(op);
