@@ -335,6 +335,50 @@ def side_prefill(device, gen, steps: int, fp32: bool = False, num_heads: int = 3
             "traffic": measured_traffic("prefill_config4")}
 
 
+def side_prefill_shapes(device, gen, steps: int) -> dict:
+    """The bf16 packed prefill (config 4's heads, 32 / 8, D 128) on batches unlike config 4, side
+    figures only: one long prompt, chunked prefill after a cached prefix (flops count the cached
+    keys), and many short prompts.  Cache contents are N(0, 1) (the kernel's cost does not depend
+    on them); tables drawn as config 4's."""
+    import numpy as np
+    import torch
+
+    from railgun_amd import workloads as wl
+    from railgun_amd.ops import PagedAttentionKernels
+
+    kernels = PagedAttentionKernels(0)
+    shapes = {"1x8192": ([8192], [0]), "4x2048_after_2048": ([2048] * 4, [2048] * 4),
+              "16x512_after_4096": ([512] * 16, [4096] * 16), "64x128": ([128] * 64, [0] * 64)}
+    out = {}
+    for name, (lens, prior) in shapes.items():
+        lens, prior = np.array(lens, np.int32), np.array(prior, np.int32)
+        ctx = lens + prior
+        mb = int(((ctx + 15) // 16).max())
+        nb = int(((ctx + 15) // 16).sum()) + 8
+        bt = wl.assign_blocks(ctx, 16, nb, mb, np.random.default_rng(1004))
+        w = wl.PrefillWorkload(name, "bf16", 32, 8, 128, 16, nb, lens, bt, 1004, prior=prior)
+        T = w.num_tokens
+        shape = (w.num_blocks, w.num_kv_heads, w.block_size, w.head_dim)
+        kc, vc = bf16_normal(shape, gen, device), bf16_normal(shape, gen, device)
+        q = bf16_normal((T, w.num_heads, w.head_dim), gen, device)
+        o = torch.empty_like(q)
+        i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+        btd, ctxd, cu = i32(w.block_table), i32(w.context_lens), i32(w.cu_seqlens)
+        maxq = int(lens.max())
+
+        def call():
+            kernels.launch_prefill_packed(q, kc, vc, btd, ctxd, cu, o, w.scale, w.num_heads, w.num_kv_heads,
+                                          w.head_dim, w.block_size, w.max_blocks, w.num_seqs, T, maxq)
+
+        ms = time_events(call, steps, 2)
+        tflops = w.causal_flops() / (ms * 1e-3) / 1e12
+        out[name] = {"tokens": T, "cached": int(prior.sum()), "us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 2),
+                     "frac_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops": w.causal_flops()}
+        del kc, vc, q, o
+        torch.cuda.empty_cache()
+    return out
+
+
 def side_model(device, steps: int) -> dict:
     """Config 5: one decode step of a random-init Llama-3.2-1B (16 layers, bf16 weights ~ N(0, 0.02))
     for 128 sequences with contexts U[64, 8192] over per-layer paged pools pre-filled with N(0, 1).
@@ -589,6 +633,8 @@ def main() -> int:
         result["fp32_decode"] = side_fp32(device, gen, max(3, args.steps // 5))
         log("[bench] config4 prefill ...")
         result["prefill"] = side_prefill(device, gen, 10)
+        log("[bench] prefill on other batch shapes ...")
+        result["prefill_shapes"] = side_prefill_shapes(device, gen, 10)
         log("[bench] config4 prefill in fp32 ...")
         result["fp32_prefill"] = side_prefill(device, gen, 3, fp32=True)
         log("[bench] GQA 3 (24 / 8 heads): config 2 decode load, config 4 prefill ...")
