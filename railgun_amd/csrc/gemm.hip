@@ -614,26 +614,31 @@ void launch_gemm_mb(const GemmArgs& a, int mb, int splits, hipStream_t s) {
 }
 
 // The wide form (wide_gemm_kernel) for layers of at least RG_GEMM_WIDE_MIN_N columns at more than
-// 32 rows, RG_GEMM_WIDE_NW 16-column blocks per wave.  Measured on the Llama-3.2-1B LM head
-// (128,256 x 2048, weights cold, paired runs): 128 rows 154.7 -> 112.0 us (hipBLASLt 133.7),
-// 100 rows 153.1 -> 109.0, 64 rows 121.5 -> 99.3, 40 rows 110.1 -> 96.7; two blocks per wave
-// (128 columns per workgroup) gave 134.9 us at 128 rows.
+// RG_GEMM_WIDE_MIN_M rows, RG_GEMM_WIDE_NW 16-column blocks per wave, X tiles of 32, 64 or 128
+// rows.  Measured on the Llama-3.2-1B LM head (128,256 x 2048, weights cold, paired runs):
+// 128 rows 154.7 -> 112.0 us (hipBLASLt 133.7), 100 rows 153.1 -> 109.0, 64 rows 121.5 -> 99.3,
+// 40 rows 110.1 -> 96.7, 32 rows 95.4 -> 89.0, 24 rows 94.3 -> 90.2, 17 rows 92.7 -> 88.5, but
+// 9 rows 83.4 -> 87.1; two blocks per wave (128 columns per workgroup) gave 134.9 us at 128 rows.
 #ifndef RG_GEMM_WIDE_MIN_N
 #define RG_GEMM_WIDE_MIN_N 32768
 #endif
 #ifndef RG_GEMM_WIDE_NW
 #define RG_GEMM_WIDE_NW 4
 #endif
+#ifndef RG_GEMM_WIDE_MIN_M
+#define RG_GEMM_WIDE_MIN_M 16
+#endif
 constexpr int kWideCols = 16 * RG_GEMM_WIDE_NW * kGemmWaves;
 bool wide_fits(int M, int N, int K, int64_t ldw) {
-  return RG_GEMM_WIDE_MIN_N > 0 && M > 32 && N >= RG_GEMM_WIDE_MIN_N && N % kWideCols == 0 && K % kWideK == 0 &&
+  return RG_GEMM_WIDE_MIN_N > 0 && M > RG_GEMM_WIDE_MIN_M && N >= RG_GEMM_WIDE_MIN_N && N % kWideCols == 0 && K % kWideK == 0 &&
          (int64_t)(kWideCols - 1) * ldw * 2 + 2 * (int64_t)K <= INT32_MAX;
 }
 template <typename T, int EPI>
 void launch_wide(const GemmArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)(a.N / kWideCols));
   if (a.M > 64) hipLaunchKernelGGL((wide_gemm_kernel<T, RG_GEMM_WIDE_NW, 8, EPI>), grid, dim3(kGemmThreads), 0, s, a);
-  else hipLaunchKernelGGL((wide_gemm_kernel<T, RG_GEMM_WIDE_NW, 4, EPI>), grid, dim3(kGemmThreads), 0, s, a);
+  else if (a.M > 32) hipLaunchKernelGGL((wide_gemm_kernel<T, RG_GEMM_WIDE_NW, 4, EPI>), grid, dim3(kGemmThreads), 0, s, a);
+  else hipLaunchKernelGGL((wide_gemm_kernel<T, RG_GEMM_WIDE_NW, 2, EPI>), grid, dim3(kGemmThreads), 0, s, a);
 }
 
 template <typename T, int EPI = kEpiPlain>

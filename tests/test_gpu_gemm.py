@@ -54,12 +54,13 @@ def test_linear_matches_fp32(device, M, N, K, dt):
 
 @pytest.mark.parametrize("M,N,K,dt", [(128, 128256, 2048, "bf16"), (100, 128256, 2048, "f16"), (17, 128256, 2048, "bf16"),
                                       (37, 65536, 128, "bf16"), (90, 131072, 128, "f16"), (64, 128256, 256, "f16"),
-                                      (33, 32768, 256, "bf16"), (65, 32768, 384, "f16"), (32, 32768, 256, "bf16")])
+                                      (33, 32768, 256, "bf16"), (65, 32768, 384, "f16"), (16, 32768, 256, "bf16"),
+                                      (17, 32768, 384, "f16")])
 def test_linear_large_n(device, M, N, K, dt):
     """Large N: the Llama LM head (N = 128,256) at 128, 100 and 17 rows (full, ragged and
-    two-block row tiles), N = 64 k / 128 k with K of one chunk, fp16; the wide form's edges (33
-    and 65 rows: the first row counts of its 64- and 128-row X tiles; 32 rows: the skinny form);
-    against the fp32 product and repeatable bit for bit."""
+    two-block row tiles), N = 64 k / 128 k with K of one chunk, fp16; the wide form's edges (17,
+    33 and 65 rows: the first row counts of its 32-, 64- and 128-row X tiles; 16 rows: the skinny
+    form); against the fp32 product and repeatable bit for bit."""
     g = torch.Generator().manual_seed(M + N + K)
     x = torch.randn(M, K, generator=g).to(TORCH[dt]).to(device)
     w = (0.02 * torch.randn(N, K, generator=g)).to(TORCH[dt]).to(device)
