@@ -18,6 +18,8 @@
 //   waves take one k-step of 32 each from every chunk and hold all NB x MB fragments of their
 //   steps.  The four partial sums are added through LDS in a fixed order, so the result is
 //   deterministic (graph replays reproduce eager runs bit for bit).
+// * Layers with many columns (the LM head) take wide_gemm_kernel instead: the 4 waves split a
+//   256-column tile rather than K, against one copy of X per workgroup.
 #include <math.h>
 
 #include <algorithm>
