@@ -783,9 +783,11 @@ struct StreamArgs {
 // touches (per-worker timestamps at config 2, 1,024 workers of ~69 units: each extra segment
 // start -- q load, partial write, the pipeline's restart -- ends the worker ~1.6 us later, about
 // 10 KB of its stream), so the split evens out (unit KB) x units + RG_SK_SEG_COST_KB x segment
-// starts instead of units alone.  0: units only.
+// starts instead of units alone.  0: units only.  Swept in paired runs against 10 (config 2 /
+// the config-5 attention shape): 5 KB 0.999 / 1.012, 15 KB 0.996 / 0.997, 20 KB 0.988-0.993 /
+// 0.999-1.000, 30 KB 1.002 / 1.003.
 #ifndef RG_SK_SEG_COST_KB
-#define RG_SK_SEG_COST_KB 10
+#define RG_SK_SEG_COST_KB 20
 #endif
 
 // 16-token sub-blocks of sequence s: ceil(ctx/16) per kv-head (context clamped to the table
