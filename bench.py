@@ -633,8 +633,6 @@ def main() -> int:
         result["fp32_decode"] = side_fp32(device, gen, max(3, args.steps // 5))
         log("[bench] config4 prefill ...")
         result["prefill"] = side_prefill(device, gen, 10)
-        log("[bench] prefill on other batch shapes ...")
-        result["prefill_shapes"] = side_prefill_shapes(device, gen, 10)
         log("[bench] config4 prefill in fp32 ...")
         result["fp32_prefill"] = side_prefill(device, gen, 3, fp32=True)
         log("[bench] GQA 3 (24 / 8 heads): config 2 decode load, config 4 prefill ...")
@@ -644,6 +642,10 @@ def main() -> int:
         result["model_step"] = side_model(device, 10)
         log("[bench] config5 projections ...")
         result["gemm"] = side_gemm(device)
+        # Last: it launches config 4's prefill kernel on other shapes, and the profiles take
+        # config 4's timed launches as the last of that kernel before the fp32 prefill leg.
+        log("[bench] prefill on other batch shapes ...")
+        result["prefill_shapes"] = side_prefill_shapes(device, gen, 10)
     if not args.no_cpu:
         log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w)

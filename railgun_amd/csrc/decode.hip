@@ -718,10 +718,11 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 // Units in flight ahead of the one being computed, per stream-K worker.  The workers are
 // one wave per SIMD (RG_SK_WAVES_PER_CU = 4): two waves sharing a SIMD progress at
 // different rates (the older one wins issue arbitration), which leaves the younger half
-// of a static split running alone at the end; one wave per SIMD with three 8 KB units in
-// flight streams at the same rate without that tail.
+// of a static split running alone at the end; one wave per SIMD with 8 KB units in flight
+// streams at the same rate without that tail.  Two ahead: in paired runs against three, with the
+// non-temporal K/V loads and the cost split, config 2 0.990 (twice), config 3 0.992, four 1.011.
 #ifndef RG_SK_PREFETCH
-#define RG_SK_PREFETCH 3
+#define RG_SK_PREFETCH 2
 #endif
 #ifndef RG_SK_BPU_D128
 #define RG_SK_BPU_D128 1
