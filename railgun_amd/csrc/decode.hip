@@ -719,10 +719,12 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 // one wave per SIMD (RG_SK_WAVES_PER_CU = 4): two waves sharing a SIMD progress at
 // different rates (the older one wins issue arbitration), which leaves the younger half
 // of a static split running alone at the end; one wave per SIMD with 8 KB units in flight
-// streams at the same rate without that tail.  Two ahead: in paired runs against three, with the
-// non-temporal K/V loads and the cost split, config 2 0.990 (twice), config 3 0.992, four 1.011.
+// streams at the same rate without that tail.  One ahead: with the non-temporal K/V loads and
+// the cost split, paired runs against three ahead gave config 2 0.990 (twice) with two ahead and
+// 0.993-0.995 more with one (config 3 0.992, then 0.995-0.996), four ahead 1.011; the 1,024
+// workers keep ~16 MB in flight with one unit each ahead, more than the HBM round trip needs.
 #ifndef RG_SK_PREFETCH
-#define RG_SK_PREFETCH 2
+#define RG_SK_PREFETCH 1
 #endif
 #ifndef RG_SK_BPU_D128
 #define RG_SK_BPU_D128 1
@@ -734,12 +736,13 @@ __global__ __launch_bounds__(kThreads) RG_DEC_OCCUPANCY void decode_mfma_kernel(
 // Llama-3.2-1B step against 216.6 us for two-block units three deep and 236.5 us for
 // one-block units four deep (2 x 4, 2 x 5 and 3 x 3 were in between), with ordinary K/V
 // loads; with the non-temporal loads 4 x 2 stays ahead of 2 x 3 and 4 x 3 (194.7 against
-// 196.0 / 198.0 us per call), as one-block units three deep do at head_dim 128.
+// 196.0 / 198.0 us per call), and with the cost split 4 x 1 ahead of 4 x 2 (0.992-0.993 in
+// paired runs at the Llama-3.2-1B attention shape).
 #ifndef RG_SK_BPU_D64
 #define RG_SK_BPU_D64 4
 #endif
 #ifndef RG_SK_PREFETCH_D64
-#define RG_SK_PREFETCH_D64 2
+#define RG_SK_PREFETCH_D64 1
 #endif
 // With 8 or more q-heads per kv-head the accumulators take 8 * G registers per lane, so at
 // head_dim 64 the unit ring shrinks to two-block units (half the registers of the four-block
