@@ -105,8 +105,11 @@ struct GemmRing {
   static constexpr int SLOT = 16 * (MB + NB) * kChunkBytes;
   static constexpr int FIT = (kLdsBytes - RESERVE) / SLOT;
   // AHEAD chunks in flight; with AHEAD + 2 slots the slot a wave refills was read two chunks ago,
-  // so one barrier per chunk orders it; with AHEAD + 1 a second barrier follows the MFMAs.
-  static constexpr int AHEAD = FIT >= RG_GEMM_AHEAD + 1 ? RG_GEMM_AHEAD : FIT - 1;
+  // so one barrier per chunk orders it; with AHEAD + 1 a second barrier follows the MFMAs.  One
+  // barrier is worth more than the second chunk in flight: a ring of three slots runs one chunk
+  // ahead (gate/up at 128 rows, 48 KB slots: 0.95 with SiLU·mul, with or without the folded norm,
+  // in paired runs against two ahead with two barriers), larger rings RG_GEMM_AHEAD.
+  static constexpr int AHEAD = FIT >= RG_GEMM_AHEAD + 2 ? RG_GEMM_AHEAD : FIT >= 3 ? FIT - 2 : FIT - 1;
   static constexpr int SLOTS = FIT >= AHEAD + 2 ? AHEAD + 2 : AHEAD + 1;
   static constexpr bool TWO_BARRIERS = SLOTS == AHEAD + 1;
   static constexpr int PER = MB + NB;  // copies per wave per chunk (1 KB each: 4 rows x 256 B)
@@ -667,7 +670,7 @@ void launch_gemm_rope(const GemmArgs& a, int nb, int mb, hipStream_t s) {
 int ring_bytes(int nb, int mb, int reserve = 0) {
   const int slot = 16 * (mb + nb) * kChunkBytes;
   const int fit = (kLdsBytes - reserve) / slot;
-  const int ahead = fit >= RG_GEMM_AHEAD + 1 ? RG_GEMM_AHEAD : fit - 1;
+  const int ahead = fit >= RG_GEMM_AHEAD + 2 ? RG_GEMM_AHEAD : fit >= 3 ? fit - 2 : fit - 1;
   const int slots = fit >= ahead + 2 ? ahead + 2 : ahead + 1;
   return std::max(slots * slot, nb * mb * kGemmWaves * 1024) + reserve;
 }
