@@ -490,7 +490,9 @@ struct WideRing {
   static constexpr int ROWS = 16 * MB + 16 * NW * kGemmWaves;  // X rows, then W rows
   static constexpr int SLOT = ROWS * kWideRow;
   static constexpr int FIT = kLdsBytes / SLOT;
-  static constexpr int AHEAD = FIT >= 5 ? 3 : FIT - 1;
+  // One barrier per chunk where the ring allows it, as in GemmRing (128 rows, three 48 KB slots:
+  // one chunk ahead 0.986 against two ahead with two barriers; 64 rows 0.978).
+  static constexpr int AHEAD = FIT >= 5 ? 3 : FIT >= 3 ? FIT - 2 : FIT - 1;
   static constexpr int SLOTS = FIT >= AHEAD + 2 ? AHEAD + 2 : AHEAD + 1;
   static constexpr bool TWO_BARRIERS = SLOTS == AHEAD + 1;
   static constexpr int QX = 16 * MB / 8 / kGemmWaves;  // X copies per wave per chunk (1 KB: 8 rows)
