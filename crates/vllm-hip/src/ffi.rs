@@ -149,6 +149,15 @@ extern "C" {
         batch_size: i32, dtype: i32, kv_block_stride: i64, workspace: *mut c_void, workspace_bytes: usize,
         stream: *mut c_void,
     ) -> c_int;
+    /// New: RoPE + reshape_and_cache of one new token per sequence fused into v1's launches
+    /// (mod.rs:196-225, 227-262, 305-348 as one call); query is read, not rotated in place.
+    pub fn rg_rope_reshape_and_cache_paged_attention_v1(
+        query: *const c_void, key: *const c_void, value: *const c_void, key_cache: *mut c_void,
+        value_cache: *mut c_void, cos_sin: *const f32, positions: *const i32, slot_mapping: *const i32,
+        block_table: *const i32, context_lens: *const i32, output: *mut c_void, scale: f32, num_heads: i32,
+        num_kv_heads: i32, head_dim: i32, block_size: i32, max_blocks_per_seq: i32, batch_size: i32, dtype: i32,
+        kv_block_stride: i64, workspace: *mut c_void, workspace_bytes: usize, stream: *mut c_void,
+    ) -> c_int;
     /// New, no counterpart: v1 on the library's static scratch, for callers that cannot allocate.
     pub fn rg_paged_attention_v1_no_alloc(
         query: *const c_void, key_cache: *const c_void, value_cache: *const c_void, block_table: *const i32,

@@ -307,6 +307,41 @@ impl PagedAttentionKernels {
             workspace.len(), self.stream))
     }
 
+    /// One decode step's RoPE + cache write (one new token per sequence: `key` / `value`
+    /// [batch, H_kv, D]) and `launch_v1_split` in the stream-K decode's launches: the same
+    /// output and caches as `launch_rope_reshape_and_cache` followed by `launch_v1_split`,
+    /// with `query` left unrotated.  `slot_mapping[s]` is -1 or the slot of position
+    /// `context_lens[s] - 1` in sequence s's block table.
+    pub unsafe fn launch_rope_reshape_and_cache_v1<T: KvElement>(
+        &self,
+        query: &HipSlice<T>,
+        key: &HipSlice<T>,
+        value: &HipSlice<T>,
+        key_cache: &mut HipSlice<T>,
+        value_cache: &mut HipSlice<T>,
+        cos_sin: &HipSlice<f32>,
+        positions: &HipSlice<i32>,
+        slot_mapping: &HipSlice<i32>,
+        block_table: &HipSlice<i32>,
+        context_lens: &HipSlice<i32>,
+        output: &mut HipSlice<T>,
+        scale: f32,
+        num_heads: i32,
+        num_kv_heads: i32,
+        head_dim: i32,
+        block_size: i32,
+        max_blocks_per_seq: i32,
+        batch_size: i32,
+        workspace: &mut HipSlice<u8>,
+    ) -> CoreResult<()> {
+        status(ffi::rg_rope_reshape_and_cache_paged_attention_v1(
+            query.as_ptr(), key.as_ptr(), value.as_ptr(), key_cache.as_mut_ptr(), value_cache.as_mut_ptr(),
+            cos_sin.as_ptr() as *const f32, positions.as_ptr() as *const i32, slot_mapping.as_ptr() as *const i32,
+            block_table.as_ptr() as *const i32, context_lens.as_ptr() as *const i32, output.as_mut_ptr(), scale,
+            num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, batch_size, T::DTYPE,
+            self.kv_block_stride, workspace.as_mut_ptr(), workspace.len(), self.stream))
+    }
+
     /// `launch_v1_split` on the library's static per-device scratch: no allocation anywhere,
     /// for code under graph capture or loops that cannot allocate.  Calls overlapping in time
     /// on one device race on that scratch.

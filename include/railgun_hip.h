@@ -320,6 +320,28 @@ int rg_paged_attention_v1(const void* query, const void* key_cache,
                           int32_t batch_size, int32_t dtype, int64_t kv_block_stride,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* One decode step's attention with its RoPE + cache pass fused in: the results of
+ * rg_rope_reshape_and_cache(q', key, value, ...) on a copy q' of query, with one new
+ * token per sequence (token s of key / value [batch_size, num_kv_heads, head_dim],
+ * positions and slot_mapping [batch_size] belongs to sequence s), followed by
+ * rg_paged_attention_v1(q', ...) — output and caches bit for bit — in the launches of
+ * the stream-K decode alone.  query is read, not rotated in place.  slot_mapping[s]
+ * is -1 (a padding token: nothing written) or the slot of position
+ * context_lens[s] - 1 in sequence s's block table, as in every decode step; any
+ * other slot is left unwritten (where the chain would write it).  Needs a workspace of
+ * rg_paged_attention_v1_workspace_bytes; bf16 / f16, head_dim 64 or 128,
+ * num_heads / num_kv_heads 1, 2, 4 or 8 (RG_ERR_NOT_SUPPORTED otherwise).
+ * New entry: the reference runs RoPE, reshape_and_cache and launch_v1 as separate
+ * calls (crates/vllm-cuda/src/kernels/mod.rs:196-225, 227-262, 305-348). */
+int rg_rope_reshape_and_cache_paged_attention_v1(
+    const void* query, const void* key, const void* value, void* key_cache,
+    void* value_cache, const float* cos_sin, const int32_t* positions,
+    const int32_t* slot_mapping, const int32_t* block_table,
+    const int32_t* context_lens, void* output, float scale, int32_t num_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int32_t max_blocks_per_seq, int32_t batch_size, int32_t dtype,
+    int64_t kv_block_stride, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Same computation as rg_paged_attention_v1, with the rotation_metadata
  * argument of launch_v1_plus (crates/vllm-cuda/src/kernels/mod.rs:350-399),
  * which is ignored (identity rotation). */

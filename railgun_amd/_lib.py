@@ -95,6 +95,10 @@ SIGNATURES = {
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32, c_int32,
          c_int32, c_int32, c_int32, c_int32, c_int64, c_void_p, c_size_t, c_void_p],
     ),
+    "rg_rope_reshape_and_cache_paged_attention_v1": (
+        c_int,
+        [c_void_p] * 11 + [c_float] + [c_int32] * 7 + [c_int64, c_void_p, c_size_t, c_void_p],
+    ),
     "rg_paged_attention_v1_no_alloc": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32, c_int32,

@@ -104,20 +104,6 @@ __global__ __launch_bounds__(kCacheThreads) void scatter_kv_elem(
 
 // ------------------------------------------------------------------ RoPE ----
 
-// Rotate-half on one pair with the rounding of the reference expression
-// (rope.cu:34-41) made explicit: each product and the difference/sum are
-// rounded separately (no fused multiply-add), so results are reproducible.
-__device__ __forceinline__ void rotate_pair(float lo, float hi, float c, float s, float& out_lo,
-                                            float& out_hi) {
-#pragma clang fp contract(off)
-  const float a = lo * c;
-  const float b = hi * s;
-  const float e = hi * c;
-  const float f = lo * s;
-  out_lo = a - b;
-  out_hi = e + f;
-}
-
 // One wave per (token, head row); each lane rotates the pairs (i, i + D/2) for
 // i = lane, lane + 64, ...  `src` and `dst` are the row's element offsets (may alias).
 template <typename T>
@@ -130,7 +116,7 @@ __device__ __forceinline__ void rope_row(const typename elem<T>::storage* __rest
     const float lo = E::to_f32(src[i]);
     const float hi = E::to_f32(src[half + i]);
     float ol, oh;
-    rotate_pair(lo, hi, cs[i], cs[half + i], ol, oh);
+    rope_rotate_pair(lo, hi, cs[i], cs[half + i], ol, oh);
     dst[i] = E::from_f32(ol);
     dst[half + i] = E::from_f32(oh);
   }
@@ -158,9 +144,9 @@ __device__ __forceinline__ void rope_chunk16(const uint16_t* __restrict__ src, u
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     float a0, b0, a1, b1;
-    rotate_pair(E::to_f32((uint16_t)(lw[k] & 0xffffu)), E::to_f32((uint16_t)(hw[k] & 0xffffu)), cv[2 * k],
+    rope_rotate_pair(E::to_f32((uint16_t)(lw[k] & 0xffffu)), E::to_f32((uint16_t)(hw[k] & 0xffffu)), cv[2 * k],
                 sv[2 * k], a0, b0);
-    rotate_pair(E::to_f32((uint16_t)(lw[k] >> 16)), E::to_f32((uint16_t)(hw[k] >> 16)), cv[2 * k + 1],
+    rope_rotate_pair(E::to_f32((uint16_t)(lw[k] >> 16)), E::to_f32((uint16_t)(hw[k] >> 16)), cv[2 * k + 1],
                 sv[2 * k + 1], a1, b1);
     ol[k] = (uint32_t)E::from_f32(a0) | ((uint32_t)E::from_f32(a1) << 16);
     oh[k] = (uint32_t)E::from_f32(b0) | ((uint32_t)E::from_f32(b1) << 16);

@@ -296,6 +296,108 @@ __device__ __forceinline__ bool softmax_block(const f32x4_t (&c)[NB], int col, i
 //     dims vd0..vd0+8, and accumulates acc[h][0..8) for all G heads.
 // The softmax runs in the exp2 domain with a wave-uniform running max per head; the
 // probabilities travel from the QK layout to the PV layout through a small LDS area.
+// Fused RoPE (decode_stream_kernel with ROPE): a lane's run of P consecutive rotation pairs
+// (x[d + j], x[d + D/2 + j]), j < P, of one row, with their cos / sin, rotated with the arithmetic
+// of the RoPE + cache pass (rope_chunk16: rope_rotate_pair, then one rounding to T) into an LDS
+// row (p points into LDS).  Spreading a row's D/2 pairs over the lanes keeps the rotation to a
+// few instructions per wave; the MFMA layouts read the rotated rows back from LDS.
+template <int P>
+__device__ __forceinline__ void load_u16(const uint16_t* p, uint16_t (&o)[P]) {
+  if constexpr (P == 1) {
+    o[0] = *p;
+  } else {
+    uint32_t w[P / 2];
+    if constexpr (P == 2) {
+      w[0] = *reinterpret_cast<const uint32_t*>(p);
+    } else if constexpr (P == 4) {
+      const uint2 v = *reinterpret_cast<const uint2*>(p);
+      w[0] = v.x;
+      w[1] = v.y;
+    } else {
+      static_assert(P == 8, "runs of 1, 2, 4 or 8 pairs");
+      const uint4 v = *reinterpret_cast<const uint4*>(p);
+      w[0] = v.x;
+      w[1] = v.y;
+      w[2] = v.z;
+      w[3] = v.w;
+    }
+#pragma unroll
+    for (int j = 0; j < P / 2; ++j) {
+      o[2 * j] = (uint16_t)(w[j] & 0xffffu);
+      o[2 * j + 1] = (uint16_t)(w[j] >> 16);
+    }
+  }
+}
+template <int P>
+__device__ __forceinline__ void store_u16(uint16_t* p, const uint16_t (&x)[P]) {
+  if constexpr (P == 1) {
+    *p = x[0];
+  } else {
+    uint32_t w[P / 2];
+#pragma unroll
+    for (int j = 0; j < P / 2; ++j) w[j] = (uint32_t)x[2 * j] | ((uint32_t)x[2 * j + 1] << 16);
+    if constexpr (P == 2) *reinterpret_cast<uint32_t*>(p) = w[0];
+    else if constexpr (P == 4) *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+template <int P>
+__device__ __forceinline__ void load_f32(const float* p, float (&o)[P]) {
+  if constexpr (P == 1) {
+    o[0] = *p;
+  } else if constexpr (P == 2) {
+    const float2 v = *reinterpret_cast<const float2*>(p);
+    o[0] = v.x;
+    o[1] = v.y;
+  } else {
+#pragma unroll
+    for (int j = 0; j < P; j += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(p + j);
+      o[j] = v.x;
+      o[j + 1] = v.y;
+      o[j + 2] = v.z;
+      o[j + 3] = v.w;
+    }
+  }
+}
+template <typename T, int P>
+struct RopeRun {
+  uint16_t lo[P], hi[P];
+  float c[P], s[P];
+  // row, cs: the row and its cos_sin row; d: the run's first pair; half = D / 2.
+  __device__ __forceinline__ void load(const uint16_t* row, const float* cs, int d, int half) {
+    load_u16<P>(row + d, lo);
+    load_u16<P>(row + half + d, hi);
+    load_f32<P>(cs + d, c);
+    load_f32<P>(cs + half + d, s);
+  }
+  // The rounding is pack2's (v_cvt_pk_*: round to nearest even, two values per instruction),
+  // which gives the bits of the pass's elem<T>::from_f32 for every value but NaN payloads.
+  __device__ __forceinline__ void rotate_to(uint16_t* dst, int d, int half) const {
+    using E = elem<T>;
+    float fl[P], fh[P];
+#pragma unroll
+    for (int j = 0; j < P; ++j) rope_rotate_pair(E::to_f32(lo[j]), E::to_f32(hi[j]), c[j], s[j], fl[j], fh[j]);
+    uint16_t ol[P], oh[P];
+    if constexpr (P == 1) {
+      const uint32_t w = pack2<T>(fl[0], fh[0]);
+      ol[0] = (uint16_t)(w & 0xffffu);
+      oh[0] = (uint16_t)(w >> 16);
+    } else {
+#pragma unroll
+      for (int j = 0; j < P; j += 2) {
+        const uint32_t wl = pack2<T>(fl[j], fl[j + 1]), wh = pack2<T>(fh[j], fh[j + 1]);
+        ol[j] = (uint16_t)(wl & 0xffffu);
+        ol[j + 1] = (uint16_t)(wl >> 16);
+        oh[j] = (uint16_t)(wh & 0xffffu);
+        oh[j + 1] = (uint16_t)(wh >> 16);
+      }
+    }
+    store_u16<P>(dst + d, ol);
+    store_u16<P>(dst + half + d, oh);
+  }
+};
+
 template <typename T, int D, int G>
 struct DecodeTile {
   using MF = mfma16<T>;
@@ -328,6 +430,28 @@ struct DecodeTile {
     const uint4* qrow = reinterpret_cast<const uint4*>(qg + (int64_t)(col % G) * D + seg * 8);
 #pragma unroll
     for (int i = 0; i < NK; ++i) qa[i] = qrow[4 * i];
+  }
+  // Puts token `tok` of block `blk` of a loaded NB-block unit to the given K row (kn, load_row's
+  // layout) and V piece (vn: dims vd0 .. vd0 + 8 of the row), as if they had been read from the
+  // cache.  Register selects only: the entries stay at compile-time indices.
+  template <int NB>
+  __device__ __forceinline__ void patch(uint4 (&kk)[NB * NK], uint4 (&vv)[NB * NV], int blk, int tok,
+                                        const uint4 (&kn)[NK], uint4 vn) const {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const bool kr = b == blk && col == tok;
+#pragma unroll
+      for (int i = 0; i < NK; ++i) {
+        const uint4 o = kk[b * NK + i];
+        kk[b * NK + i] = make_uint4(kr ? kn[i].x : o.x, kr ? kn[i].y : o.y, kr ? kn[i].z : o.z, kr ? kn[i].w : o.w);
+      }
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const bool vr = b == blk && i * TPI + vrow == tok;
+        const uint4 o = vv[b * NV + i];
+        vv[b * NV + i] = make_uint4(vr ? vn.x : o.x, vr ? vn.y : o.y, vr ? vn.z : o.z, vr ? vn.w : o.w);
+      }
+    }
   }
   __device__ __forceinline__ void reset() {
 #pragma unroll
@@ -781,6 +905,13 @@ struct StreamArgs {
   int64_t kv_stride;
   int32_t table_stride;  // entries per block-table row (max_blocks counts 16-token sub-blocks)
   int32_t bs_shift;      // block_size = 16 << bs_shift
+  // Fused RoPE + cache write of the step's new tokens (decode_stream_kernel with ROPE): token s
+  // is sequence s's; its k / v rows are [H_kv, D] at k_new / v_new + s H_kv D.
+  const void* k_new;
+  const void* v_new;
+  const float* cos_sin;         // [positions, D]: cos at [d], sin at [D/2 + d]
+  const int32_t* positions;     // [batch]
+  const int32_t* slot_mapping;  // [batch]; negative: a padding token, not cached
 };
 
 // Cost of a segment start, in KB of K/V streaming.  A worker's end time tracks the segments it
@@ -823,12 +954,20 @@ __device__ __forceinline__ int64_t wave_incl_scan(int64_t v, int lane) {
   return v;
 }
 
-template <typename T, int D, int G>
+// ROPE: the step's RoPE + cache pass fused in (16-bit tiles).  q is read unrotated and left
+// so; every worker of a segment rotates its q rows itself, and the worker holding a segment's
+// last unit rotates the new token's k row, writes k and v to the token's cache slot and puts
+// them into its own loaded copy of that block in place of what the cache held.  No worker reads
+// another's store, and the outputs and cache equal those of the RoPE + cache pass followed by
+// the decode bit for bit.  positions / slot_mapping: [batch], token s being sequence s's.
+template <typename T, int D, int G, bool ROPE = false>
 __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
     StreamArgs a, const typename DecodeTileFor<T, D, G>::S* __restrict__ q_ptr,
     const typename DecodeTileFor<T, D, G>::S* __restrict__ kc, const typename DecodeTileFor<T, D, G>::S* __restrict__ vc,
-    const int32_t* __restrict__ block_table, const int32_t* __restrict__ context_lens) {
+    const int32_t* __restrict__ block_table, const int32_t* __restrict__ context_lens,
+    const int32_t* __restrict__ positions, const int32_t* __restrict__ slot_mapping) {
   using Tile = DecodeTileFor<T, D, G>;
+  static_assert(!ROPE || !std::is_same_v<T, f32_t>, "the fused RoPE runs on the 16-bit tiles");
   constexpr int GP = Tile::GP;
   constexpr int HG = Tile::HG;
   constexpr int NK = Tile::NK;
@@ -1011,6 +1150,11 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   // in the loop.
   int64_t wbase = 0;
   int btw[BPU];
+  // ROPE: per window lane, the RoPE position of its unit's sequence (pwin) and, if the unit is its
+  // segment's last and the sequence's slot is the block table's slot of position context_len - 1,
+  // that slot (rwin; else -1).  Read with the block numbers, so no segment start waits on a
+  // scalar load for them.
+  int pwin = 0, rwin = -1;
   auto fill_window = [&](const Cursor& c0, int64_t base) __attribute__((always_inline)) {
     int ss = c0.s, kh = c0.kvh, b = c0.b + lane, nb = c0.nblk;
     while (b >= nb && ss < a.batch) {
@@ -1031,16 +1175,33 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
       const int bk = b * BPU + r < nbk ? b * BPU + r : b * BPU;
       btw[r] = live ? (row[bk >> a.bs_shift] << a.bs_shift) | (bk & ((1 << a.bs_shift) - 1)) : 0;
     }
+    if constexpr (ROPE) {
+      pwin = live ? positions[ss] : 0;
+      const int slot = live ? slot_mapping[ss] : -1;
+      const int p = (live ? context_lens[ss] : 0) - 1;  // the new token's position
+      rwin = -1;
+      if (b == nb - 1 && slot >= 0 && p >= 0 && p < a.max_blocks * kBS) {
+        // p's sub-block is the unit's sub-block r (its last with tokens); btw[r] * 16 is the slot
+        // of that sub-block's first token.
+        const int r = (p >> 4) - b * BPU;
+        int ent = btw[0];
+#pragma unroll
+        for (int q = 1; q < BPU; ++q) ent = r == q ? btw[q] : ent;
+        if (ent * kBS + (p & (kBS - 1)) == slot) rwin = slot;
+      }
+    }
   };
   // ldi: index of the unit cursor c points at.  A window refill (every 64 units) waits for
   // everything in flight once.
-  auto load_unit = [&](const Cursor& c, int64_t ldi, uint4 (&kk)[BPU * NK], uint4 (&vv)[BPU * NV], const Tile& t)
-      __attribute__((always_inline)) {
+  // rp (ROPE): the unit's rwin entry, carried to its computation with its ring slot.
+  auto load_unit = [&](const Cursor& c, int64_t ldi, uint4 (&kk)[BPU * NK], uint4 (&vv)[BPU * NV], const Tile& t,
+                       int& rp) __attribute__((always_inline)) {
     if (ldi - wbase >= 64) {
       wbase = ldi;
       fill_window(c, ldi);
       __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0)
     }
+    if constexpr (ROPE) rp = __builtin_amdgcn_readlane(rwin, (int)(ldi - wbase));
     const int64_t head = (int64_t)c.kvh * (kBS << a.bs_shift) * D;
     auto off = [&](int e) __attribute__((always_inline)) {
       return (int64_t)(e >> a.bs_shift) * a.kv_stride + head + (int64_t)(e & ((1 << a.bs_shift) - 1)) * (kBS * D);
@@ -1055,10 +1216,49 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   Tile tile;
   tile.init(lane);
   const int H = a.num_heads;
+  // Fused RoPE state (ROPE).  A segment's start loads its q rows' rotation pairs (QP per lane,
+  // the G heads' D/2 pairs spread over the lanes) with their cos / sin, and the worker holding
+  // the segment's last unit (kRopeHaveK) the new k row's pairs (KP per lane) and this lane's V
+  // piece of the new v row.  They are rotated in the segment's first unit once that unit's next
+  // loads are out (the rotation's wait then retires only loads issued before them), into
+  // rope_lds (q rows [G, D], then the k row [D]); qa reads q back in the MFMA layout, the last
+  // unit reads k.  rpatch[slot]: the rwin entry of the unit in that ring slot (>= 0: write the new
+  // row there and put it into the loaded copy).  The segment start reads the position from the
+  // window (unit j + 1 is in it when j ends, with one unit ahead).
+  constexpr int QP = G * D / 2 >= 64 ? G * D / 128 : 1;
+  constexpr int KP = D / 2 >= 64 ? D / 128 : 1;
+  constexpr int kRopePending = 1, kRopeHaveK = 2;
+  static_assert(!ROPE || kSkPrefetch == 1, "the window holds the next segment's first unit with one unit ahead");
+  __shared__ __attribute__((aligned(16))) uint16_t rope_lds[ROPE ? G * D + D : 1];
+  uint16_t* const rq_lds = rope_lds;
+  uint16_t* const rk_lds = rope_lds + G * D;
+  const int rq_p0 = lane * QP;  // this lane's first q pair over the G heads' G D/2
+  const int rk_p0 = lane * KP;  // and k pair over D/2
+  RopeRun<T, QP> rq;
+  RopeRun<T, KP> rk;
+  uint4 vnew = make_uint4(0, 0, 0, 0);
+  int rope_flags = 0;
+  int rpatch[NBUF];
   // Segment start at global unit ubeg + c.b.  The worker holding a segment's first block
   // (b == 0) is the first of the segment's workers: it records them for the merge kernel.
   auto begin_segment = [&](const Cursor& c, int64_t ubeg) __attribute__((always_inline)) {
-    tile.load_q(q_ptr + ((int64_t)c.s * H + (int64_t)c.kvh * G) * D);
+    if constexpr (ROPE) {
+      using S = typename Tile::S;
+      const int pos = __builtin_amdgcn_readlane(pwin, (int)(ubeg - u0 - wbase));
+      const float* cs = a.cos_sin + (int64_t)pos * D;
+      const S* qg = q_ptr + ((int64_t)c.s * H + (int64_t)c.kvh * G) * D;
+      if (rq_p0 < G * D / 2) rq.load(qg + (rq_p0 / (D / 2)) * D, cs, rq_p0 % (D / 2), D / 2);
+      rope_flags = kRopePending;
+      // The segment's last unit (global index ubeg + nblk - 1 - b) is this worker's.
+      if (ubeg + (c.nblk - 1 - c.b) < u1) {
+        rope_flags |= kRopeHaveK;
+        const int64_t row = ((int64_t)c.s * hkv + c.kvh) * D;
+        if (rk_p0 < D / 2) rk.load(static_cast<const S*>(a.k_new) + row, cs, rk_p0, D / 2);
+        vnew = *reinterpret_cast<const uint4*>(static_cast<const S*>(a.v_new) + row + tile.vd0);
+      }
+    } else {
+      tile.load_q(q_ptr + ((int64_t)c.s * H + (int64_t)c.kvh * G) * D);
+    }
     tile.reset();
     if (c.b == 0 && lane == 0) {
       // The worker of the segment's last unit (the last k with k C / W <= its cost).
@@ -1105,7 +1305,7 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   // Prologue: the first kSkPrefetch units (the last one repeated past the end of the range).
 #pragma unroll
   for (int q = 0; q < kSkPrefetch; ++q) {
-    load_unit(ld, ldi, kbuf[q], vbuf[q], tile);
+    load_unit(ld, ldi, kbuf[q], vbuf[q], tile, rpatch[q]);
     if (q + 1 < n) {
       advance(ld);
       ++ldi;
@@ -1119,12 +1319,43 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   // load in flight at the loop head); the last n % NBUF units run after it.
   auto unit = [&](int64_t j, auto qc) __attribute__((always_inline)) {
     constexpr int q = decltype(qc)::value;
-    load_unit(ld, ldi, kbuf[(q + kSkPrefetch) % NBUF], vbuf[(q + kSkPrefetch) % NBUF], tile);
+    load_unit(ld, ldi, kbuf[(q + kSkPrefetch) % NBUF], vbuf[(q + kSkPrefetch) % NBUF], tile,
+              rpatch[(q + kSkPrefetch) % NBUF]);
     if (loaded < n) {
       ++loaded;
       if (loaded < n) {
         advance(ld);
         ++ldi;
+      }
+    }
+    if constexpr (ROPE) {
+      if (rope_flags & kRopePending) {
+        if (rq_p0 < G * D / 2) rq.rotate_to(rq_lds + (rq_p0 / (D / 2)) * D, rq_p0 % (D / 2), D / 2);
+        if ((rope_flags & kRopeHaveK) && rk_p0 < D / 2) rk.rotate_to(rk_lds, rk_p0, D / 2);
+        // One wave per workgroup: its LDS reads follow its writes in order.
+        const uint4* qrow = reinterpret_cast<const uint4*>(rq_lds + (tile.col % G) * D + 8 * tile.seg);
+#pragma unroll
+        for (int i = 0; i < NK; ++i) tile.qa[i] = qrow[4 * i];
+        rope_flags = 0;
+      }
+      const int slot = rpatch[q];
+      if (slot >= 0) {
+        using S = typename Tile::S;
+        uint4 knew[NK];
+        const uint4* krow = reinterpret_cast<const uint4*>(rk_lds + 8 * tile.seg);
+#pragma unroll
+        for (int i = 0; i < NK; ++i) knew[i] = krow[4 * i];
+        tile.template patch<BPU>(kbuf[q], vbuf[q], ((ctx_cur - 1) >> 4) - cur.b * BPU, slot & (kBS - 1), knew, vnew);
+        const int bsz = kBS << a.bs_shift;
+        const int64_t row = (int64_t)(slot >> (4 + a.bs_shift)) * a.kv_stride +
+                            ((int64_t)cur.kvh * bsz + (slot & (bsz - 1))) * D;
+        S* kdst = const_cast<S*>(kc) + row;
+        S* vdst = const_cast<S*>(vc) + row;
+        if (tile.col == 0) {
+#pragma unroll
+          for (int i = 0; i < NK; ++i) *reinterpret_cast<uint4*>(kdst + 32 * i + 8 * tile.seg) = knew[i];
+        }
+        if (tile.vrow == 0) *reinterpret_cast<uint4*>(vdst + tile.vd0) = vnew;
       }
     }
     tile.template step<BPU>(kbuf[q], vbuf[q], cur.b * BPU * kBS, ctx_cur, a.scale_log2, p_lds[j & 1],
@@ -1560,12 +1791,13 @@ size_t stream_bytes(const Shape& sh, int32_t workers, StreamScratch* carve, void
   return acc + ml + desc;
 }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, bool ROPE = false>
 void launch_stream(const StreamArgs& sa, const DecodeArgs& a, hipStream_t s) {
   using S = typename DecodeTileFor<T, D, G>::S;
-  hipLaunchKernelGGL((decode_stream_kernel<T, D, G>), dim3(sa.num_workers), dim3(64), 0, s, sa,
+  hipLaunchKernelGGL((decode_stream_kernel<T, D, G, ROPE>), dim3(sa.num_workers), dim3(64), 0, s, sa,
                      static_cast<const S*>(a.q), static_cast<const S*>(a.k_cache),
-                     static_cast<const S*>(a.v_cache), a.block_table, a.context_lens);
+                     static_cast<const S*>(a.v_cache), a.block_table, a.context_lens, sa.positions,
+                     sa.slot_mapping);
   hipLaunchKernelGGL((decode_stream_merge_kernel<T, D, G>), dim3(sa.num_kv_heads, sa.batch), dim3(64 * G), 0, s,
                      sa, a.context_lens);
 }
@@ -1590,14 +1822,43 @@ void launch_stream_g(const StreamArgs& sa, const DecodeArgs& a, int G, hipStream
   }
 }
 
+// The step's new tokens for the fused RoPE form: rows [batch, H_kv, D] of k and v, token s
+// being sequence s's.
+struct RopeIn {
+  const void* k;
+  const void* v;
+  const float* cos_sin;
+  const int32_t* positions;
+  const int32_t* slot_mapping;
+};
+
+// The fused RoPE form runs at bf16 / f16, head_dim 64 and 128 and G 1, 2, 4 and 8.
+bool rope_stream_applies(const DecodeArgs& a, int32_t dtype, const RopeIn& r) {
+  const int G = a.num_heads / a.num_kv_heads;
+  return (dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && stream_applies(a, dtype) &&
+         (a.head_dim == 64 || a.head_dim == 128) && (G == 1 || G == 2 || G == 4 || G == 8) &&
+         aligned16(r.k) && aligned16(r.v) && aligned16(r.cos_sin);
+}
+
+template <typename T, int D>
+void launch_stream_rope_g(const StreamArgs& sa, const DecodeArgs& a, int G, hipStream_t s) {
+  switch (G) {
+    case 1: launch_stream<T, D, 1, true>(sa, a, s); break;
+    case 2: launch_stream<T, D, 2, true>(sa, a, s); break;
+    case 4: launch_stream<T, D, 4, true>(sa, a, s); break;
+    default: launch_stream<T, D, 8, true>(sa, a, s); break;  // G = 8 (rope_stream_applies)
+  }
+}
+
 // Runs the stream-K decode if it applies and the workspace holds its scratch; returns
-// RG_ERR_WORKSPACE (without recording an error) when the workspace is too small.
+// RG_ERR_WORKSPACE (without recording an error) when the workspace is too small.  With rope,
+// the fused RoPE form (rope_stream_applies holds).
 int run_stream(const char* op, const DecodeArgs& a, int32_t dtype, const Shape& sh, void* ws, size_t ws_bytes,
-               hipStream_t s) {
+               hipStream_t s, const RopeIn* rope = nullptr) {
   const int32_t workers = stream_workers(sh);
   StreamScratch sc;
   if (ws_bytes < stream_bytes(sh, workers, &sc, ws)) return RG_ERR_WORKSPACE;
-  StreamArgs sa;
+  StreamArgs sa{};
   sa.out = a.out;
   sa.part_acc = sc.acc;
   sa.part_ml = sc.ml;
@@ -1612,6 +1873,21 @@ int run_stream(const char* op, const DecodeArgs& a, int32_t dtype, const Shape& 
   sa.table_stride = sh.MB;
   sa.bs_shift = a.bs_shift;
   const int G = sh.H / sh.Hkv;
+  if (rope != nullptr) {
+    sa.k_new = rope->k;
+    sa.v_new = rope->v;
+    sa.cos_sin = rope->cos_sin;
+    sa.positions = rope->positions;
+    sa.slot_mapping = rope->slot_mapping;
+    if (dtype == RG_DTYPE_BF16) {
+      if (sh.D == 128) launch_stream_rope_g<bf16_t, 128>(sa, a, G, s);
+      else launch_stream_rope_g<bf16_t, 64>(sa, a, G, s);
+    } else {
+      if (sh.D == 128) launch_stream_rope_g<f16_t, 128>(sa, a, G, s);
+      else launch_stream_rope_g<f16_t, 64>(sa, a, G, s);
+    }
+    return check_launch(op);
+  }
   if (dtype == RG_DTYPE_BF16) {
     if (sh.D == 256) launch_stream_g<bf16_t, 256>(sa, a, G, s);
     else if (sh.D == 128) launch_stream_g<bf16_t, 128>(sa, a, G, s);
@@ -1762,6 +2038,37 @@ extern "C" int rg_paged_attention_v1(const void* query, const void* key_cache,
   const Shape sh{num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, batch_size};
   return paged_v1("paged_attention_v1", query, key_cache, value_cache, block_table, context_lens,
                   output, scale, sh, dtype, kv_block_stride, workspace, workspace_bytes, stream);
+}
+
+extern "C" int rg_rope_reshape_and_cache_paged_attention_v1(
+    const void* query, const void* key, const void* value, void* key_cache, void* value_cache,
+    const float* cos_sin, const int32_t* positions, const int32_t* slot_mapping, const int32_t* block_table,
+    const int32_t* context_lens, void* output, float scale, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq, int32_t batch_size, int32_t dtype,
+    int64_t kv_block_stride, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* op = "rope_reshape_and_cache_paged_attention_v1";
+  const Shape sh{num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, batch_size};
+  int st = check_decode_shape(op, sh, dtype, kv_block_stride);
+  if (st != RG_OK) return st;
+  if (sh.B == 0) return ok();
+  if (!query || !key || !value || !key_cache || !value_cache || !cos_sin || !positions || !slot_mapping ||
+      !block_table || !context_lens || !output) {
+    return fail(RG_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
+  }
+  if (workspace == nullptr) return fail(RG_ERR_INVALID_ARGUMENT, "%s: needs a workspace", op);
+  const DecodeArgs a = make_args(query, key_cache, value_cache, block_table, context_lens, output, scale, sh,
+                                 kv_block_stride, kBS, 1, MODE_AUTO);
+  const RopeIn rope{key, value, cos_sin, positions, slot_mapping};
+  if (sh.MB <= 0 || !rope_stream_applies(a, dtype, rope)) {
+    return fail(RG_ERR_NOT_SUPPORTED,
+                "%s: runs at bf16 / f16, head_dim 64 or 128, num_heads / num_kv_heads 1, 2, 4 or 8, "
+                "block_size 16 * 2^j and 16-byte aligned rows (rg_rope_reshape_and_cache followed by "
+                "rg_paged_attention_v1 covers the rest)", op);
+  }
+  st = run_stream(op, a, dtype, sh, workspace, workspace_bytes, as_stream(stream), &rope);
+  if (st != RG_ERR_WORKSPACE) return st;
+  return fail(RG_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu required", op, workspace_bytes,
+              stream_bytes(sh, stream_workers(sh), nullptr, nullptr));
 }
 
 extern "C" int rg_paged_attention_v1_plus(const void* query, const void* key_cache,

@@ -200,16 +200,6 @@ __device__ __forceinline__ uint2 add_rounded(uint2 c, gf32x4_t v) {
   return make_uint2(pack2<T>(c0 + rnd(v[0]), c1 + rnd(v[1])), pack2<T>(c2 + rnd(v[2]), c3 + rnd(v[3])));
 }
 
-// out = (lo c - hi s, hi c + lo s), unfused (the rotation of rope_cache_kernel).
-__device__ __forceinline__ void rope_rotate(float lo, float hi, float c, float s, float& out_lo, float& out_hi) {
-#pragma clang fp contract(off)
-  const float a = lo * c;
-  const float b = hi * s;
-  const float e = hi * c;
-  const float f = lo * s;
-  out_lo = a - b;
-  out_hi = e + f;
-}
 template <typename T, int NB, int MB, int EPI, bool NORM = false>
 __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
   static_assert(EPI == kEpiPlain || EPI == kEpiResidual || NB % 2 == 0,
@@ -417,7 +407,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(GemmArgs a) {
         const float4 s4 = *reinterpret_cast<const float4*>(cs + HD + d);
         const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) rope_rotate(round_to(vl[e]), round_to(vh[e]), c[e], sn[e], ol[e], oh[e]);
+        for (int e = 0; e < 4; ++e) rope_rotate_pair(round_to(vl[e]), round_to(vh[e]), c[e], sn[e], ol[e], oh[e]);
       }
       uint16_t* dst;
       if (is_q) {

@@ -51,6 +51,20 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, h);
 }
 
+// RoPE (rotate-half) of one pair (lo, hi) = (x[i], x[i + D/2]) with the rounding of the
+// reference expression (rope.cu:34-41) made explicit: each product and the difference / sum
+// rounded separately (no fused multiply-add), so every kernel that rotates gets the same bits.
+__device__ __forceinline__ void rope_rotate_pair(float lo, float hi, float c, float s, float& out_lo,
+                                                 float& out_hi) {
+#pragma clang fp contract(off)
+  const float a = lo * c;
+  const float b = hi * s;
+  const float e = hi * c;
+  const float f = lo * s;
+  out_lo = a - b;
+  out_hi = e + f;
+}
+
 template <typename T> struct elem;
 template <> struct elem<f32_t> {
   using storage = float;

@@ -164,6 +164,28 @@ class PagedAttentionKernels:
             block_size, max_blocks_per_seq, batch_size, dtype_code(query), key_cache.stride(0),
             _ptr(workspace), ws_bytes, _stream(query)))
 
+    def launch_rope_reshape_and_cache_v1(self, query, key, value, key_cache, value_cache, cos_sin, positions,
+                                         slot_mapping, block_table, context_lens, output, scale: float,
+                                         num_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
+                                         max_blocks_per_seq: int, batch_size: int,
+                                         workspace: torch.Tensor) -> None:
+        """launch_rope_reshape_and_cache of one new token per sequence (key / value [batch, H_kv, D])
+        followed by launch_v1, in the stream-K decode's launches
+        (rg_rope_reshape_and_cache_paged_attention_v1): the same output and caches bit for bit,
+        with query read and left unrotated."""
+        _require_cuda(query, key, value, key_cache, value_cache, cos_sin, positions, slot_mapping, block_table,
+                      context_lens, output, workspace)
+        _require_i32(positions, slot_mapping, block_table, context_lens)
+        for t in (query, key, value):
+            if not t.is_contiguous():
+                raise RailgunError(_lib.RG_ERR_INVALID_ARGUMENT, "query, key and value must be contiguous")
+        check(self.lib.rg_rope_reshape_and_cache_paged_attention_v1(
+            query.data_ptr(), key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+            cos_sin.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(), block_table.data_ptr(),
+            context_lens.data_ptr(), output.data_ptr(), float(scale), num_heads, num_kv_heads, head_dim,
+            block_size, max_blocks_per_seq, batch_size, dtype_code(query), key_cache.stride(0),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(query)))
+
     def launch_v1_no_alloc(self, query, key_cache, value_cache, block_table, context_lens, output, scale: float,
                            num_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
                            max_blocks_per_seq: int, batch_size: int) -> None:
