@@ -924,6 +924,14 @@ struct StreamArgs {
 #ifndef RG_SK_SEG_COST_KB
 #define RG_SK_SEG_COST_KB 20
 #endif
+// The same with the step's RoPE + cache pass fused in (its segment starts also rotate q).  Kept
+// at RG_SK_SEG_COST_KB, so that the fused step splits the work as the decode alone does and its
+// output equals the two-entry chain's bit for bit; swept in paired runs of the fused entry at
+// config 2 against 20: 14 KB 1.004, 26 KB 0.996, 32 KB 0.999 (26 KB moves the split, and three
+// of config 2's 98,304 outputs then differ from the chain's by 2 ulp).
+#ifndef RG_SK_SEG_COST_KB_ROPE
+#define RG_SK_SEG_COST_KB_ROPE RG_SK_SEG_COST_KB
+#endif
 
 // 16-token sub-blocks of sequence s: ceil(ctx/16) per kv-head (context clamped to the table
 // row, max_blocks of them).
@@ -991,7 +999,7 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   // Consecutive z are at most KQ + KS apart, so with W <= C / (KQ + KS) every worker owns a unit
   // (with fewer units than workers, only the first workers run), as the merge's segment ranges
   // need.
-  constexpr int64_t KS = RG_SK_SEG_COST_KB;
+  constexpr int64_t KS = ROPE ? RG_SK_SEG_COST_KB_ROPE : RG_SK_SEG_COST_KB;
   constexpr int64_t KQ = KS > 0 ? (int64_t)BPU * kBS * D * sizeof(typename Tile::S) * 2 / 1024 : 1;
   static_assert(KQ >= 1, "unit cost");
   int64_t C, W, u0, u1, seq_start;
