@@ -256,6 +256,22 @@ class PagedAttentionKernels {
                                     kv_block_stride, stream_),
           "launch_rope_reshape_and_cache");
   }
+  // launch_rope_reshape_and_cache of one new token per sequence followed by launch_v1, in the
+  // stream-K decode's launches (query is read, not rotated in place).
+  void launch_rope_reshape_and_cache_v1(const void* query, const void* k, const void* v, void* k_cache,
+                                        void* v_cache, const float* cos_sin, const int32_t* positions,
+                                        const int32_t* slot_mapping, const int32_t* block_table,
+                                        const int32_t* context_lens, void* output, float scale, int32_t num_heads,
+                                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                        int32_t max_blocks_per_seq, int32_t batch_size, void* workspace,
+                                        size_t workspace_bytes, DType dtype = DType::BF16,
+                                        int64_t kv_block_stride = 0) const {
+    check(rg_rope_reshape_and_cache_paged_attention_v1(
+              query, k, v, k_cache, v_cache, cos_sin, positions, slot_mapping, block_table, context_lens, output,
+              scale, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, batch_size, (int32_t)dtype,
+              kv_block_stride, workspace, workspace_bytes, stream_),
+          "launch_rope_reshape_and_cache_v1");
+  }
   void launch_prefill_packed(const void* query, const void* key_cache, const void* value_cache,
                              const int32_t* block_table, const int32_t* context_lens, const int32_t* cu_seqlens,
                              void* output, float scale, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
