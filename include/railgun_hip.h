@@ -330,7 +330,7 @@ int rg_paged_attention_v1(const void* query, const void* key_cache,
  * context_lens[s] - 1 in sequence s's block table, as in every decode step; any
  * other slot is left unwritten (where the chain would write it).  Needs a workspace of
  * rg_paged_attention_v1_workspace_bytes; bf16 / f16, head_dim 64 or 128,
- * num_heads / num_kv_heads 1, 2, 4 or 8 (RG_ERR_NOT_SUPPORTED otherwise).
+ * num_heads / num_kv_heads 1 to 8 (RG_ERR_NOT_SUPPORTED otherwise).
  * New entry: the reference runs RoPE, reshape_and_cache and launch_v1 as separate
  * calls (crates/vllm-cuda/src/kernels/mod.rs:196-225, 227-262, 305-348). */
 int rg_rope_reshape_and_cache_paged_attention_v1(

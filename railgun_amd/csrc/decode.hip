@@ -1233,7 +1233,9 @@ __global__ __launch_bounds__(64) RG_SK_OCCUPANCY void decode_stream_kernel(
   // unit reads k.  rpatch[slot]: the rwin entry of the unit in that ring slot (>= 0: write the new
   // row there and put it into the loaded copy).  The segment start reads the position from the
   // window (unit j + 1 is in it when j ends, with one unit ahead).
-  constexpr int QP = G * D / 2 >= 64 ? G * D / 128 : 1;
+  // Pairs per lane: G D / 128 rounded up to a power of two (runs then never cross a head's D/2
+  // pairs), the lanes past the G D / 2 pairs idle.
+  constexpr int QP = G * D <= 128 ? 1 : G * D <= 256 ? 2 : G * D <= 512 ? 4 : 8;
   constexpr int KP = D / 2 >= 64 ? D / 128 : 1;
   constexpr int kRopePending = 1, kRopeHaveK = 2;
   static_assert(!ROPE || kSkPrefetch == 1, "the window holds the next segment's first unit with one unit ahead");
@@ -1840,12 +1842,12 @@ struct RopeIn {
   const int32_t* slot_mapping;
 };
 
-// The fused RoPE form runs at bf16 / f16, head_dim 64 and 128 and G 1, 2, 4 and 8.
+// The fused RoPE form runs at bf16 / f16, head_dim 64 and 128 and G 1 to 8.
 bool rope_stream_applies(const DecodeArgs& a, int32_t dtype, const RopeIn& r) {
   const int G = a.num_heads / a.num_kv_heads;
   return (dtype == RG_DTYPE_BF16 || dtype == RG_DTYPE_F16) && stream_applies(a, dtype) &&
-         (a.head_dim == 64 || a.head_dim == 128) && (G == 1 || G == 2 || G == 4 || G == 8) &&
-         aligned16(r.k) && aligned16(r.v) && aligned16(r.cos_sin);
+         (a.head_dim == 64 || a.head_dim == 128) && G >= 1 && G <= 8 && aligned16(r.k) && aligned16(r.v) &&
+         aligned16(r.cos_sin);
 }
 
 template <typename T, int D>
@@ -1853,7 +1855,11 @@ void launch_stream_rope_g(const StreamArgs& sa, const DecodeArgs& a, int G, hipS
   switch (G) {
     case 1: launch_stream<T, D, 1, true>(sa, a, s); break;
     case 2: launch_stream<T, D, 2, true>(sa, a, s); break;
+    case 3: launch_stream<T, D, 3, true>(sa, a, s); break;
     case 4: launch_stream<T, D, 4, true>(sa, a, s); break;
+    case 5: launch_stream<T, D, 5, true>(sa, a, s); break;
+    case 6: launch_stream<T, D, 6, true>(sa, a, s); break;
+    case 7: launch_stream<T, D, 7, true>(sa, a, s); break;
     default: launch_stream<T, D, 8, true>(sa, a, s); break;  // G = 8 (rope_stream_applies)
   }
 }
@@ -2069,7 +2075,7 @@ extern "C" int rg_rope_reshape_and_cache_paged_attention_v1(
   const RopeIn rope{key, value, cos_sin, positions, slot_mapping};
   if (sh.MB <= 0 || !rope_stream_applies(a, dtype, rope)) {
     return fail(RG_ERR_NOT_SUPPORTED,
-                "%s: runs at bf16 / f16, head_dim 64 or 128, num_heads / num_kv_heads 1, 2, 4 or 8, "
+                "%s: runs at bf16 / f16, head_dim 64 or 128, num_heads / num_kv_heads 1 to 8, "
                 "block_size 16 * 2^j and 16-byte aligned rows (rg_rope_reshape_and_cache followed by "
                 "rg_paged_attention_v1 covers the rest)", op);
   }

@@ -122,6 +122,10 @@ CASES = {
     "f16_d128_g4": ((16, 1, 600), dict(dt="f16", seed=8)),
     "more_units_than_workers": ([5000, 7000, 4321], dict(seed=9)),
     "one_token_sequences": ([1] * 40, dict(seed=10)),
+    "llama32_3b_g3_d128": ((20, 1, 900), dict(H=24, Hkv=8, seed=13)),
+    "qwen2_7b_g7_d128": ((12, 1, 700), dict(H=28, Hkv=4, seed=14)),
+    "g5_d64": ((16, 1, 500), dict(H=40, Hkv=8, D=64, seed=15)),
+    "g6_d64_block32": ((14, 1, 400), dict(H=24, Hkv=4, D=64, bs=32, seed=16)),
 }
 
 
@@ -172,9 +176,9 @@ def test_fused_step_small_against_oracle(device, kernels):
     assert_close(dev_f32(out), want, "bf16", "small fused step vs the oracle")
 
 
-@pytest.mark.parametrize("kw", [dict(dt="f32"), dict(H=24, Hkv=8), dict(D=256)])
+@pytest.mark.parametrize("kw", [dict(dt="f32"), dict(H=32, Hkv=2), dict(D=256)])
 def test_fused_step_rejects_other_shapes(device, kernels, kw):
-    """fp32, GQA ratios outside 1/2/4/8 and head_dim 256 are refused with RG_ERR_NOT_SUPPORTED
+    """fp32, GQA ratios above 8 and head_dim 256 are refused with RG_ERR_NOT_SUPPORTED
     (the chain of two entries covers them); nothing is launched."""
     st = make_step(device, [40, 70], **kw)
     with pytest.raises(RailgunError, match="not supported|runs at"):
